@@ -1,0 +1,208 @@
+"""ctypes binding of the CPU oracle (oracle/tmq_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product (tensomite.cr_amd/).
+
+Functions mirror the reference's `Quant` module (src/tensomite/quant.cr) and
+`F16` (src/tensomite/f16.cr); numpy arrays in and out.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+Q8_0, Q4_0, Q4_1 = 0, 1, 2
+KINDS = {"Q8_0": Q8_0, "Q4_0": Q4_0, "Q4_1": Q4_1}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
+
+
+def build() -> None:
+    """Compiles the three oracle builds (portable, x86-64-v3, x86-64-v4)."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
+
+
+def _cpu_flags() -> set:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def best_variant() -> str:
+    """The widest oracle build the host CPU can run: v4 (AVX-512), v3 (AVX2) or portable."""
+    flags = _cpu_flags()
+    if {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd"} <= flags:
+        return "v4"
+    if {"avx2", "fma", "bmi2", "f16c", "movbe"} <= flags:
+        return "v3"
+    return "portable"
+
+
+_LIBS: dict = {}
+
+
+def lib(variant: str = "portable") -> ctypes.CDLL:
+    if variant in _LIBS:
+        return _LIBS[variant]
+    name = {"portable": "libtmq_oracle.so", "v3": "libtmq_oracle_v3.so", "v4": "libtmq_oracle_v4.so"}[variant]
+    path = os.path.join(HERE, name)
+    if not os.path.exists(path):
+        build()
+    so = ctypes.CDLL(path)
+    P = ctypes.c_void_p
+    so.tmo_f16_bits.restype = ctypes.c_uint16
+    so.tmo_f16_bits.argtypes = [ctypes.c_float]
+    so.tmo_f16_value.restype = ctypes.c_float
+    so.tmo_f16_value.argtypes = [ctypes.c_uint16]
+    so.tmo_quantize.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
+    so.tmo_dequantize.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
+    so.tmo_quantize_activations.argtypes = [P, ctypes.c_int32, P, P, P, ctypes.c_int]
+    so.tmo_quantize_activations.restype = None
+    so.tmo_matmul_reference.argtypes = [ctypes.c_int, P, P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P]
+    so.tmo_matmul.argtypes = [ctypes.c_int, P, P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P]
+    so.tmo_gather.restype = ctypes.c_int64
+    so.tmo_gather.argtypes = [ctypes.c_int, P, ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int64, P]
+    so.tmo_add_bias.argtypes = [P, P, ctypes.c_int64, ctypes.c_int32]
+    so.tmo_add_bias.restype = None
+    so.tmo_set_threads.argtypes = [ctypes.c_int]
+    so.tmo_set_threads.restype = None
+    so.tmo_threads.restype = ctypes.c_int
+    so.tmo_f16_bits_many.argtypes = [P, ctypes.c_int64, P]
+    so.tmo_f16_bits_many.restype = ctypes.c_int64
+    so.tmo_f16_values_many.argtypes = [P, ctypes.c_int64, P]
+    so.tmo_f16_values_many.restype = ctypes.c_int64
+    _LIBS[variant] = so
+    return so
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def kind_of(kind) -> int:
+    return KINDS[kind] if isinstance(kind, str) else int(kind)
+
+
+def row_bytes(kind, k: int) -> int:
+    return k // 32 * BLOCK_BYTES[kind_of(kind)]
+
+
+def f16_bits(value: float) -> int:
+    """F16.new(value).bits, f16.cr:29-41."""
+    return lib().tmo_f16_bits(float(value))
+
+
+def f16_value(bits: int) -> float:
+    """F16.from_bits(bits).to_f32, f16.cr:44-57."""
+    return lib().tmo_f16_value(int(bits))
+
+
+def f16_bits_many(values: np.ndarray) -> np.ndarray:
+    words = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32)
+    out = np.empty(words.shape, dtype=np.uint16)
+    lib().tmo_f16_bits_many(_ptr(words), words.size, _ptr(out))
+    return out
+
+
+def f16_values_many(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().tmo_f16_values_many(_ptr(b), b.size, _ptr(out))
+    return out
+
+
+def quantize(kind, values: np.ndarray) -> np.ndarray:
+    """Quant.quantize, quant.cr:77-90: f32 values (a whole number of blocks) -> block bytes."""
+    k = kind_of(kind)
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.empty(v.size // 32 * BLOCK_BYTES[k], dtype=np.uint8)
+    if lib().tmo_quantize(k, _ptr(v), v.size, _ptr(out)) != 0:
+        raise ValueError("bad kind or count")
+    return out
+
+
+def dequantize(kind, data: np.ndarray, count: int) -> np.ndarray:
+    """Quant.dequantize, quant.cr:93-105."""
+    k = kind_of(kind)
+    b = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+    if b.size != count // 32 * BLOCK_BYTES[k]:
+        raise ValueError(f"{b.size} bytes do not hold {count} values")
+    out = np.empty(count, dtype=np.float32)
+    lib().tmo_dequantize(k, _ptr(b), count, _ptr(out))
+    return out
+
+
+def quantize_activations(x: np.ndarray, with_sums: bool):
+    """quantize_activations, quant.cr:424-442, one row: (scales, sums, qs)."""
+    v = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    nb = v.size // 32
+    scales = np.zeros(nb, np.float32)
+    sums = np.zeros(nb, np.float32)
+    qs = np.zeros(v.size, np.int8)
+    lib().tmo_quantize_activations(_ptr(v), v.size, _ptr(scales), _ptr(sums), _ptr(qs), int(with_sums))
+    return scales, sums, qs
+
+
+def matmul_reference(kind, x: np.ndarray, w: np.ndarray, rows: int, n: int, k: int) -> np.ndarray:
+    """Quant.matmul_reference, quant.cr:122-142: the oracle, [rows, n] f32."""
+    kk = kind_of(kind)
+    xs = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    ws = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    if ws.size != n * row_bytes(kk, k) or xs.size != rows * k:
+        raise ValueError("shape mismatch")
+    out = np.empty(rows * n, dtype=np.float32)
+    if lib().tmo_matmul_reference(kk, _ptr(xs), _ptr(ws), rows, n, k, _ptr(out)) != 0:
+        raise ValueError("bad kind or k")
+    return out.reshape(rows, n)
+
+
+def matmul(kind, x: np.ndarray, w: np.ndarray, rows: int, n: int, k: int, variant: str = "portable") -> np.ndarray:
+    """Quant.matmul, quant.cr:155-182: the fast CPU path on set_threads() threads."""
+    kk = kind_of(kind)
+    xs = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    ws = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    if ws.size != n * row_bytes(kk, k) or xs.size != rows * k:
+        raise ValueError("shape mismatch")
+    out = np.empty(rows * n, dtype=np.float32)
+    if lib(variant).tmo_matmul(kk, _ptr(xs), _ptr(ws), rows, n, k, _ptr(out)) != 0:
+        raise ValueError("bad kind or k")
+    return out.reshape(rows, n)
+
+
+def add_bias(dst: np.ndarray, bias: np.ndarray) -> np.ndarray:
+    """HostDevice#add_bias, devices/host.cr:725-734."""
+    out = np.ascontiguousarray(dst, dtype=np.float32).copy()
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    lib().tmo_add_bias(_ptr(out), _ptr(b), out.size // b.size, b.size)
+    return out
+
+
+def gather(kind, table: np.ndarray, rows: int, width: int, ids) -> np.ndarray:
+    """Quant.gather with HostDevice#block_gather's id check (quant.cr:417-422; host.cr:648-658)."""
+    kk = kind_of(kind)
+    t = np.ascontiguousarray(table, dtype=np.uint8).reshape(-1)
+    idx = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    out = np.empty(idx.size * width, dtype=np.float32)
+    bad = lib().tmo_gather(kk, _ptr(t), rows, width, _ptr(idx), idx.size, _ptr(out))
+    if bad:
+        raise IndexError(f"index {idx[bad - 1]} out of range for {rows} rows")
+    return out.reshape(idx.size, width)
+
+
+def set_threads(threads: int, variant: str = "portable") -> None:
+    """Quant.threads=, quant.cr:188."""
+    lib(variant).tmo_set_threads(int(threads))
+
+
+def threads(variant: str = "portable") -> int:
+    return lib(variant).tmo_threads()
