@@ -1,0 +1,244 @@
+/*
+ * tensomite_hip.h -- the C ABI of libtensomite_hip.so, an MI355X (gfx950)
+ * backend for tensomite's quantised products (Op::BlockMatMul) and block
+ * gathers (Op::Gather on a block table).
+ *
+ * It replaces, for this device, the native seam the reference's CUDA device
+ * binds through `lib LibCUDA` / `lib LibNVRTC` (src/tensomite/cuda/lib.cr:48-110)
+ * and the host-side pieces of `CUDA < HostDevice` that manage device memory
+ * (src/tensomite/cuda.cr). Conventions follow that seam so a Crystal `lib`
+ * binding is a line per function:
+ *
+ *   - every entry point returns an int: 0 on success, a HIP runtime error
+ *     code (1..999, hipError_t's numbering) or a library code (TMH_ERROR_*);
+ *     tmh_error_name/tmh_error_string describe it (cuda/lib.cr:51-52,
+ *     cuda.cr:1069-1075);
+ *   - device memory is a uint64_t address (LibCUDA::DevicePtr, cuda/lib.cr:49);
+ *   - no run-time compilation: the kernels are built offline for gfx950.
+ *
+ * Threads: any thread may call. Each thread addresses the device it last
+ * passed to tmh_set_device (device 0 if none), as the reference's
+ * Context#bind makes its context current per thread (cuda.cr:1118-1125).
+ * All work for a device -- kernels and copies -- is queued on ONE ordered
+ * stream, so it runs in submission order (the reference's single default
+ * stream, cuda.cr:1176-1196).
+ */
+#ifndef TENSOMITE_HIP_H
+#define TENSOMITE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ result codes */
+
+#define TMH_SUCCESS 0
+/* 1..999: hipError_t values, passed through. */
+#define TMH_ERROR_INVALID_VALUE 1000 /* an argument out of range (null pointer, size) */
+#define TMH_ERROR_SHAPE 1001         /* shapes disagree: ShapeError (errors.cr) */
+#define TMH_ERROR_DTYPE 1002         /* not a block kind: DTypeError (errors.cr) */
+#define TMH_ERROR_NO_KERNELS 1003    /* kernels unavailable: the caller runs its host kernel
+                                        (cuda.cr:1164-1172, CUDA_ERROR_NOT_SUPPORTED) */
+#define TMH_ERROR_OUT_OF_MEMORY 1004 /* device allocation failed */
+#define TMH_ERROR_EXECUTION 1005     /* a kernel found an index out of range: ExecutionError,
+                                        reported at tmh_sync (cuda.cr:967-983) */
+#define TMH_ERROR_NO_DEVICE 1006     /* no GPU, or a device index out of range */
+#define TMH_ERROR_BUSY 1007          /* the retired list is busy or full (buffer_pool.cr:101-111) */
+
+/* Block kinds, numbered as the reference's kernels number them (cuda.cr:774-781). */
+#define TMH_Q8_0 0 /* F16 d, 32 int8: x = q·d                      (34 bytes) */
+#define TMH_Q4_0 1 /* F16 d, 16 bytes of nibbles: x = (q - 8)·d     (18 bytes) */
+#define TMH_Q4_1 2 /* F16 d, F16 m, 16 bytes of nibbles: x = q·d + m (20 bytes) */
+
+/* How a product divides its work: BlockMatMulMode (quant.cr:5-28). AUTO,
+ * THREAD, LANES and MATRIX give the host's bits; UNORDERED is for
+ * measurement only and may differ in the last bits. LOADS, STREAM and
+ * STREAM_ACTIVATIONS are Metal measurement modes the reference runs as LANES
+ * elsewhere; so does this device. MATRIX has no counterpart in the
+ * reference: the int8 matrix-core path for many activation rows. */
+#define TMH_MODE_AUTO 0
+#define TMH_MODE_THREAD 1
+#define TMH_MODE_LANES 2
+#define TMH_MODE_UNORDERED 3
+#define TMH_MODE_LOADS 4
+#define TMH_MODE_STREAM 5
+#define TMH_MODE_STREAM_ACTIVATIONS 6
+#define TMH_MODE_MATRIX 7
+
+typedef struct tmh_device_info {
+    char name[256];          /* marketing name, as GPU#name (cuda.cr:316) */
+    char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    uint64_t memory;         /* global memory in bytes, as GPU#memory */
+    int32_t compute_units;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width;
+    int32_t l2_bytes;
+    int32_t lds_bytes_per_block;
+} tmh_device_info;
+
+/* Device counters, as CUDA#uploads/#downloads/#gpu_ops/#device_bytes and
+ * BufferPool#hits/#misses/#held/#limit (cuda.cr:214-230, buffer_pool.cr:14-35). */
+typedef struct tmh_counters {
+    int64_t uploads;
+    int64_t downloads;
+    int64_t gpu_ops;
+    int64_t device_bytes;
+    int64_t pool_held;
+    int64_t pool_limit;
+    int64_t pool_hits;
+    int64_t pool_misses;
+    int64_t frees;
+} tmh_counters;
+
+/* ------------------------------------------------------------ devices */
+
+/* Starts the runtime and counts the GPUs: CUDA.init + gpu_count
+ * (cuda.cr:985-1000; cuInit/cuDeviceGetCount, cuda/lib.cr:53-54). */
+int tmh_init(int32_t* count);
+
+/* Name, memory and shape of a GPU (GPU record, cuda.cr:310-320;
+ * cuDeviceGetName/cuDeviceTotalMem/cuDeviceGetAttribute, cuda/lib.cr:55-58). */
+int tmh_device_info_get(int32_t device, tmh_device_info* out);
+
+/* Makes `device` current on the calling thread (Context#bind, cuda.cr:1118-1125;
+ * cuCtxSetCurrent, cuda/lib.cr:61). */
+int tmh_set_device(int32_t device);
+int tmh_get_device(int32_t* device);
+
+/* ------------------------------------------------------------ memory */
+
+/* Raw device memory: Context#alloc/#free (cuda.cr:1128-1137; cuMemAlloc/cuMemFree,
+ * cuda/lib.cr:65-66). At least 4 bytes are allocated, as CUDA#alloc does. */
+int tmh_malloc(uint64_t* ptr, uint64_t bytes);
+int tmh_free(uint64_t ptr);
+
+/* Frees from any thread, never failing the caller: Context#free_from_any_thread
+ * (cuda.cr:1139-1143), for finalizers. Returns 0. */
+int tmh_free_any_thread(uint64_t ptr);
+
+/* Copies host memory into device memory and returns when the bytes are on
+ * the device: Context#upload (cuda.cr:1146-1149; cuMemcpyHtoD, cuda/lib.cr:67). */
+int tmh_upload(uint64_t dst, const void* src, uint64_t bytes);
+
+/* Queues a copy into device memory and returns once `src` has been copied
+ * into the library's pinned staging ring, so the caller may free or reuse it
+ * at once. Ordered with kernels and copies like every other call. No
+ * counterpart in the reference, whose uploads are synchronous (cuda.cr:360-370):
+ * it overlaps the host-side copy of one chunk with the DMA of the last. */
+int tmh_upload_async(uint64_t dst, const void* src, uint64_t bytes);
+
+/* Copies device memory to the host after all queued work has finished:
+ * Context#download (cuda.cr:1151-1154; cuMemcpyDtoH, cuda/lib.cr:68). */
+int tmh_download(void* dst, uint64_t src, uint64_t bytes);
+
+/* Device-to-device copy, queued in order (Tensor#take_rows/.cat_rows on a
+ * device, tensor/quantised.cr:32-55, without the host round trip). */
+int tmh_copy(uint64_t dst, uint64_t src, uint64_t bytes);
+
+/* Waits for all queued work: Context#synchronize (cuda.cr:1156-1158;
+ * cuCtxSynchronize, cuda/lib.cr:62). */
+int tmh_synchronize(void);
+
+/* ------------------------------------------------------- the buffer layer */
+
+/* Device memory of exactly `bytes`, from the pool when a buffer of that size
+ * is free, else newly allocated: CUDA#alloc (cuda.cr:339-353) over
+ * BufferPool#take (buffer_pool.cr:38-51). */
+int tmh_alloc(uint64_t* ptr, uint64_t bytes);
+
+/* Gives memory back, from any thread and never waiting: CUDA#retire
+ * (cuda.cr:439-444) over RetiredList#push (buffer_pool.cr:101-111). When the
+ * list is busy or full, the memory is freed at once instead. Returns 0. */
+int tmh_retire(uint64_t ptr, uint64_t bytes);
+
+/* Waits for the GPU, moves retired memory into the pool (freeing what it
+ * cannot hold), then reports a kernel's index error, if any, as
+ * TMH_ERROR_EXECUTION: CUDA#sync (cuda.cr:419-428), #recycle_retired
+ * (447-454), #check_errors (972-983). */
+int tmh_sync(void);
+
+/* The pool's limit in bytes (default max(1 GiB, a quarter of device memory),
+ * cuda.cr:319). */
+int tmh_pool_set_limit(int64_t bytes);
+
+int tmh_counters_get(tmh_counters* out);
+
+/* ------------------------------------------------------------ errors */
+
+/* hipGetErrorName/hipGetErrorString for HIP codes; the library's own names
+ * for TMH_ERROR_* (cuGetErrorName/cuGetErrorString, cuda/lib.cr:51-52). */
+const char* tmh_error_name(int code);
+const char* tmh_error_string(int code);
+
+/* The first index error a gather kernel reported since the last call:
+ * out[0] = reports, out[1] = the id, out[2] = the table's rows; clears it
+ * (the error buffer of cuda.cr:961-983). */
+int tmh_error_report(int32_t out[3]);
+
+/* Test hook: makes the next `count` device allocations fail with
+ * TMH_ERROR_OUT_OF_MEMORY (the stub driver's malloc failure,
+ * scripts/cuda_stub/libcuda.c:100-106). */
+int tmh_debug_fail_allocations(int32_t count);
+
+/* Test hook: with `off` non-zero, every kernel entry point returns
+ * TMH_ERROR_NO_KERNELS, as when the reference's module cannot load
+ * (cuda.cr:1164-1172). */
+int tmh_debug_disable_kernels(int32_t off);
+
+/* ------------------------------------------------------------ events */
+
+/* Timing on the library's stream: cuEventCreate/Record/ElapsedTime
+ * (cuda/lib.cr:80-86; CUDA::Profile per-kernel timing, cuda.cr:463-481). */
+int tmh_event_create(uint64_t* event);
+int tmh_event_record(uint64_t event);
+int tmh_event_elapsed_ms(uint64_t start, uint64_t stop, float* ms);
+int tmh_event_destroy(uint64_t event);
+
+/* ------------------------------------------------------------ kernels */
+
+/* Quantises `rows` rows of `k` activations (k a multiple of 32, rows `ldx`
+ * floats apart) to 8 bits per block of 32, as quantize_rows_q8_f32
+ * (cuda/kernels.cu:1190-1207) and the host's quantize_activations
+ * (quant.cr:424-442) do: per block d = amax/127, q = round-half-away(x/d),
+ * scales[b] = F16(d), sums[b] = F16(Σq·d), totals[b] = Σq; qs is [rows, k]
+ * int8, the others [rows, k/32]. */
+int tmh_quantize_rows_q8(uint64_t x, uint32_t rows, uint32_t k, uint32_t ldx, uint64_t scales, uint64_t sums,
+                         uint64_t totals, uint64_t qs);
+
+/* dst[rows, n] = x[rows, k] · wᵀ (+ bias[n]) for a block-format weight w of n
+ * rows of k values, the weight's first row `w_byte_offset` bytes into its
+ * buffer (a row slice, as `bytes_for(view.offset)`): Op::BlockMatMul as
+ * CUDA#launch_blocks queues it (cuda.cr:736-756) -- the activations
+ * quantised into library scratch, then the product, every output summing its
+ * blocks in order with the host's expressions, so the bits equal
+ * Quant.matmul_reference's (quant.cr:122-142) and do not depend on `rows`.
+ * Rows of x are `ldx` floats apart; dst is dense [rows, n]; bias may be 0.
+ * `mode` is a TMH_MODE_*. */
+int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
+                     uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode);
+
+/* The product of tmh_block_matmul from activations already quantised by
+ * tmh_quantize_rows_q8 (its four outputs), for callers that share one
+ * quantisation between products. */
+int tmh_block_matmul_quantised(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t scales, uint64_t sums,
+                               uint64_t totals, uint64_t qs, uint64_t dst, uint64_t bias, uint32_t rows, uint32_t n,
+                               uint32_t k, uint32_t mode);
+
+/* dst[count, width] = rows ids[0..count) of a block table of `table_rows`
+ * rows of `width` values, dequantised: gather_blocks_f32
+ * (cuda/kernels.cu:1172-1185) for Op::Gather on a block table. An id out of
+ * range writes zeros and is reported at the next tmh_sync as
+ * TMH_ERROR_EXECUTION (HostDevice#block_gather raises ExecutionError,
+ * host.cr:648-658). */
+int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset, int32_t table_rows, uint32_t width,
+                      uint64_t ids, uint32_t count, uint64_t dst);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSOMITE_HIP_H */

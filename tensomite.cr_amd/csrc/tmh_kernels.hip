@@ -1,0 +1,578 @@
+// Kernels of libtensomite_hip.so for gfx950 (CDNA4, wave64).
+//
+// Every kernel computes what the reference's host path computes, operation
+// for operation (src/tensomite/quant.cr; behaviour of the CUDA kernels in
+// src/tensomite/cuda/kernels.cu:1114-1375), so results are bit-identical to
+// tensomite's CPU quantised path:
+//
+//   - integer block dot products may be taken in any order (they are exact);
+//   - each block's floating-point contribution uses the host's expression:
+//       Q8_0  float(t) * (d * sx)             quant.cr:454
+//       Q4_0  (float(t) * d) * sx             quant.cr:471
+//       Q4_1  (d * sx) * float(t) + m * mx    quant.cr:488
+//   - every output adds its contributions one by one in block order,
+//     starting from 0.0f (quant.cr:447-455);
+//   - the bias is a separate addition after the sum (host.cr:725-734).
+//
+// The library is compiled with -ffp-contract=off, so no multiply-add is
+// fused, and with correctly rounded f32 division.
+#include "tmh_internal.h"
+
+namespace tmh {
+
+// ------------------------------------------------------------------ halves
+
+// Returns the half with bits `bits` (low 16 bits) as a float: exact for every
+// half that is not a NaN (F16#to_f32, f16.cr:44-57).
+__device__ __forceinline__ float half_value(uint32_t bits) {
+    union {
+        uint16_t u;
+        _Float16 h;
+    } v;
+    v.u = (uint16_t)bits;
+    return (float)v.h;
+}
+
+// Returns x rounded to the nearest half, ties to even, as a float: F16.new
+// (f16.cr:29-41) -- NaN becomes 0x7e00, values from 65520 up overflow,
+// subnormals are x * 2^24 rounded to even.
+__device__ __forceinline__ float round_to_half(float x) {
+    uint32_t word = __float_as_uint(x);
+    uint32_t sign = (word >> 16) & 0x8000u;
+    uint32_t magnitude = word & 0x7fffffffu;
+    uint32_t h;
+    if (magnitude >= 0x7f800000u) h = sign | (magnitude > 0x7f800000u ? 0x7e00u : 0x7c00u);
+    else if (magnitude >= 0x477ff000u) h = sign | 0x7c00u;
+    else if (magnitude < 0x38800000u) h = sign | (uint32_t)__builtin_rintf(__uint_as_float(magnitude) * 16777216.0f);
+    else h = sign | ((magnitude - 0x38000000u + 0xfffu + ((magnitude >> 13) & 1u)) >> 13);
+    return half_value(h);
+}
+
+// ------------------------------------------------------ activation quantise
+
+// One group of 8 lanes per block of 32 activations, 4 values a lane: the
+// block's largest magnitude and Σq are reduced over the 8 lanes (max and
+// integer sums are exact in any order). Then, as quantize_activations
+// (quant.cr:428-442): d = amax/127, id = 1/d (0 when d is 0),
+// q = round-half-away(x·id) as int8, scale F16(d), sum F16(float(Σq)·d).
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_quantize_rows_q8(const float* __restrict__ x, uint32_t ldx, uint32_t nb,
+                                                          uint32_t k, uint32_t blocks, float* __restrict__ scales,
+                                                          float* __restrict__ sums, int32_t* __restrict__ totals,
+                                                          int8_t* __restrict__ qs) {
+    const uint32_t g = (blockIdx.x * 256u + threadIdx.x) >> 3;
+    const uint32_t sub = threadIdx.x & 7u;
+    if (g >= blocks) return;  // all 8 lanes of a block leave together
+    const uint32_t row = g / nb, blk = g - row * nb;
+    const float* src = x + (size_t)row * ldx + blk * 32u + sub * 4u;
+    float v0, v1, v2, v3;
+    if constexpr (VEC) {
+        float4 v = *(const float4*)src;
+        v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+    } else {
+        v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+    }
+    float amax = fabsf(v0);
+    amax = fabsf(v1) > amax ? fabsf(v1) : amax;
+    amax = fabsf(v2) > amax ? fabsf(v2) : amax;
+    amax = fabsf(v3) > amax ? fabsf(v3) : amax;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) {
+        float other = __shfl_xor(amax, width, 8);
+        amax = other > amax ? other : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = d == 0.0f ? 0.0f : 1.0f / d;
+    const int q0 = (int8_t)(int)roundf(v0 * id);
+    const int q1 = (int8_t)(int)roundf(v1 * id);
+    const int q2 = (int8_t)(int)roundf(v2 * id);
+    const int q3 = (int8_t)(int)roundf(v3 * id);
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | (uint32_t)(q1 & 0xff) << 8 | (uint32_t)(q2 & 0xff) << 16 |
+                            (uint32_t)(q3 & 0xff) << 24;
+    *(uint32_t*)(qs + (size_t)row * k + blk * 32u + sub * 4u) = packed;
+    int total = q0 + q1 + q2 + q3;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) total += __shfl_xor(total, width, 8);
+    if (sub == 0) {
+        scales[g] = round_to_half(d);
+        sums[g] = round_to_half((float)total * d);
+        totals[g] = total;
+    }
+}
+
+// ------------------------------------------------------ block contributions
+
+// Formats as the kernels see them: a pair of consecutive blocks is PW
+// dwords, dword-aligned when the row is (two blocks of 18, 34 or 20 bytes are
+// 36, 68 or 40 bytes).
+template <int KIND>
+struct Fmt;
+template <>
+struct Fmt<0> {
+    static constexpr uint32_t BB = 34, PW = 17;
+};
+template <>
+struct Fmt<1> {
+    static constexpr uint32_t BB = 18, PW = 9;
+};
+template <>
+struct Fmt<2> {
+    static constexpr uint32_t BB = 20, PW = 10;
+};
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t bytes) {
+    return __builtin_amdgcn_alignbyte(hi, lo, bytes);
+}
+
+// The contributions of the two blocks of one pair (dwords u) to one output,
+// given the pair's quantised activations: a[0..7] and a[8..15] the int8
+// values of the two blocks, sx the scales, ex the Q4_0 totals (as -8·Σq) or
+// the Q4_1 F16(d·Σq).
+template <int KIND>
+struct Pair;
+
+// Q8_0: block 0 = d at bytes 0-1, values at 2-33; block 1 = d at 34-35,
+// values at 36-67 (dwords 9-16, aligned). t = Σ w·q; float(t) * (d * sx).
+template <>
+struct Pair<0> {
+    __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
+                                                      int, int, float&, float&, float& c0, float& c1) {
+        int t0 = 0, t1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t0 = dot4(funnel(u[i + 1], u[i], 2), a[i], t0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t1 = dot4(u[9 + i], a[8 + i], t1);
+        const float s0 = half_value(u[0] & 0xffffu) * sx0;
+        const float s1 = half_value(u[8] >> 16) * sx1;
+        c0 = (float)t0 * s0;
+        c1 = (float)t1 * s1;
+    }
+};
+
+// Q4_0: block 0 = d at bytes 0-1, nibbles at 2-17; block 1 = d at 18-19,
+// nibbles at 20-35 (dwords 5-8, aligned). Byte j holds element j (low) and
+// j+16 (high). t = Σ(q-8)·y = Σq·y - 8·Σy; (float(t) * d) * sx.
+template <>
+struct Pair<1> {
+    __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
+                                                      int neg8_0, int neg8_1, float&, float&, float& c0,
+                                                      float& c1) {
+        int t0 = neg8_0, t1 = neg8_1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = funnel(u[i + 1], u[i], 2);
+            t0 = dot4(w & 0x0f0f0f0fu, a[i], t0);
+            t0 = dot4((w >> 4) & 0x0f0f0f0fu, a[4 + i], t0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = u[5 + i];
+            t1 = dot4(w & 0x0f0f0f0fu, a[8 + i], t1);
+            t1 = dot4((w >> 4) & 0x0f0f0f0fu, a[12 + i], t1);
+        }
+        const float p0 = (float)t0 * half_value(u[0] & 0xffffu);
+        const float p1 = (float)t1 * half_value(u[4] >> 16);
+        c0 = p0 * sx0;
+        c1 = p1 * sx1;
+    }
+};
+
+// Q4_1: block 0 = d, m at bytes 0-3, nibbles at 4-19; block 1 = d, m at
+// 20-23, nibbles at 24-39; all aligned. t = Σq·y;
+// (d * sx) * float(t) + m * mx.
+template <>
+struct Pair<2> {
+    __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
+                                                      int, int, float& mx0, float& mx1, float& c0, float& c1) {
+        int t0 = 0, t1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            t0 = dot4(u[1 + i] & 0x0f0f0f0fu, a[i], t0);
+            t0 = dot4((u[1 + i] >> 4) & 0x0f0f0f0fu, a[4 + i], t0);
+            t1 = dot4(u[6 + i] & 0x0f0f0f0fu, a[8 + i], t1);
+            t1 = dot4((u[6 + i] >> 4) & 0x0f0f0f0fu, a[12 + i], t1);
+        }
+        const float s0 = half_value(u[0] & 0xffffu) * sx0;
+        const float s1 = half_value(u[5] & 0xffffu) * sx1;
+        const float f0 = s0 * (float)t0;
+        const float f1 = s1 * (float)t1;
+        const float g0 = half_value(u[0] >> 16) * mx0;
+        const float g1 = half_value(u[5] >> 16) * mx1;
+        c0 = f0 + g0;
+        c1 = f1 + g1;
+    }
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Loads the PW dwords of a pair at p (dword-aligned).
+template <int KIND>
+__device__ __forceinline__ void load_pair(const uint32_t* __restrict__ p, uint32_t* u) {
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+#pragma unroll
+    for (uint32_t i = 0; i + 4 <= PW; i += 4) {
+        u32x4 v;
+        __builtin_memcpy(&v, p + i, 16);
+        u[i] = v.x, u[i + 1] = v.y, u[i + 2] = v.z, u[i + 3] = v.w;
+    }
+    if constexpr (PW % 4 == 1) {
+        u[PW - 1] = p[PW - 1];
+    } else if constexpr (PW % 4 == 2) {
+        u32x2 v;
+        __builtin_memcpy(&v, p + PW - 2, 8);
+        u[PW - 2] = v.x, u[PW - 1] = v.y;
+    }
+}
+
+// The quantised activations of pair j of activation row b.
+template <int KIND>
+__device__ __forceinline__ void load_activations(const Activations& act, uint32_t k, uint32_t nb, uint32_t b,
+                                                 uint32_t j, uint32_t* a, float& sx0, float& sx1, int& e0, int& e1,
+                                                 float& mx0, float& mx1) {
+    const u32x4* q = (const u32x4*)(act.qs + (size_t)b * k + (size_t)j * 64u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32x4 v = q[i];
+        a[4 * i] = v.x, a[4 * i + 1] = v.y, a[4 * i + 2] = v.z, a[4 * i + 3] = v.w;
+    }
+    const size_t at = (size_t)b * nb + 2u * j;
+    const float2 s = *(const float2*)(act.scales + at);
+    sx0 = s.x, sx1 = s.y;
+    if constexpr (KIND == 1) {
+        const int2 t = *(const int2*)(act.totals + at);
+        e0 = -8 * t.x, e1 = -8 * t.y;
+    }
+    if constexpr (KIND == 2) {
+        const float2 m = *(const float2*)(act.sums + at);
+        mx0 = m.x, mx1 = m.y;
+    }
+}
+
+// --------------------------------------------------------- lanes: matvec
+
+// x · wᵀ for NB activation rows and a tile of `tr` weight rows per
+// workgroup of 256 threads, for rows of an even number of blocks nb ≤ 512
+// starting dword-aligned.
+//
+// Work: each weight row is np = nb/2 pairs of blocks. Threads form row
+// groups of np threads; thread t takes pair j = t % np of row t / np of each
+// step of rpi = 256/np rows, so consecutive threads read consecutive bytes of
+// one row and each thread keeps its pair's activations for the whole tile.
+// A thread computes its pair's two contributions to each output it touches
+// and writes them to LDS, part[output][block]. Then thread o < NB·tr adds
+// the contributions of output o (and o + 256, ...) one by one in block order
+// -- the host's order -- and writes it, plus the bias.
+template <int KIND, int NB>
+__global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, Activations act,
+                                                float* __restrict__ dst, const float* __restrict__ bias, uint32_t n,
+                                                uint32_t k, uint32_t tr, uint32_t stride) {
+    extern __shared__ float part[];
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+    const uint32_t t = threadIdx.x;
+    const uint32_t nb = k >> 5;
+    const uint32_t np = nb >> 1;
+    const uint32_t rpi = 256u / np;
+    const uint32_t j = t % np, rsub = t / np;
+    const uint32_t row0 = blockIdx.x * tr;
+    const uint32_t steps = tr / rpi;
+    const size_t row_words = (size_t)np * PW;
+    const uint32_t* wp = (const uint32_t*)w;
+
+    if (rsub < rpi) {
+        uint32_t a[NB == 1 ? 16 : 1];
+        float sx0 = 0, sx1 = 0, mx0 = 0, mx1 = 0;
+        int e0 = 0, e1 = 0;
+        if constexpr (NB == 1) load_activations<KIND>(act, k, nb, 0, j, a, sx0, sx1, e0, e1, mx0, mx1);
+#pragma unroll 2
+        for (uint32_t s = 0; s < steps; ++s) {
+            const uint32_t r = s * rpi + rsub;
+            const uint32_t row = row0 + r;
+            if (row >= n) break;
+            uint32_t u[PW];
+            load_pair<KIND>(wp + (size_t)row * row_words + (size_t)j * PW, u);
+            if constexpr (NB == 1) {
+                float c0, c1;
+                Pair<KIND>::contribute(u, a, sx0, sx1, e0, e1, mx0, mx1, c0, c1);
+                *(float2*)(part + (size_t)r * stride + 2u * j) = make_float2(c0, c1);
+            } else {
+#pragma unroll 1
+                for (uint32_t b = 0; b < (uint32_t)NB; ++b) {
+                    uint32_t ab[16];
+                    float bsx0, bsx1, bmx0 = 0, bmx1 = 0;
+                    int be0 = 0, be1 = 0;
+                    load_activations<KIND>(act, k, nb, b, j, ab, bsx0, bsx1, be0, be1, bmx0, bmx1);
+                    float c0, c1;
+                    Pair<KIND>::contribute(u, ab, bsx0, bsx1, be0, be1, bmx0, bmx1, c0, c1);
+                    *(float2*)(part + (size_t)(b * tr + r) * stride + 2u * j) = make_float2(c0, c1);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t o = t; o < (uint32_t)NB * tr; o += 256u) {
+        const uint32_t b = o / tr, r = o - b * tr;
+        const uint32_t row = row0 + r;
+        if (row < n) {
+            const float* c = part + (size_t)o * stride;
+            float sum = 0.0f;
+            uint32_t i = 0;
+            for (; i + 4 <= nb; i += 4) {
+                const float4 v = *(const float4*)(c + i);
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+            }
+            for (; i < nb; ++i) sum += c[i];
+            dst[(size_t)b * n + row] = bias ? sum + bias[row] : sum;
+        }
+    }
+}
+
+// ------------------------------------------------- thread per output
+
+// One thread per output, adding its blocks in order from byte loads: any
+// alignment, any k (block_matmul_f32's division of work, cuda/kernels.cu:1230-1246).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_block_matmul_thread(const uint8_t* __restrict__ w, Activations act,
+                                                             float* __restrict__ dst,
+                                                             const float* __restrict__ bias, uint32_t n,
+                                                             uint32_t k, uint32_t count) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t row = i / n, col = i - row * n;
+    const uint32_t nb = k >> 5;
+    constexpr uint32_t BB = Fmt<KIND>::BB;
+    const uint8_t* wr = w + (size_t)col * nb * BB;
+    const int8_t* qr = act.qs + (size_t)row * k;
+    float sum = 0.0f;
+    for (uint32_t blk = 0; blk < nb; ++blk) {
+        const uint8_t* p = wr + blk * BB;
+        const int8_t* q = qr + blk * 32u;
+        const float d = half_value((uint32_t)p[0] | (uint32_t)p[1] << 8);
+        const float sx = act.scales[(size_t)row * nb + blk];
+        if constexpr (KIND == 0) {
+            int t = 0;
+            for (int e = 0; e < 32; ++e) t += (int)(int8_t)p[2 + e] * (int)q[e];
+            const float s = d * sx;
+            sum += (float)t * s;
+        } else if constexpr (KIND == 1) {
+            int t = 0;
+            for (int e = 0; e < 16; ++e) {
+                t += ((int)(p[2 + e] & 0x0f) - 8) * (int)q[e];
+                t += ((int)(p[2 + e] >> 4) - 8) * (int)q[e + 16];
+            }
+            const float c = (float)t * d;
+            sum += c * sx;
+        } else {
+            int t = 0;
+            for (int e = 0; e < 16; ++e) {
+                t += (int)(p[4 + e] & 0x0f) * (int)q[e];
+                t += (int)(p[4 + e] >> 4) * (int)q[e + 16];
+            }
+            const float m = half_value((uint32_t)p[2] | (uint32_t)p[3] << 8);
+            const float s = d * sx;
+            const float f = s * (float)t;
+            const float g = m * act.sums[(size_t)row * nb + blk];
+            sum += f + g;
+        }
+    }
+    dst[i] = bias ? sum + bias[col] : sum;
+}
+
+// ---------------------------------------------------------------- gather
+
+// One thread per output element: element i is value i % width of table row
+// ids[i / width], dequantised as dequantize_* (quant.cr:537-556). An id out of
+// range writes 0 and is reported: errors[0] counts reports, and the first
+// reporter writes the id and the row count (cuda/kernels.cu:176-184).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_gather_blocks(const uint8_t* __restrict__ table,
+                                                       const int32_t* __restrict__ ids, float* __restrict__ dst,
+                                                       int32_t* __restrict__ errors, int32_t rows, uint32_t width,
+                                                       uint32_t total) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t r = i / width, e = i - r * width;
+    const int32_t id = ids[r];
+    if (id < 0 || id >= rows) {
+        if (atomicAdd(&errors[0], 1) == 0) {
+            errors[1] = id;
+            errors[2] = rows;
+        }
+        dst[i] = 0.0f;
+        return;
+    }
+    constexpr uint32_t BB = Fmt<KIND>::BB;
+    const uint8_t* p = table + (size_t)id * (width >> 5) * BB + (e >> 5) * BB;
+    const uint32_t at = e & 31u;
+    const float d = half_value((uint32_t)p[0] | (uint32_t)p[1] << 8);
+    float v;
+    if constexpr (KIND == 0) {
+        v = (float)(int8_t)p[2 + at] * d;
+    } else {
+        const uint32_t packed = p[(KIND == 1 ? 2u : 4u) + (at & 15u)];
+        const uint32_t q = at < 16u ? (packed & 0x0fu) : (packed >> 4);
+        if constexpr (KIND == 1) {
+            v = (float)((int)q - 8) * d;
+        } else {
+            const float m = half_value((uint32_t)p[2] | (uint32_t)p[3] << 8);
+            const float s = d * (float)q;
+            v = s + m;
+        }
+    }
+    dst[i] = v;
+}
+
+// ---------------------------------------------------------------- launchers
+
+hipError_t launch_quantize(const float* x, uint32_t ldx, uint32_t rows, uint32_t k, float* scales, float* sums,
+                           int32_t* totals, int8_t* qs, hipStream_t stream) {
+    const uint32_t nb = k >> 5;
+    const uint32_t blocks = rows * nb;
+    if (blocks == 0) return hipSuccess;
+    const uint32_t grid = (blocks * 8u + 255u) / 256u;
+    const bool vec = ((uintptr_t)x % 16u == 0) && (ldx % 4u == 0);
+    if (vec)
+        hipLaunchKernelGGL(k_quantize_rows_q8<true>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks, scales,
+                           sums, totals, qs);
+    else
+        hipLaunchKernelGGL(k_quantize_rows_q8<false>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks,
+                           scales, sums, totals, qs);
+    return hipGetLastError();
+}
+
+// Padded LDS row stride, in floats, for a row of nb contributions: a
+// multiple of 4 (16-byte reads) whose quarter is odd, so 8 consecutive
+// output rows start in 8 different 16-byte bank groups.
+static uint32_t lanes_stride(uint32_t nb) {
+    uint32_t s = (nb + 3u) & ~3u;
+    if (((s >> 2) & 1u) == 0) s += 4u;
+    return s;
+}
+
+static constexpr size_t LANES_LDS_LIMIT = 56u * 1024u;
+
+// Chooses the rows per workgroup: a multiple of the rows one step covers,
+// with every output's fold on its own thread and the contributions within
+// the LDS limit, as large as still leaves about two workgroups per compute
+// unit, else the smallest.
+static uint32_t lanes_tile(uint32_t nb, uint32_t nbatch, uint32_t n, int compute_units) {
+    const uint32_t np = nb / 2u;
+    const uint32_t rpi = 256u / np;
+    const uint32_t stride = lanes_stride(nb);
+    uint32_t best = rpi;
+    const uint64_t want = (uint64_t)2u * (uint32_t)(compute_units > 0 ? compute_units : 256);
+    for (uint32_t m = 2;; ++m) {
+        const uint32_t tr = rpi * m;
+        if (nbatch * tr > 256u || (size_t)nbatch * tr * stride * 4u > LANES_LDS_LIMIT) break;
+        if ((n + tr - 1u) / tr < want) break;
+        best = tr;
+    }
+    return best;
+}
+
+template <int KIND, int NB>
+static hipError_t launch_lanes_nb(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t n,
+                                  uint32_t k, int compute_units, hipStream_t stream) {
+    const uint32_t nb = k >> 5;
+    const uint32_t tr = lanes_tile(nb, NB, n, compute_units);
+    const uint32_t stride = lanes_stride(nb);
+    const size_t lds = (size_t)NB * tr * stride * sizeof(float);
+    const uint32_t grid = (n + tr - 1u) / tr;
+    hipLaunchKernelGGL((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, n, k, tr, stride);
+    return hipGetLastError();
+}
+
+template <int KIND>
+static hipError_t launch_lanes(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
+                               uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+    // Activation rows in groups of 16, 8, 4, 2 and 1: each output depends on
+    // its own row only, so the grouping changes no bits.
+    const uint32_t nb = k >> 5;
+    const uint32_t rpi = 256u / (nb / 2u);
+    const size_t smallest = (size_t)rpi * lanes_stride(nb) * sizeof(float);  // LDS of one row group
+    uint32_t done = 0;
+    while (done < rows) {
+        const uint32_t left = rows - done;
+        Activations a = act;
+        a.scales += (size_t)done * nb;
+        a.sums += (size_t)done * nb;
+        a.totals += (size_t)done * nb;
+        a.qs += (size_t)done * k;
+        float* d = dst + (size_t)done * n;
+        hipError_t err;
+        uint32_t take;
+        if (left >= 16 && 16u * smallest <= LANES_LDS_LIMIT)
+            err = launch_lanes_nb<KIND, 16>(w, a, d, bias, n, k, compute_units, stream), take = 16;
+        else if (left >= 8 && 8u * smallest <= LANES_LDS_LIMIT)
+            err = launch_lanes_nb<KIND, 8>(w, a, d, bias, n, k, compute_units, stream), take = 8;
+        else if (left >= 4 && 4u * smallest <= LANES_LDS_LIMIT)
+            err = launch_lanes_nb<KIND, 4>(w, a, d, bias, n, k, compute_units, stream), take = 4;
+        else if (left >= 2 && 2u * smallest <= LANES_LDS_LIMIT)
+            err = launch_lanes_nb<KIND, 2>(w, a, d, bias, n, k, compute_units, stream), take = 2;
+        else err = launch_lanes_nb<KIND, 1>(w, a, d, bias, n, k, compute_units, stream), take = 1;
+        if (err != hipSuccess) return err;
+        done += take;
+    }
+    return hipSuccess;
+}
+
+template <int KIND>
+static hipError_t launch_thread(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
+                                uint32_t n, uint32_t k, hipStream_t stream) {
+    const uint32_t count = rows * n;
+    const uint32_t grid = (count + 255u) / 256u;
+    hipLaunchKernelGGL(k_block_matmul_thread<KIND>, dim3(grid), dim3(256), 0, stream, w, act, dst, bias, n, k, count);
+    return hipGetLastError();
+}
+
+// Whether the lanes kernel can take a weight: rows of an even number of
+// blocks, at most 512, starting dword-aligned.
+static bool lanes_fit(const uint8_t* w, uint32_t k) {
+    const uint32_t nb = k >> 5;
+    return nb >= 2 && nb % 2 == 0 && nb <= 512 && (uintptr_t)w % 4u == 0;
+}
+
+hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, Activations act, float* dst,
+                               const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                               hipStream_t stream) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    const bool thread = mode == 1u /* THREAD */ || !lanes_fit(w, k) ||
+                        (mode == 0u /* AUTO */ && (uint64_t)rows * n >= 65536u && rows > 16u);
+    switch (kind) {
+    case 0:
+        return thread ? launch_thread<0>(w, act, dst, bias, rows, n, k, stream)
+                      : launch_lanes<0>(w, act, dst, bias, rows, n, k, compute_units, stream);
+    case 1:
+        return thread ? launch_thread<1>(w, act, dst, bias, rows, n, k, stream)
+                      : launch_lanes<1>(w, act, dst, bias, rows, n, k, compute_units, stream);
+    default:
+        return thread ? launch_thread<2>(w, act, dst, bias, rows, n, k, stream)
+                      : launch_lanes<2>(w, act, dst, bias, rows, n, k, compute_units, stream);
+    }
+}
+
+hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
+                         uint32_t count, float* dst, int32_t* errors, hipStream_t stream) {
+    const uint32_t total = count * width;
+    if (total == 0) return hipSuccess;
+    const uint32_t grid = (total + 255u) / 256u;
+    if (kind == 0)
+        hipLaunchKernelGGL(k_gather_blocks<0>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+                           width, total);
+    else if (kind == 1)
+        hipLaunchKernelGGL(k_gather_blocks<1>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+                           width, total);
+    else
+        hipLaunchKernelGGL(k_gather_blocks<2>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+                           width, total);
+    return hipGetLastError();
+}
+
+}  // namespace tmh

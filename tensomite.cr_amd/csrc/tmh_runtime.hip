@@ -1,0 +1,697 @@
+// The C ABI of libtensomite_hip.so (include/tensomite_hip.h): devices,
+// memory, the buffer layer, errors, events, and the kernel entry points.
+//
+// Per device the library keeps one ordered stream, a pool of freed device
+// memory keyed by exact size with a finalizer-safe retired list in front of
+// it, a pinned staging ring for asynchronous uploads, growable scratch for
+// quantised activations, and the 12-byte error buffer gather kernels report
+// into. This is the host side of the reference's `CUDA < HostDevice`
+// (src/tensomite/cuda.cr) and its `BufferPool`/`RetiredList`
+// (src/tensomite/buffer_pool.cr), restated natively for HIP.
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/tensomite_hip.h"
+#include "tmh_internal.h"
+
+namespace {
+
+constexpr int MAX_DEVICES = 16;
+
+// Exact-size pool of freed device memory, as BufferPool (buffer_pool.cr:12-74):
+// `take` and `give` never wait -- while another caller holds the lock, take
+// returns nothing and give returns false, and the caller allocates or frees
+// instead.
+class Pool {
+  public:
+    int64_t limit = 1ll << 30;
+    int64_t held = 0;
+    std::atomic<int64_t> hits{0}, misses{0};
+
+    uint64_t take(uint64_t bytes) {
+        uint64_t ptr = 0;
+        if (lock()) {
+            auto it = free_.find(bytes);
+            if (it != free_.end() && !it->second.empty()) {
+                ptr = it->second.back();
+                it->second.pop_back();
+                held -= (int64_t)bytes;
+            }
+            unlock();
+        }
+        (ptr ? hits : misses).fetch_add(1);
+        return ptr;
+    }
+
+    bool give(uint64_t ptr, uint64_t bytes) {
+        if (bytes == 0 || !lock()) return false;
+        bool kept = false;
+        if (held + (int64_t)bytes <= limit) {
+            free_[bytes].push_back(ptr);
+            held += (int64_t)bytes;
+            kept = true;
+        }
+        unlock();
+        return kept;
+    }
+
+    // Frees everything held (at process teardown or on request).
+    template <typename F>
+    void drain_all(F&& free_fn) {
+        while (!lock()) std::this_thread::yield();
+        for (auto& [bytes, list] : free_)
+            for (uint64_t p : list) free_fn(p, bytes);
+        free_.clear();
+        held = 0;
+        unlock();
+    }
+
+  private:
+    std::unordered_map<uint64_t, std::vector<uint64_t>> free_;
+    std::atomic<bool> lock_{false};
+    bool lock() {
+        bool expected = false;
+        return lock_.compare_exchange_strong(expected, true);
+    }
+    void unlock() { lock_.store(false); }
+};
+
+// Memory given back from any thread, waiting to move into the pool, as
+// RetiredList (buffer_pool.cr:87-129): `push` never allocates and never
+// waits; it stores into one of two fixed arrays and returns false when busy
+// or full. `drain` swaps the arrays, on the device's own calls only.
+class Retired {
+  public:
+    static constexpr int CAPACITY = 16384;
+    struct Entry {
+        uint64_t ptr, bytes;
+    };
+
+    bool push(uint64_t ptr, uint64_t bytes) {
+        bool expected = false;
+        if (!lock_.compare_exchange_strong(expected, true)) return false;
+        bool kept = false;
+        if (count_ < CAPACITY) {
+            filling_[count_++] = Entry{ptr, bytes};
+            kept = true;
+        }
+        lock_.store(false);
+        return kept;
+    }
+
+    template <typename F>
+    void drain(F&& each) {
+        if (count_ == 0) return;
+        bool expected = false;
+        while (!lock_.compare_exchange_strong(expected, true)) {
+            expected = false;
+            std::this_thread::yield();
+        }
+        Entry* full = filling_;
+        int count = count_;
+        filling_ = draining_;
+        draining_ = full;
+        count_ = 0;
+        lock_.store(false);
+        for (int i = 0; i < count; ++i) each(full[i].ptr, full[i].bytes);
+    }
+
+  private:
+    Entry a_[CAPACITY];
+    Entry b_[CAPACITY];
+    Entry* filling_ = a_;
+    Entry* draining_ = b_;
+    int count_ = 0;
+    std::atomic<bool> lock_{false};
+};
+
+// Pinned host memory for asynchronous uploads: SLOTS buffers of SLOT_BYTES,
+// used round robin; a slot is reused once the copy out of it has finished.
+struct Staging {
+    static constexpr int SLOTS = 4;
+    static constexpr size_t SLOT_BYTES = 16u << 20;
+    void* slot[SLOTS] = {};
+    hipEvent_t done[SLOTS] = {};
+    bool used[SLOTS] = {};
+    int next = 0;
+    bool ready = false;
+};
+
+struct Device {
+    std::mutex setup;
+    bool ready = false;
+    int index = 0;
+    hipStream_t stream = nullptr;
+    int compute_units = 256;
+    uint64_t memory = 0;
+
+    // The error buffer (count, first id, rows), cuda.cr:961-964.
+    int32_t* errors = nullptr;
+    std::atomic<bool> errors_pending{false};
+    int32_t report[3] = {0, 0, 0};
+
+    // Scratch for quantised activations, kept and grown across launches
+    // (cuda.cr:788-798); `launch` keeps a quantise pass and its product
+    // together.
+    std::mutex launch;
+    uint8_t* scratch = nullptr;
+    size_t scratch_bytes = 0;
+
+    Pool pool;
+    Retired* retired = nullptr;
+    std::mutex staging_lock;
+    Staging staging;
+
+    std::atomic<int64_t> uploads{0}, downloads{0}, gpu_ops{0}, device_bytes{0}, frees{0};
+};
+
+Device g_devices[MAX_DEVICES];
+std::atomic<int> g_count{-1};
+std::atomic<int> g_fail_allocations{0};
+std::atomic<bool> g_kernels_off{false};
+thread_local int t_device = 0;
+
+int code(hipError_t e) { return (int)e; }
+
+// Device allocation honouring the test hook.
+hipError_t device_malloc(void** p, size_t bytes) {
+    int left = g_fail_allocations.load();
+    while (left > 0) {
+        if (g_fail_allocations.compare_exchange_weak(left, left - 1)) return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
+int count_devices() {
+    int n = g_count.load();
+    if (n >= 0) return n;
+    int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+    if (c > MAX_DEVICES) c = MAX_DEVICES;
+    g_count.store(c);
+    return c;
+}
+
+// Returns the calling thread's device, made current and set up on first
+// use, or null with *err set.
+Device* current(int* err) {
+    const int n = count_devices();
+    if (n == 0 || t_device < 0 || t_device >= n) {
+        *err = TMH_ERROR_NO_DEVICE;
+        return nullptr;
+    }
+    int now = -1;
+    if (hipGetDevice(&now) != hipSuccess || now != t_device) {
+        hipError_t e = hipSetDevice(t_device);
+        if (e != hipSuccess) {
+            *err = code(e);
+            return nullptr;
+        }
+    }
+    Device& d = g_devices[t_device];
+    if (!d.ready) {
+        std::lock_guard<std::mutex> guard(d.setup);
+        if (!d.ready) {
+            d.index = t_device;
+            hipDeviceProp_t prop;
+            hipError_t e = hipGetDeviceProperties(&prop, t_device);
+            if (e == hipSuccess) {
+                d.compute_units = prop.multiProcessorCount;
+                d.memory = prop.totalGlobalMem;
+                int64_t quarter = (int64_t)(prop.totalGlobalMem / 4);
+                d.pool.limit = quarter > (1ll << 30) ? quarter : (1ll << 30);
+                e = hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking);
+            }
+            if (e == hipSuccess) e = hipMalloc((void**)&d.errors, 3 * sizeof(int32_t));
+            if (e == hipSuccess) e = hipMemset(d.errors, 0, 3 * sizeof(int32_t));
+            if (e != hipSuccess) {
+                *err = code(e);
+                return nullptr;
+            }
+            d.retired = new Retired();
+            d.ready = true;
+        }
+    }
+    *err = TMH_SUCCESS;
+    return &d;
+}
+
+void recycle_retired(Device& d) {
+    d.retired->drain([&](uint64_t ptr, uint64_t bytes) {
+        if (d.pool.give(ptr, bytes)) return;
+        (void)hipFree((void*)ptr);
+        d.device_bytes.fetch_sub((int64_t)(bytes < 4 ? 4 : bytes));
+        d.frees.fetch_add(1);
+    });
+}
+
+// Grows the activation scratch to at least `bytes`, waiting for the work
+// that may still read the old one.
+int ensure_scratch(Device& d, size_t bytes) {
+    if (bytes <= d.scratch_bytes) return TMH_SUCCESS;
+    size_t grown = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    hipError_t e = hipStreamSynchronize(d.stream);
+    if (e != hipSuccess) return code(e);
+    if (d.scratch) (void)hipFree(d.scratch);
+    d.scratch = nullptr;
+    d.scratch_bytes = 0;
+    void* p = nullptr;
+    e = device_malloc(&p, grown);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
+    d.scratch = (uint8_t*)p;
+    d.scratch_bytes = grown;
+    return TMH_SUCCESS;
+}
+
+size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
+
+// Carves the scratch into the quantise pass's four outputs for `rows` rows of k.
+tmh::Activations carve(Device& d, uint32_t rows, uint32_t k, float** scales, float** sums, int32_t** totals,
+                       int8_t** qs) {
+    const size_t nb = k / 32u;
+    const size_t per = align256((size_t)rows * nb * 4u);
+    uint8_t* base = d.scratch;
+    *scales = (float*)base;
+    *sums = (float*)(base + per);
+    *totals = (int32_t*)(base + 2 * per);
+    *qs = (int8_t*)(base + 3 * per);
+    return tmh::Activations{*scales, *sums, *totals, *qs};
+}
+
+size_t scratch_need(uint32_t rows, uint32_t k) {
+    const size_t nb = k / 32u;
+    return 3 * align256((size_t)rows * nb * 4u) + align256((size_t)rows * k);
+}
+
+const char* library_name(int c) {
+    switch (c) {
+    case TMH_SUCCESS: return "TMH_SUCCESS";
+    case TMH_ERROR_INVALID_VALUE: return "TMH_ERROR_INVALID_VALUE";
+    case TMH_ERROR_SHAPE: return "TMH_ERROR_SHAPE";
+    case TMH_ERROR_DTYPE: return "TMH_ERROR_DTYPE";
+    case TMH_ERROR_NO_KERNELS: return "TMH_ERROR_NO_KERNELS";
+    case TMH_ERROR_OUT_OF_MEMORY: return "TMH_ERROR_OUT_OF_MEMORY";
+    case TMH_ERROR_EXECUTION: return "TMH_ERROR_EXECUTION";
+    case TMH_ERROR_NO_DEVICE: return "TMH_ERROR_NO_DEVICE";
+    case TMH_ERROR_BUSY: return "TMH_ERROR_BUSY";
+    default: return nullptr;
+    }
+}
+
+const char* library_string(int c) {
+    switch (c) {
+    case TMH_SUCCESS: return "no error";
+    case TMH_ERROR_INVALID_VALUE: return "an argument is out of range";
+    case TMH_ERROR_SHAPE: return "shapes do not agree";
+    case TMH_ERROR_DTYPE: return "not a block format (Q8_0, Q4_0 or Q4_1)";
+    case TMH_ERROR_NO_KERNELS: return "the library's kernels are not available";
+    case TMH_ERROR_OUT_OF_MEMORY: return "out of device memory";
+    case TMH_ERROR_EXECUTION: return "a kernel found an index out of range";
+    case TMH_ERROR_NO_DEVICE: return "no such GPU";
+    case TMH_ERROR_BUSY: return "the retired list is busy or full";
+    default: return nullptr;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmh_init(int32_t* count) {
+    if (!count) return TMH_ERROR_INVALID_VALUE;
+    *count = count_devices();
+    return TMH_SUCCESS;
+}
+
+int tmh_device_info_get(int32_t device, tmh_device_info* out) {
+    if (!out) return TMH_ERROR_INVALID_VALUE;
+    if (device < 0 || device >= count_devices()) return TMH_ERROR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return code(e);
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+    out->memory = prop.totalGlobalMem;
+    out->compute_units = prop.multiProcessorCount;
+    out->clock_khz = prop.clockRate;
+    out->memory_clock_khz = prop.memoryClockRate;
+    out->memory_bus_width = prop.memoryBusWidth;
+    out->l2_bytes = prop.l2CacheSize;
+    out->lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
+    return TMH_SUCCESS;
+}
+
+int tmh_set_device(int32_t device) {
+    if (device < 0 || device >= count_devices()) return TMH_ERROR_NO_DEVICE;
+    t_device = device;
+    int err;
+    current(&err);
+    return err;
+}
+
+int tmh_get_device(int32_t* device) {
+    if (!device) return TMH_ERROR_INVALID_VALUE;
+    *device = t_device;
+    return TMH_SUCCESS;
+}
+
+int tmh_malloc(uint64_t* ptr, uint64_t bytes) {
+    if (!ptr) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    void* p = nullptr;
+    const uint64_t size = bytes < 4 ? 4 : bytes;
+    hipError_t e = device_malloc(&p, size);
+    if (e == hipErrorOutOfMemory) return TMH_ERROR_OUT_OF_MEMORY;
+    if (e != hipSuccess) return code(e);
+    d->device_bytes.fetch_add((int64_t)size);
+    *ptr = (uint64_t)p;
+    return TMH_SUCCESS;
+}
+
+int tmh_free(uint64_t ptr) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (ptr == 0) return TMH_SUCCESS;
+    return code(hipFree((void*)ptr));
+}
+
+int tmh_free_any_thread(uint64_t ptr) {
+    if (ptr) (void)hipFree((void*)ptr);
+    return TMH_SUCCESS;
+}
+
+int tmh_upload(uint64_t dst, const void* src, uint64_t bytes) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    d->uploads.fetch_add(1);
+    if (bytes == 0) return TMH_SUCCESS;
+    if (!dst || !src) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = hipMemcpyAsync((void*)dst, src, bytes, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    return code(e);
+}
+
+int tmh_upload_async(uint64_t dst, const void* src, uint64_t bytes) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    d->uploads.fetch_add(1);
+    if (bytes == 0) return TMH_SUCCESS;
+    if (!dst || !src) return TMH_ERROR_INVALID_VALUE;
+    std::lock_guard<std::mutex> guard(d->staging_lock);
+    Staging& s = d->staging;
+    if (!s.ready) {
+        for (int i = 0; i < Staging::SLOTS; ++i) {
+            hipError_t e = hipHostMalloc(&s.slot[i], Staging::SLOT_BYTES, hipHostMallocDefault);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&s.done[i], hipEventDisableTiming);
+            if (e != hipSuccess) return code(e);
+        }
+        s.ready = true;
+    }
+    uint64_t off = 0;
+    while (off < bytes) {
+        const size_t len = (size_t)std::min<uint64_t>(bytes - off, Staging::SLOT_BYTES);
+        const int i = s.next;
+        s.next = (s.next + 1) % Staging::SLOTS;
+        if (s.used[i]) {
+            hipError_t e = hipEventSynchronize(s.done[i]);
+            if (e != hipSuccess) return code(e);
+        }
+        std::memcpy(s.slot[i], (const uint8_t*)src + off, len);
+        hipError_t e = hipMemcpyAsync((void*)(dst + off), s.slot[i], len, hipMemcpyHostToDevice, d->stream);
+        if (e == hipSuccess) e = hipEventRecord(s.done[i], d->stream);
+        if (e != hipSuccess) return code(e);
+        s.used[i] = true;
+        off += len;
+    }
+    return TMH_SUCCESS;
+}
+
+int tmh_download(void* dst, uint64_t src, uint64_t bytes) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    d->downloads.fetch_add(1);
+    if (bytes == 0) return TMH_SUCCESS;
+    if (!dst || !src) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = hipMemcpyAsync(dst, (const void*)src, bytes, hipMemcpyDeviceToHost, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    return code(e);
+}
+
+int tmh_copy(uint64_t dst, uint64_t src, uint64_t bytes) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (bytes == 0) return TMH_SUCCESS;
+    if (!dst || !src) return TMH_ERROR_INVALID_VALUE;
+    return code(hipMemcpyAsync((void*)dst, (const void*)src, bytes, hipMemcpyDeviceToDevice, d->stream));
+}
+
+int tmh_synchronize(void) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    return code(hipStreamSynchronize(d->stream));
+}
+
+int tmh_alloc(uint64_t* ptr, uint64_t bytes) {
+    if (!ptr) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    recycle_retired(*d);
+    uint64_t p = d->pool.take(bytes);
+    if (!p) {
+        void* fresh = nullptr;
+        const uint64_t size = bytes < 4 ? 4 : bytes;
+        hipError_t e = device_malloc(&fresh, size);
+        if (e == hipErrorOutOfMemory) return TMH_ERROR_OUT_OF_MEMORY;
+        if (e != hipSuccess) return code(e);
+        d->device_bytes.fetch_add((int64_t)size);
+        p = (uint64_t)fresh;
+    }
+    *ptr = p;
+    return TMH_SUCCESS;
+}
+
+int tmh_retire(uint64_t ptr, uint64_t bytes) {
+    if (!ptr) return TMH_SUCCESS;
+    int err;
+    Device* d = current(&err);
+    if (!d) {
+        (void)hipFree((void*)ptr);
+        return TMH_SUCCESS;
+    }
+    if (d->retired->push(ptr, bytes)) return TMH_SUCCESS;
+    (void)hipFree((void*)ptr);
+    d->device_bytes.fetch_sub((int64_t)(bytes < 4 ? 4 : bytes));
+    d->frees.fetch_add(1);
+    return TMH_SUCCESS;
+}
+
+int tmh_sync(void) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    hipError_t e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return code(e);
+    recycle_retired(*d);
+    if (d->errors_pending.exchange(false)) {
+        int32_t got[3];
+        e = hipMemcpy(got, d->errors, sizeof(got), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return code(e);
+        if (got[0] != 0) {
+            std::memcpy(d->report, got, sizeof(got));
+            e = hipMemset(d->errors, 0, sizeof(got));
+            if (e != hipSuccess) return code(e);
+            return TMH_ERROR_EXECUTION;
+        }
+    }
+    return TMH_SUCCESS;
+}
+
+int tmh_pool_set_limit(int64_t bytes) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (bytes < 0) return TMH_ERROR_INVALID_VALUE;
+    d->pool.limit = bytes;
+    return TMH_SUCCESS;
+}
+
+int tmh_counters_get(tmh_counters* out) {
+    if (!out) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    out->uploads = d->uploads.load();
+    out->downloads = d->downloads.load();
+    out->gpu_ops = d->gpu_ops.load();
+    out->device_bytes = d->device_bytes.load();
+    out->pool_held = d->pool.held;
+    out->pool_limit = d->pool.limit;
+    out->pool_hits = d->pool.hits.load();
+    out->pool_misses = d->pool.misses.load();
+    out->frees = d->frees.load();
+    return TMH_SUCCESS;
+}
+
+const char* tmh_error_name(int c) {
+    if (const char* s = library_name(c)) return s;
+    if (c > 0 && c < 1000) return hipGetErrorName((hipError_t)c);
+    return "TMH_ERROR_UNKNOWN";
+}
+
+const char* tmh_error_string(int c) {
+    if (const char* s = library_string(c)) return s;
+    if (c > 0 && c < 1000) return hipGetErrorString((hipError_t)c);
+    return "unknown error";
+}
+
+int tmh_error_report(int32_t out[3]) {
+    if (!out) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    std::memcpy(out, d->report, sizeof(d->report));
+    std::memset(d->report, 0, sizeof(d->report));
+    return TMH_SUCCESS;
+}
+
+int tmh_debug_fail_allocations(int32_t count) {
+    g_fail_allocations.store(count < 0 ? 0 : count);
+    return TMH_SUCCESS;
+}
+
+int tmh_debug_disable_kernels(int32_t off) {
+    g_kernels_off.store(off != 0);
+    return TMH_SUCCESS;
+}
+
+int tmh_event_create(uint64_t* event) {
+    if (!event) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    if (!current(&err)) return err;
+    hipEvent_t ev;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) return code(e);
+    *event = (uint64_t)ev;
+    return TMH_SUCCESS;
+}
+
+int tmh_event_record(uint64_t event) {
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    return code(hipEventRecord((hipEvent_t)event, d->stream));
+}
+
+int tmh_event_elapsed_ms(uint64_t start, uint64_t stop, float* ms) {
+    if (!ms) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = hipEventSynchronize((hipEvent_t)stop);
+    if (e != hipSuccess) return code(e);
+    return code(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+}
+
+int tmh_event_destroy(uint64_t event) { return code(hipEventDestroy((hipEvent_t)event)); }
+
+int tmh_quantize_rows_q8(uint64_t x, uint32_t rows, uint32_t k, uint32_t ldx, uint64_t scales, uint64_t sums,
+                         uint64_t totals, uint64_t qs) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (k == 0 || k % 32u != 0 || ldx < k) return TMH_ERROR_SHAPE;
+    if (rows == 0) return TMH_SUCCESS;
+    if (!x || !scales || !sums || !totals || !qs) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)rows * k > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, (float*)scales, (float*)sums, (int32_t*)totals,
+                                        (int8_t*)qs, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
+namespace {
+
+int check_product(uint32_t kind, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
+    if (kind > 2u) return TMH_ERROR_DTYPE;
+    if (k == 0 || k % 32u != 0) return TMH_ERROR_SHAPE;
+    if (mode > TMH_MODE_MATRIX) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)rows * n > 0x7fffffffull || (uint64_t)rows * k > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    return TMH_SUCCESS;
+}
+
+}  // namespace
+
+int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
+                     uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if ((err = check_product(kind, rows, n, k, mode)) != TMH_SUCCESS) return err;
+    if (ldx < k) return TMH_ERROR_SHAPE;
+    if (rows == 0 || n == 0) return TMH_SUCCESS;
+    if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
+    std::lock_guard<std::mutex> guard(d->launch);
+    if ((err = ensure_scratch(*d, scratch_need(rows, k))) != TMH_SUCCESS) return err;
+    float *scales, *sums;
+    int32_t* totals;
+    int8_t* qs;
+    tmh::Activations act = carve(*d, rows, k, &scales, &sums, &totals, &qs);
+    hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, scales, sums, totals, qs, d->stream);
+    if (e == hipSuccess)
+        e = tmh::launch_block_matmul(kind, mode, (const uint8_t*)(w + w_byte_offset), act, (float*)dst,
+                                     (const float*)bias, rows, n, k, d->compute_units, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
+int tmh_block_matmul_quantised(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t scales, uint64_t sums,
+                               uint64_t totals, uint64_t qs, uint64_t dst, uint64_t bias, uint32_t rows, uint32_t n,
+                               uint32_t k, uint32_t mode) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if ((err = check_product(kind, rows, n, k, mode)) != TMH_SUCCESS) return err;
+    if (rows == 0 || n == 0) return TMH_SUCCESS;
+    if (!w || !scales || !sums || !totals || !qs || !dst) return TMH_ERROR_INVALID_VALUE;
+    if (qs % 16u != 0 || scales % 8u != 0 || sums % 8u != 0 || totals % 8u != 0) return TMH_ERROR_INVALID_VALUE;
+    tmh::Activations act{(const float*)scales, (const float*)sums, (const int32_t*)totals, (const int8_t*)qs};
+    hipError_t e = tmh::launch_block_matmul(kind, mode, (const uint8_t*)(w + w_byte_offset), act, (float*)dst,
+                                            (const float*)bias, rows, n, k, d->compute_units, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
+int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset, int32_t table_rows, uint32_t width,
+                      uint64_t ids, uint32_t count, uint64_t dst) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (kind > 2u) return TMH_ERROR_DTYPE;
+    if (width == 0 || width % 32u != 0 || table_rows < 0) return TMH_ERROR_SHAPE;
+    if ((uint64_t)count * width > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    if (count == 0) return TMH_SUCCESS;
+    if (!table || !ids || !dst) return TMH_ERROR_INVALID_VALUE;
+    d->errors_pending.store(true);
+    hipError_t e = tmh::launch_gather(kind, (const uint8_t*)(table + table_byte_offset), table_rows, width,
+                                      (const int32_t*)ids, count, (float*)dst, d->errors, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
+}  // extern "C"

@@ -1,0 +1,362 @@
+"""Host binding of libtensomite_hip.so: a `HIP` device with the reference's
+device API (src/tensomite/device.cr:6-68) for the quantised-product path.
+
+The reference's host language is Crystal, whose toolchain is absent here; this
+module is the same binding a Crystal `lib LibTensomiteHIP` would be (the
+Crystal stub is in INTEGRATION.md), written with ctypes so tests and bench.py
+drive the C ABI directly. It loads only the in-tree library and raises when
+it is missing: there is no CPU fallback.
+
+    dev = HIPDevice()
+    w = dev.alloc(nbytes); dev.upload(w, weight_bytes)       # Device#alloc/#upload
+    y = dev.block_matmul(Q4_0, w, x, rows=1, n=N, k=K)       # Op::BlockMatMul
+    dev.sync()                                                # Device#sync
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libtensomite_hip.so")
+
+Q8_0, Q4_0, Q4_1 = 0, 1, 2
+KINDS = {"Q8_0": Q8_0, "Q4_0": Q4_0, "Q4_1": Q4_1}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
+
+# BlockMatMulMode, quant.cr:5-28 (MATRIX is this device's own).
+MODES = {"auto": 0, "thread": 1, "lanes": 2, "unordered": 3, "loads": 4, "stream": 5,
+         "stream_activations": 6, "matrix": 7}
+
+SUCCESS = 0
+ERROR_INVALID_VALUE = 1000
+ERROR_SHAPE = 1001
+ERROR_DTYPE = 1002
+ERROR_NO_KERNELS = 1003
+ERROR_OUT_OF_MEMORY = 1004
+ERROR_EXECUTION = 1005
+ERROR_NO_DEVICE = 1006
+
+
+class Error(Exception):
+    """Base of the errors below (errors.cr:1-16)."""
+
+
+class DeviceError(Error):
+    """A failed runtime call: "call: NAME (text)", as CUDA.check raises (cuda.cr:1069-1075)."""
+
+
+class ShapeError(Error):
+    pass
+
+
+class DTypeError(Error):
+    pass
+
+
+class ExecutionError(Error):
+    """A kernel found an index out of range, reported at sync (cuda.cr:972-983)."""
+
+
+class NoKernels(DeviceError):
+    """The library's kernels are unavailable: the caller's host kernel must run."""
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("memory", ctypes.c_uint64),
+                ("compute_units", ctypes.c_int32), ("clock_khz", ctypes.c_int32),
+                ("memory_clock_khz", ctypes.c_int32), ("memory_bus_width", ctypes.c_int32),
+                ("l2_bytes", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32)]
+
+
+class Counters(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int64) for name in
+                ("uploads", "downloads", "gpu_ops", "device_bytes", "pool_held", "pool_limit", "pool_hits",
+                 "pool_misses", "frees")]
+
+
+# Every symbol include/tensomite_hip.h declares, with (restype, argtypes).
+U32, I32, U64, I64 = ctypes.c_uint32, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int64
+VP, INT = ctypes.c_void_p, ctypes.c_int
+SIGNATURES = {
+    "tmh_init": (INT, [ctypes.POINTER(I32)]),
+    "tmh_device_info_get": (INT, [I32, ctypes.POINTER(DeviceInfo)]),
+    "tmh_set_device": (INT, [I32]),
+    "tmh_get_device": (INT, [ctypes.POINTER(I32)]),
+    "tmh_malloc": (INT, [ctypes.POINTER(U64), U64]),
+    "tmh_free": (INT, [U64]),
+    "tmh_free_any_thread": (INT, [U64]),
+    "tmh_upload": (INT, [U64, VP, U64]),
+    "tmh_upload_async": (INT, [U64, VP, U64]),
+    "tmh_download": (INT, [VP, U64, U64]),
+    "tmh_copy": (INT, [U64, U64, U64]),
+    "tmh_synchronize": (INT, []),
+    "tmh_alloc": (INT, [ctypes.POINTER(U64), U64]),
+    "tmh_retire": (INT, [U64, U64]),
+    "tmh_sync": (INT, []),
+    "tmh_pool_set_limit": (INT, [I64]),
+    "tmh_counters_get": (INT, [ctypes.POINTER(Counters)]),
+    "tmh_error_name": (ctypes.c_char_p, [INT]),
+    "tmh_error_string": (ctypes.c_char_p, [INT]),
+    "tmh_error_report": (INT, [ctypes.POINTER(I32)]),
+    "tmh_debug_fail_allocations": (INT, [I32]),
+    "tmh_debug_disable_kernels": (INT, [I32]),
+    "tmh_event_create": (INT, [ctypes.POINTER(U64)]),
+    "tmh_event_record": (INT, [U64]),
+    "tmh_event_elapsed_ms": (INT, [U64, U64, ctypes.POINTER(ctypes.c_float)]),
+    "tmh_event_destroy": (INT, [U64]),
+    "tmh_quantize_rows_q8": (INT, [U64, U32, U32, U32, U64, U64, U64, U64]),
+    "tmh_block_matmul": (INT, [U32, U64, U64, U64, U32, U64, U64, U32, U32, U32, U32]),
+    "tmh_block_matmul_quantised": (INT, [U32, U64, U64, U64, U64, U64, U64, U64, U64, U32, U32, U32, U32]),
+    "tmh_gather_blocks": (INT, [U32, U64, U64, I32, U32, U64, U32, U64]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+
+def library() -> ctypes.CDLL:
+    """Loads the in-tree libtensomite_hip.so; raises when it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIBRARY):
+                raise DeviceError(f"{LIBRARY} is missing: run __graft_entry__.build() (hipcc, gfx950)")
+            so = ctypes.CDLL(LIBRARY)
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(so, name)
+                fn.restype, fn.argtypes = restype, argtypes
+            _lib = so
+    return _lib
+
+
+def error_text(code: int) -> str:
+    lib = library()
+    return f"{lib.tmh_error_name(code).decode()} ({lib.tmh_error_string(code).decode()})"
+
+
+def check(call: str, code: int) -> None:
+    """Raises the reference's error for a failed call (CUDA.check, cuda.cr:1069-1075)."""
+    if code == SUCCESS:
+        return
+    text = f"{call}: {error_text(code)}"
+    if code == ERROR_SHAPE:
+        raise ShapeError(text)
+    if code == ERROR_DTYPE:
+        raise DTypeError(text)
+    if code == ERROR_NO_KERNELS:
+        raise NoKernels(text)
+    raise DeviceError(text)
+
+
+def kind_of(kind) -> int:
+    if isinstance(kind, str):
+        if kind not in KINDS:
+            raise DTypeError(f"{kind} is not a block format")
+        return KINDS[kind]
+    return int(kind)
+
+
+def row_bytes(kind, k: int) -> int:
+    """DType#bytes_for of one row (dtype.cr:221-244)."""
+    if k % 32:
+        raise ShapeError(f"rows of {k} do not split into blocks of 32")
+    return k // 32 * BLOCK_BYTES[kind_of(kind)]
+
+
+def device_count() -> int:
+    n = I32(0)
+    check("tmh_init", library().tmh_init(ctypes.byref(n)))
+    return n.value
+
+
+class Buffer:
+    """Device memory owned by a device (device.cr:6-33): given back to the
+    device's pool when released or collected."""
+
+    def __init__(self, device: "HIPDevice", pointer: int, bytesize: int):
+        self.device = device
+        self.pointer = pointer
+        self.bytesize = bytesize
+        self._released = False
+
+    @property
+    def released(self) -> bool:
+        return self._released
+
+    def release(self) -> None:
+        if self._released:
+            return
+        self._released = True
+        self.device._retire(self)
+
+    def __del__(self):
+        if not getattr(self, "_released", True):
+            try:
+                self.device._retire(self)
+            except Exception:
+                pass
+
+
+class HIPDevice:
+    """An MI355X through libtensomite_hip.so: `#map` returns None, data moves
+    through `#upload`/`#download`, and BlockMatMul and block Gather run on the
+    GPU, queued in order on one stream (the pattern of `CUDA < HostDevice`,
+    cuda.cr:92-415)."""
+
+    def __init__(self, index: int = 0, block_mode: str = "auto"):
+        self.lib = library()
+        count = device_count()
+        if index >= count:
+            raise DeviceError(f"tmh_init: no GPU {index} ({count} found)")
+        self.index = index
+        self.block_mode = block_mode
+        self.bind()
+        info = DeviceInfo()
+        check("tmh_device_info_get", self.lib.tmh_device_info_get(index, ctypes.byref(info)))
+        self.name = info.name.decode()
+        self.arch = info.arch.decode()
+        self.memory = int(info.memory)
+        self.compute_units = int(info.compute_units)
+
+    def bind(self) -> None:
+        """Makes this device current on the calling thread (Context#bind, cuda.cr:1118-1125)."""
+        check("tmh_set_device", self.lib.tmh_set_device(self.index))
+
+    # -- the Device contract (device.cr:39-68)
+    def alloc(self, bytesize: int) -> Buffer:
+        ptr = U64(0)
+        check("tmh_alloc", self.lib.tmh_alloc(ctypes.byref(ptr), int(bytesize)))
+        return Buffer(self, ptr.value, int(bytesize))
+
+    def upload(self, buffer: Buffer, data, asynchronous: bool = False) -> None:
+        arr = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray))
+                                   else data)
+        nbytes = arr.nbytes
+        if nbytes > buffer.bytesize:
+            raise DeviceError(f"upload: {nbytes} bytes into a buffer of {buffer.bytesize}")
+        fn = self.lib.tmh_upload_async if asynchronous else self.lib.tmh_upload
+        check("tmh_upload_async" if asynchronous else "tmh_upload", fn(buffer.pointer, arr.ctypes.data, nbytes))
+
+    def download(self, buffer: Buffer, out: np.ndarray) -> np.ndarray:
+        if not out.flags["C_CONTIGUOUS"]:
+            raise DeviceError("download needs contiguous host memory")
+        if out.nbytes > buffer.bytesize:
+            raise DeviceError(f"download: {out.nbytes} bytes from a buffer of {buffer.bytesize}")
+        check("tmh_download", self.lib.tmh_download(out.ctypes.data, buffer.pointer, out.nbytes))
+        return out
+
+    def map(self, buffer: Buffer):
+        """Device memory is not host-visible (cuda.cr:355-358)."""
+        return None
+
+    def sync(self) -> None:
+        """Waits, recycles retired memory, and raises ExecutionError for an index
+        a kernel reported out of range (CUDA#sync, cuda.cr:419-428)."""
+        code = self.lib.tmh_sync()
+        if code == ERROR_EXECUTION:
+            report = (I32 * 3)()
+            check("tmh_error_report", self.lib.tmh_error_report(report))
+            raise ExecutionError(f"index {report[1]} out of range for {report[2]} rows")
+        check("tmh_sync", code)
+
+    def shape_invariant(self) -> bool:
+        """Each output depends only on its own row and column (quant.cr:120-121)."""
+        return True
+
+    def fuses_attention(self) -> bool:
+        return False
+
+    # -- helpers
+    def from_array(self, values: np.ndarray, asynchronous: bool = False) -> Buffer:
+        arr = np.ascontiguousarray(values)
+        buf = self.alloc(max(arr.nbytes, 1))
+        if arr.nbytes:
+            self.upload(buf, arr, asynchronous)
+        return buf
+
+    def to_array(self, buffer: Buffer, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        return self.download(buffer, out)
+
+    def copy(self, dst: Buffer, src: Buffer, bytesize: int, dst_offset: int = 0, src_offset: int = 0) -> None:
+        check("tmh_copy", self.lib.tmh_copy(dst.pointer + dst_offset, src.pointer + src_offset, bytesize))
+
+    def counters(self) -> dict:
+        c = Counters()
+        check("tmh_counters_get", self.lib.tmh_counters_get(ctypes.byref(c)))
+        return {name: getattr(c, name) for name, _ in Counters._fields_}
+
+    def set_pool_limit(self, bytes_: int) -> None:
+        check("tmh_pool_set_limit", self.lib.tmh_pool_set_limit(int(bytes_)))
+
+    def _retire(self, buffer: Buffer) -> None:
+        self.lib.tmh_retire(buffer.pointer, buffer.bytesize)
+
+    # -- the quantised path
+    def quantize_rows(self, x: Buffer, rows: int, k: int, ldx: Optional[int] = None):
+        """quantize_rows_q8 into new buffers: (scales, sums, totals, qs)."""
+        nb = k // 32
+        stride = k if ldx is None else ldx
+        if k % 32 or stride < k or (rows and ((rows - 1) * stride + k) * 4 > x.bytesize):
+            raise ShapeError(f"{x.bytesize} bytes do not hold {rows} rows of {k} values {stride} apart")
+        scales, sums, totals = (self.alloc(max(4 * rows * nb, 4)) for _ in range(3))
+        qs = self.alloc(max(rows * k, 4))
+        check("tmh_quantize_rows_q8", self.lib.tmh_quantize_rows_q8(
+            x.pointer, rows, k, k if ldx is None else ldx, scales.pointer, sums.pointer, totals.pointer,
+            qs.pointer))
+        return scales, sums, totals, qs
+
+    def block_matmul(self, kind, w: Buffer, x: Buffer, rows: int, n: int, k: int, dst: Optional[Buffer] = None,
+                     bias: Optional[Buffer] = None, w_row: int = 0, ldx: Optional[int] = None,
+                     mode: Optional[str] = None) -> Buffer:
+        """Op::BlockMatMul: dst[rows, n] = x[rows, k] · w[w_row:w_row+n]ᵀ (+ bias), queued."""
+        kk = kind_of(kind)
+        rb = row_bytes(kk, k)
+        if (w_row + n) * rb > w.bytesize:
+            raise ShapeError(f"{w.bytesize} bytes do not hold rows {w_row}...{w_row + n} of {k} values")
+        stride = k if ldx is None else ldx
+        if stride < k or (rows and ((rows - 1) * stride + k) * 4 > x.bytesize):
+            raise ShapeError(f"{x.bytesize} bytes do not hold {rows} rows of {k} values {stride} apart")
+        if dst is None:
+            dst = self.alloc(max(4 * rows * n, 4))
+        if rows * n * 4 > dst.bytesize or (bias is not None and n * 4 > bias.bytesize):
+            raise ShapeError(f"output or bias too small for [{rows}, {n}]")
+        m = MODES[mode or self.block_mode]
+        check("tmh_block_matmul", self.lib.tmh_block_matmul(
+            kk, w.pointer, w_row * rb, x.pointer, k if ldx is None else ldx, dst.pointer,
+            bias.pointer if bias is not None else 0, rows, n, k, m))
+        return dst
+
+    def gather(self, kind, table: Buffer, table_rows: int, width: int, ids: Buffer, count: int,
+               dst: Optional[Buffer] = None, first_row: int = 0) -> Buffer:
+        """Op::Gather on a block table: rows ids of table[first_row:], dequantised to F32."""
+        kk = kind_of(kind)
+        rb = row_bytes(kk, width)
+        if (first_row + table_rows) * rb > table.bytesize or count * 4 > ids.bytesize:
+            raise ShapeError(f"table of {table.bytesize} bytes or ids of {ids.bytesize} too small")
+        if dst is None:
+            dst = self.alloc(max(4 * count * width, 4))
+        if count * width * 4 > dst.bytesize:
+            raise ShapeError("output too small")
+        check("tmh_gather_blocks", self.lib.tmh_gather_blocks(
+            kk, table.pointer, first_row * rb, table_rows, width, ids.pointer, count, dst.pointer))
+        return dst
+
+    # -- timing on the library's stream
+    def event(self) -> int:
+        ev = U64(0)
+        check("tmh_event_create", self.lib.tmh_event_create(ctypes.byref(ev)))
+        return ev.value
+
+    def record(self, event: int) -> None:
+        check("tmh_event_record", self.lib.tmh_event_record(event))
+
+    def elapsed_ms(self, start: int, stop: int) -> float:
+        ms = ctypes.c_float(0)
+        check("tmh_event_elapsed_ms", self.lib.tmh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+        return ms.value

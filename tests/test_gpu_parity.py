@@ -1,0 +1,312 @@
+"""HIP path against the oracle, bit for bit (tests/ only; runs on an MI355X).
+
+Follows the reference's own checks for the path: spec/quant_spec.cr and
+spec/block_matmul_spec.cr (device equals CPU bit for bit with a bias; every
+mode; groups straddling rows; views; row slices; row alone == in batch;
+gather), at the BASELINE configs' full shapes where the oracle's fast path
+finishes in seconds, and through size-independent properties otherwise.
+"""
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+import tensomite_hip as th
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = ["Q8_0", "Q4_0", "Q4_1"]
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return th.HIPDevice(0)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def weights(fmt, n, k, seed, scale=0.02):
+    values = np.random.default_rng(seed).normal(0.0, scale, n * k).astype(np.float32)
+    return oracle.quantize(fmt, values)
+
+
+def acts(rows, k, seed, scale=1.0):
+    return np.random.default_rng(seed).normal(0.0, scale, rows * k).astype(np.float32)
+
+
+def run_product(dev, fmt, wq, x, rows, n, k, mode="auto", bias=None, w_row=0, ldx=None):
+    wbuf = dev.from_array(wq)
+    xbuf = dev.from_array(x)
+    bbuf = dev.from_array(bias) if bias is not None else None
+    out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k, bias=bbuf, w_row=w_row, ldx=ldx, mode=mode)
+    got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
+    dev.sync()
+    return got
+
+
+def test_device_is_gfx950(dev):
+    say("device", dev.name, dev.arch, dev.compute_units)
+    assert dev.arch.startswith("gfx950")
+
+
+@pytest.mark.parametrize("k", [32, 64, 96, 576, 768, 1280, 2048, 8192])
+def test_quantised_activations_bit_exact(dev, k):
+    # quantize_rows_q8 == quantize_activations (quant.cr:424-442), bytes and
+    # scales, for rows with zero blocks, the spike and the half-integer row.
+    say("quantise k", k)
+    rows = 5
+    x = acts(rows, k, 100 + k)
+    x[k:k + 32] = 0
+    x[2 * k:2 * k + 32] = [127.0 if j == 0 else j - 15.5 for j in range(32)]
+    x[3 * k + 3] = 50.0
+    x[4 * k:5 * k] *= 1e-3
+    xbuf = dev.from_array(x)
+    scales, sums, totals, qs = dev.quantize_rows(xbuf, rows, k)
+    nb = k // 32
+    g_scales = dev.to_array(scales, np.float32, rows * nb)
+    g_sums = dev.to_array(sums, np.float32, rows * nb)
+    g_totals = dev.to_array(totals, np.int32, rows * nb)
+    g_qs = dev.to_array(qs, np.int8, rows * k)
+    for r in range(rows):
+        s, m, q = oracle.quantize_activations(x[r * k:(r + 1) * k], with_sums=True)
+        assert np.array_equal(g_qs[r * k:(r + 1) * k], q), r
+        assert np.array_equal(bits(g_scales[r * nb:(r + 1) * nb]), bits(s)), r
+        assert np.array_equal(bits(g_sums[r * nb:(r + 1) * nb]), bits(m)), r
+        assert np.array_equal(g_totals[r * nb:(r + 1) * nb], q.reshape(nb, 32).astype(np.int32).sum(1)), r
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("mode", ["auto", "thread", "lanes", "unordered"])
+def test_matches_cpu_with_bias_every_mode(dev, fmt, mode):
+    # block_matmul_spec.cr:102-116 (rows 5, n 7, k 96: odd block count) and
+    # 142-158 (3 x 37 over 1280-long rows: more blocks than lanes).
+    rng = np.random.default_rng(1)
+    for rows, n, k in ((5, 7, 96), (3, 37, 1280), (1, 37, 1280)):
+        say("product", fmt, mode, rows, n, k)
+        x = rng.uniform(-1, 1, rows * k).astype(np.float32)
+        w = rng.uniform(-1, 1, n * k).astype(np.float32)
+        bias = rng.uniform(-1, 1, n).astype(np.float32)
+        wq = oracle.quantize(fmt, w)
+        want = oracle.add_bias(oracle.matmul_reference(fmt, x, wq, rows, n, k), bias)
+        got = run_product(dev, fmt, wq, x, rows, n, k, mode=mode, bias=bias)
+        assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_activation_row_groups(dev, fmt):
+    # Every activation row count 1..17 (groups of 16, 8, 4, 2, 1), and each
+    # row alone equals the row in the batch (block_matmul_spec.cr:118-123).
+    n, k = 300, 576
+    wq = weights(fmt, n, k, 7)
+    x = acts(17, k, 8)
+    want = oracle.matmul(fmt, x, wq, 17, n, k)
+    for rows in list(range(1, 18)):
+        say("rows", fmt, rows)
+        got = run_product(dev, fmt, wq, x[:rows * k], rows, n, k)
+        assert np.array_equal(bits(got), bits(want[:rows])), rows
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_views_and_row_slices(dev, fmt):
+    # block_matmul_spec.cr:197-205: activation rows read through a view
+    # (rows ldx apart) and a weight sliced by rows (a merged projection).
+    n, k, rows = 50, 1024, 3
+    wq = weights(fmt, n, k, 9)
+    x = acts(rows, k, 10)
+    full = oracle.matmul_reference(fmt, x, wq, rows, n, k)
+    say("slice", fmt)
+    got = run_product(dev, fmt, wq, x, rows, 20, k, w_row=17)
+    assert np.array_equal(bits(got), bits(full[:, 17:37]))
+    ldx = k + 96
+    strided = np.zeros(rows * ldx, np.float32)
+    for r in range(rows):
+        strided[r * ldx:r * ldx + k] = x[r * k:(r + 1) * k]
+    say("view", fmt)
+    wbuf, xbuf = dev.from_array(wq), dev.from_array(strided)
+    out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k, ldx=ldx)
+    got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
+    assert np.array_equal(bits(got), bits(full))
+
+
+CONFIG_SHAPES = {
+    # config 1: GPT-2 c_attn, Q8_0
+    "c_attn": ("Q8_0", 2304, 768, 1),
+    # config 2: SmolLM2-135M Q4_0 set
+    "qkv_135m": ("Q4_0", 960, 576, 1),
+    "o_135m": ("Q4_0", 576, 576, 1),
+    "gate_up_135m": ("Q4_0", 3072, 576, 1),
+    "down_135m": ("Q4_0", 576, 1536, 1),
+    "head_135m": ("Q4_0", 49152, 576, 1),
+    # config 3: Q4_1 batched decode
+    "q41_up_b16": ("Q4_1", 8192, 2048, 16),
+    "q41_down_b5": ("Q4_1", 2048, 8192, 5),
+    # config 5: 1.7B Q4_0 products at batch 1 and 8
+    "qkv_1p7b": ("Q4_0", 6144, 2048, 1),
+    "gate_up_1p7b_b8": ("Q4_0", 16384, 2048, 8),
+    "down_1p7b": ("Q4_0", 2048, 8192, 1),
+    "head_1p7b": ("Q4_0", 49152, 2048, 1),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CONFIG_SHAPES))
+def test_config_shapes_bit_exact(dev, name):
+    fmt, n, k, rows = CONFIG_SHAPES[name]
+    say("config", name, fmt, n, k, rows)
+    wq = weights(fmt, n, k, zlib.crc32(name.encode()))
+    x = acts(rows, k, 3)
+    want = oracle.matmul(fmt, x, wq, rows, n, k)
+    got = run_product(dev, fmt, wq, x, rows, n, k)
+    assert np.array_equal(bits(got), bits(want))
+    # run to run: the same bits again
+    again = run_product(dev, fmt, wq, x, rows, n, k)
+    assert np.array_equal(bits(again), bits(got))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_special_rows(dev, fmt):
+    # quant_spec.cr:30-48 on the device: zero first block, a spike of 50, a
+    # zero activation block, the [127, j - 15.5] row, at {3, 5, 1280} and
+    # {2, 9, 4096}.
+    rng = np.random.default_rng(11)
+    for count, n, k in ((1, 37, 64), (3, 5, 1280), (2, 9, 4096)):
+        say("special", fmt, count, n, k)
+        values = rng.uniform(-2.0, 2.0, n * k).astype(np.float32)
+        values[:32] = 0
+        values[32 * 3] = 50
+        x = rng.uniform(-3.0, 3.0, count * k).astype(np.float32)
+        if count > 1:
+            x[k:k + 32] = 0
+        if count > 2:
+            x[2 * k:2 * k + 32] = [127.0 if j == 0 else j - 15.5 for j in range(32)]
+        wq = oracle.quantize(fmt, values)
+        want = oracle.matmul_reference(fmt, x, wq, count, n, k)
+        for mode in ("auto", "thread"):
+            got = run_product(dev, fmt, wq, x, count, n, k, mode=mode)
+            assert np.array_equal(bits(got), bits(want)), mode
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_gather(dev, fmt):
+    # block_matmul_spec.cr:221-236: rows [4, 0, 4] of a 6 x 64 table, and a
+    # row slice of it; the embedding shape of config 5.
+    rng = np.random.default_rng(4)
+    table = rng.uniform(-1, 1, 6 * 64).astype(np.float32)
+    q = oracle.quantize(fmt, table)
+    tbuf = dev.from_array(q)
+    ids = dev.from_array(np.array([4, 0, 4], np.int32))
+    say("gather", fmt)
+    out = dev.gather(fmt, tbuf, 6, 64, ids, 3)
+    got = dev.to_array(out, np.float32, 3 * 64).reshape(3, 64)
+    dev.sync()
+    assert np.array_equal(bits(got), bits(oracle.gather(fmt, q, 6, 64, [4, 0, 4])))
+    ids2 = dev.from_array(np.array([2], np.int32))
+    out = dev.gather(fmt, tbuf, 4, 64, ids2, 1, first_row=2)
+    got = dev.to_array(out, np.float32, 64)
+    dev.sync()
+    assert np.array_equal(bits(got), bits(oracle.gather(fmt, q, 6, 64, [4])[0]))
+    emb = weights(fmt, 49152, 2048, 21)
+    ebuf = dev.from_array(emb)
+    want_ids = np.array([0, 49151, 12345, 7, 7, 30000, 1, 2], np.int32)
+    out = dev.gather(fmt, ebuf, 49152, 2048, dev.from_array(want_ids), 8)
+    got = dev.to_array(out, np.float32, 8 * 2048).reshape(8, 2048)
+    dev.sync()
+    assert np.array_equal(bits(got), bits(oracle.gather(fmt, emb, 49152, 2048, want_ids)))
+
+
+def test_gather_out_of_range_raises_at_sync(dev):
+    # host.cr:652-654 raises ExecutionError; cuda.cr:972-983 at sync.
+    q = oracle.quantize("Q4_0", np.ones(4 * 64, np.float32))
+    tbuf = dev.from_array(q)
+    for bad in (4, -1):
+        say("gather bad id", bad)
+        ids = dev.from_array(np.array([1, bad, 0], np.int32))
+        out = dev.gather("Q4_0", tbuf, 4, 64, ids, 3)
+        with pytest.raises(th.ExecutionError, match=f"index {bad} out of range for 4 rows"):
+            dev.sync()
+        got = dev.to_array(out, np.float32, 3 * 64)
+        assert np.all(got[64:128] == 0)
+    dev.sync()  # the report was cleared
+
+
+def test_every_half_widens_exactly(dev):
+    # F16#to_f32 (f16.cr:44-57) on the device, for all 65,536 halves: a Q8_0
+    # table whose block b has d = half b and values (1, 0, ..., 0) gathers to
+    # d itself.
+    blocks = np.zeros((65536, 34), np.uint8)
+    h = np.arange(65536, dtype=np.uint32)
+    blocks[:, 0] = h & 0xFF
+    blocks[:, 1] = h >> 8
+    blocks[:, 2] = 1
+    table = blocks.reshape(-1)
+    rows, width = 65536 // 32, 32 * 32
+    tbuf = dev.from_array(table)
+    ids = dev.from_array(np.arange(rows, dtype=np.int32))
+    say("halves")
+    out = dev.gather("Q8_0", tbuf, rows, width, ids, rows)
+    got = dev.to_array(out, np.float32, rows * width).reshape(65536, 32)[:, 0]
+    dev.sync()
+    want = oracle.f16_values_many(h.astype(np.uint16))
+    finite = ~np.isnan(want)
+    assert np.array_equal(bits(got[finite]), bits(want[finite]))
+    assert np.all(np.isnan(got[~finite]))
+
+
+def test_buffer_pool_reuse_and_counters(dev):
+    # CUDA#alloc from the pool after retire + sync (cuda.cr:339-353, 439-454).
+    say("pool")
+    before = dev.counters()
+    b = dev.alloc(123457)
+    b.release()
+    dev.sync()
+    c = dev.alloc(123457)
+    after = dev.counters()
+    assert after["pool_hits"] >= before["pool_hits"] + 1
+    c.release()
+    assert after["pool_limit"] >= 1 << 30
+
+
+def test_async_upload_round_trip(dev):
+    # tmh_upload_async: the caller's memory may change right after the call.
+    rng = np.random.default_rng(5)
+    data = rng.integers(0, 256, (40 << 20) + 13, dtype=np.uint8)
+    buf = dev.alloc(data.nbytes)
+    say("async upload")
+    scratch = data.copy()
+    dev.upload(buf, scratch, asynchronous=True)
+    scratch[:] = 0  # reused at once
+    got = dev.to_array(buf, np.uint8, data.nbytes)
+    assert np.array_equal(got, data)
+
+
+def test_errors_are_typed(dev):
+    say("errors")
+    w = dev.from_array(np.zeros(34 * 4, np.uint8))
+    x = dev.from_array(np.zeros(64, np.float32))
+    with pytest.raises(th.ShapeError):
+        th.check("tmh_block_matmul", dev.lib.tmh_block_matmul(0, w.pointer, 0, x.pointer, 48, x.pointer, 0, 1, 2,
+                                                               48, 0))
+    with pytest.raises(th.DTypeError):
+        th.check("tmh_block_matmul", dev.lib.tmh_block_matmul(5, w.pointer, 0, x.pointer, 64, x.pointer, 0, 1, 2,
+                                                               64, 0))
+    dev.lib.tmh_debug_fail_allocations(1)
+    try:
+        with pytest.raises(th.DeviceError, match="OUT_OF_MEMORY"):
+            dev.alloc(77777777)
+    finally:
+        dev.lib.tmh_debug_fail_allocations(0)
+    dev.lib.tmh_debug_disable_kernels(1)
+    try:
+        with pytest.raises(th.NoKernels):
+            dev.block_matmul("Q8_0", w, x, 1, 2, 64)
+    finally:
+        dev.lib.tmh_debug_disable_kernels(0)
+    dev.sync()
