@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""bench.py -- Q4_0 decode matvec throughput on one MI355X.
+
+Workload ("config 2"): the SmolLM2-135M Llama
+shape's Q4_0 matvec set at batch 1 -- per token 30 layers of merged qkv
+[960, 576], o [576, 576], merged gate_up [3072, 576], down [576, 1536], plus
+the tied head [49152, 576]: 121 products, 75,644,928 weight bytes. Weights
+~N(0, 0.02) quantised to Q4_0 (host quantiser), activations ~N(0, 1), all
+resident in HBM before timing. One step = one token's 121 products as ONE
+launch (tmh_plan_run). Steps rotate through enough distinct copies of the
+weights (>= 512 MB) that the 256 MB Infinity Cache cannot serve them.
+
+value = algorithmic bytes per step (weights + f32 x + f32 y) / time per
+step, in GB/s; the roofline object prices the launch against 8 TB/s.
+The CPU baseline times the oracle's restatement of tensomite's CPU path
+(Quant.matmul, all host cores) on the same bytes, and checks the GPU's
+output bits against it.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "tensomite.cr_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+# config 2: (name, n, k) per layer, then the head
+LAYER = [("qkv", 960, 576), ("o", 576, 576), ("gate_up", 3072, 576), ("down", 576, 1536)]
+LAYERS = 30
+HEAD = ("head", 49152, 576)
+
+
+def products_135m():
+    out = []
+    for layer in range(LAYERS):
+        for name, n, k in LAYER:
+            out.append((f"{name}.{layer}", n, k))
+    out.append(HEAD)
+    return out
+
+
+def q4_0_bytes(n, k):
+    return n * (k // 32) * 18
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by a copy kernel's reading), if the committed summary has them."""
+    path = os.path.join(ROOT, "profiles", "traffic_q4_0_set_135m.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(weights, xs, prods, gpu_out, seconds):
+    """The oracle's Quant.matmul restatement on the host's cores, timed over
+    whole tokens for about `seconds`; also checks the GPU's bits."""
+    from oracle import oracle
+
+    variant = oracle.best_variant()
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    oracle.set_threads(cores, variant)
+    # parity: every product's output bits
+    mismatched = 0
+    for i, (name, n, k) in enumerate(prods):
+        want = oracle.matmul("Q4_0", xs[i], weights[i], 1, n, k, variant)[0]
+        if not np.array_equal(want.view(np.uint32), gpu_out[i].view(np.uint32)):
+            mismatched += 1
+    tokens = 0
+    start = time.perf_counter()
+    while True:
+        for i, (name, n, k) in enumerate(prods):
+            oracle.matmul("Q4_0", xs[i], weights[i], 1, n, k, variant)
+        tokens += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds:
+            break
+    algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
+    return {
+        "value": algorithmic * tokens / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{tokens} tokens of the config-2 set (121 products each) in {elapsed:.1f} s; "
+                  f"oracle Quant.matmul restatement, {variant} build, spin pool of {cores} threads",
+        "ms_per_token": elapsed / tokens * 1e3,
+        "parity_mismatched_products": mismatched,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
+              "how it would shard is described in DESIGN.md", file=sys.stderr)
+        sys.exit(1)
+
+    import quant_host
+    import tensomite_hip as th
+
+    dev = th.HIPDevice(0)
+    log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
+    prods = products_135m()
+    weight_bytes = sum(q4_0_bytes(n, k) for _, n, k in prods)
+    algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
+    copies = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
+
+    # Host weights (one copy), quantised by the package's host quantiser.
+    t0 = time.perf_counter()
+    rng = np.random.default_rng(0x5EED0002)
+    weights, xs = [], []
+    for i, (name, n, k) in enumerate(prods):
+        weights.append(quant_host.synthetic_weights("Q4_0", n, k, seed=0x5EED0002 + i))
+        xs.append(rng.normal(0.0, 1.0, k).astype(np.float32))
+    log(f"weights quantised in {time.perf_counter() - t0:.1f} s; {weight_bytes / 1e6:.1f} MB per token, "
+        f"{copies} copies = {copies * weight_bytes / 1e6:.0f} MB")
+
+    # Device: one packed weight buffer per copy, activations, outputs.
+    offsets, off = [], 0
+    for w in weights:
+        offsets.append(off)
+        off += (w.nbytes + 255) // 256 * 256
+    packed = np.zeros(off, np.uint8)
+    for w, o in zip(weights, offsets):
+        packed[o:o + w.nbytes] = w
+    wbufs = [dev.from_array(packed, asynchronous=True) for _ in range(copies)]
+    xbufs = [dev.from_array(x) for x in xs]
+    ybufs = [dev.alloc(4 * n) for _, n, _ in prods]
+    plans = []
+    for c in range(copies):
+        items = []
+        for i, (name, n, k) in enumerate(prods):
+            items.append((wbufs[c], 0, xbufs[i], ybufs[i], None, n, k))
+        # w_row is in rows; the packed offset is in bytes: pass it through a view
+        plan_items = []
+        for i, (w, _, x, y, b, n, k) in enumerate(items):
+            plan_items.append((_View(w, offsets[i]), 0, x, y, b, n, k))
+        plans.append(dev.plan("Q4_0", plan_items))
+    dev.sync()
+
+    # Warm-up, then the timed region: K launches back to back.
+    for s in range(args.warmup):
+        plans[s % copies].run()
+    dev.sync()
+    ev = [dev.event() for _ in range(args.steps + 1)]
+    t_start = time.perf_counter()
+    dev.record(ev[0])
+    for s in range(args.steps):
+        plans[s % copies].run()
+        dev.record(ev[s + 1])
+    dev.sync()
+    t_end = time.perf_counter()
+    per_launch = [dev.elapsed_ms(ev[s], ev[s + 1]) for s in range(args.steps)]
+    ms_per_step = (t_end - t_start) * 1e3 / args.steps
+    launch_ms = float(np.mean(per_launch))
+    value = algorithmic / (ms_per_step * 1e-3) / 1e9
+    achieved = algorithmic / (launch_ms * 1e-3) / 1e9
+
+    # Outputs of the last step, for the CPU parity check.
+    gpu_out = [dev.to_array(y, np.float32, n) for y, (_, n, _) in zip(ybufs, prods)]
+
+    # Per-product launches (the reference's one launch per product), for comparison.
+    for s in range(3):
+        for i, (name, n, k) in enumerate(prods):
+            dev.lib.tmh_block_matmul(th.Q4_0, wbufs[s % copies].pointer, offsets[i], xbufs[i].pointer, k,
+                                     ybufs[i].pointer, 0, 1, n, k, 0)
+    dev.sync()
+    reps = 20
+    e0, e1 = dev.event(), dev.event()
+    dev.record(e0)
+    for s in range(reps):
+        for i, (name, n, k) in enumerate(prods):
+            dev.lib.tmh_block_matmul(th.Q4_0, wbufs[s % copies].pointer, offsets[i], xbufs[i].pointer, k,
+                                     ybufs[i].pointer, 0, 1, n, k, 0)
+    dev.record(e1)
+    dev.sync()
+    per_product_ms = dev.elapsed_ms(e0, e1) / reps
+
+    result = {
+        "metric": "Q4_0 matvec HBM GB/s (% peak); decode tokens/sec at 1.7B Llama shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot + f32 fold",
+        "data": "synthetic: W ~ N(0,0.02) quantised to Q4_0, x ~ N(0,1); random init, no checkpoint",
+        "config": {
+            "workload": "config 2: SmolLM2-135M Q4_0 matvec set at batch 1 (30 x [qkv 960x576, o 576x576, "
+                        "gate_up 3072x576, down 576x1536] + head 49152x576), one launch per token",
+            "products_per_step": len(prods),
+            "weight_bytes_per_step": weight_bytes,
+            "algorithmic_bytes_per_step": algorithmic,
+            "weight_copies_rotated": copies,
+            "rotated_bytes": copies * weight_bytes,
+        },
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+        "roofline": {
+            "kernel": "tmh::k_matvec_rows<1> (Q4_0, one launch = 121 products)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(),
+            "launch_us_mean": round(launch_ms * 1e3, 2),
+            "launch_us_median": round(float(np.median(per_launch)) * 1e3, 2),
+        },
+        "per_product_launches": {
+            "ms_per_token": round(per_product_ms, 4),
+            "GB_per_s": round(algorithmic / (per_product_ms * 1e-3) / 1e9, 1),
+            "note": "the same 121 products as 121 tmh_block_matmul calls",
+        },
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(weights, xs, prods, gpu_out, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+class _View:
+    """A buffer seen from a byte offset (a product's weights inside the packed buffer)."""
+
+    def __init__(self, buf, offset):
+        self.pointer = buf.pointer + offset
+        self.bytesize = buf.bytesize - offset
+
+
+if __name__ == "__main__":
+    main()

@@ -237,6 +237,34 @@ int tmh_block_matmul_quantised(uint32_t kind, uint64_t w, uint64_t w_byte_offset
 int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset, int32_t table_rows, uint32_t width,
                       uint64_t ids, uint32_t count, uint64_t dst);
 
+/* ------------------------------------------------------------ plans */
+
+/* One product of a plan: Op::BlockMatMul with ONE activation row,
+ * dst[n] = x[k] · w[n, k]ᵀ (+ bias[n]). */
+typedef struct tmh_product {
+    uint64_t w;             /* weight buffer */
+    uint64_t w_byte_offset; /* byte offset of the first row (a row slice) */
+    uint64_t x;             /* f32 [k] */
+    uint64_t dst;           /* f32 [n] */
+    uint64_t bias;          /* f32 [n], or 0 */
+    uint32_t n;
+    uint32_t k;
+} tmh_product;
+
+/* Records `count` independent products of one block kind to run as ONE
+ * kernel launch, each with the bits tmh_block_matmul gives it. The products
+ * must not write what another reads. No counterpart in the reference, which
+ * launches products one by one (cuda.cr:736-756): it is the batched launch
+ * that small decode products need to stream weights at HBM speed rather
+ * than at the launch rate. Rows must hold an even number of blocks and start
+ * 4-byte aligned (TMH_ERROR_SHAPE otherwise). */
+int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, uint64_t* plan);
+
+/* Queues the plan's launch on the device's stream. */
+int tmh_plan_run(uint64_t plan);
+
+int tmh_plan_destroy(uint64_t plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@
 // fused, and with correctly rounded f32 division.
 #include "tmh_internal.h"
 
+#include <stdlib.h>
+
 namespace tmh {
 
 // ------------------------------------------------------------------ halves
@@ -140,7 +142,7 @@ struct Pair;
 template <>
 struct Pair<0> {
     __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
-                                                      int, int, float&, float&, float& c0, float& c1) {
+                                                      int, int, float, float, float& c0, float& c1) {
         int t0 = 0, t1 = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) t0 = dot4(funnel(u[i + 1], u[i], 2), a[i], t0);
@@ -159,7 +161,7 @@ struct Pair<0> {
 template <>
 struct Pair<1> {
     __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
-                                                      int neg8_0, int neg8_1, float&, float&, float& c0,
+                                                      int neg8_0, int neg8_1, float, float, float& c0,
                                                       float& c1) {
         int t0 = neg8_0, t1 = neg8_1;
 #pragma unroll
@@ -187,7 +189,7 @@ struct Pair<1> {
 template <>
 struct Pair<2> {
     __device__ __forceinline__ static void contribute(const uint32_t* u, const uint32_t* a, float sx0, float sx1,
-                                                      int, int, float& mx0, float& mx1, float& c0, float& c1) {
+                                                      int, int, float mx0, float mx1, float& c0, float& c1) {
         int t0 = 0, t1 = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -210,21 +212,46 @@ struct Pair<2> {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Pointers known to be in global memory. Pointers read from a table are
+// generic to the compiler, which then issues flat loads; those count
+// against the LDS wait counter too, so every LDS wait would also drain the
+// weight loads in flight. Casting to the global address space keeps them
+// global loads.
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ gptr<T> global(const T* p) {
+    return (gptr<T>)p;
+}
+
+// Four floats from global memory, one 16-byte load when `vec` (16-byte aligned).
+__device__ __forceinline__ float4 load_f4(const float* p, bool vec) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    if (vec) {
+        const f4 v = *(const __attribute__((address_space(1))) f4*)p;
+        return make_float4(v.x, v.y, v.z, v.w);
+    }
+    const gptr<float> g = global(p);
+    return make_float4(g[0], g[1], g[2], g[3]);
+}
+
 // Loads the PW dwords of a pair at p (dword-aligned).
 template <int KIND>
-__device__ __forceinline__ void load_pair(const uint32_t* __restrict__ p, uint32_t* u) {
+__device__ __forceinline__ void load_pair(const uint32_t* __restrict__ pp, uint32_t* u) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
+    typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+    typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
+    const gptr<uint32_t> p = global(pp);
 #pragma unroll
     for (uint32_t i = 0; i + 4 <= PW; i += 4) {
-        u32x4 v;
-        __builtin_memcpy(&v, p + i, 16);
+        const u32x4a v = *(const __attribute__((address_space(1))) u32x4a*)(p + i);
         u[i] = v.x, u[i + 1] = v.y, u[i + 2] = v.z, u[i + 3] = v.w;
     }
     if constexpr (PW % 4 == 1) {
         u[PW - 1] = p[PW - 1];
     } else if constexpr (PW % 4 == 2) {
-        u32x2 v;
-        __builtin_memcpy(&v, p + PW - 2, 8);
+        const u32x2a v = *(const __attribute__((address_space(1))) u32x2a*)(p + PW - 2);
         u[PW - 2] = v.x, u[PW - 1] = v.y;
     }
 }
@@ -234,22 +261,24 @@ template <int KIND>
 __device__ __forceinline__ void load_activations(const Activations& act, uint32_t k, uint32_t nb, uint32_t b,
                                                  uint32_t j, uint32_t* a, float& sx0, float& sx1, int& e0, int& e1,
                                                  float& mx0, float& mx1) {
-    const u32x4* q = (const u32x4*)(act.qs + (size_t)b * k + (size_t)j * 64u);
+    typedef uint32_t gu32x4 __attribute__((ext_vector_type(4)));
+    const __attribute__((address_space(1))) gu32x4* q =
+        (const __attribute__((address_space(1))) gu32x4*)(act.qs + (size_t)b * k + (size_t)j * 64u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        u32x4 v = q[i];
+        const gu32x4 v = q[i];
         a[4 * i] = v.x, a[4 * i + 1] = v.y, a[4 * i + 2] = v.z, a[4 * i + 3] = v.w;
     }
     const size_t at = (size_t)b * nb + 2u * j;
-    const float2 s = *(const float2*)(act.scales + at);
-    sx0 = s.x, sx1 = s.y;
+    const gptr<float> sc = global(act.scales + at);
+    sx0 = sc[0], sx1 = sc[1];
     if constexpr (KIND == 1) {
-        const int2 t = *(const int2*)(act.totals + at);
-        e0 = -8 * t.x, e1 = -8 * t.y;
+        const gptr<int32_t> tt = global(act.totals + at);
+        e0 = -8 * tt[0], e1 = -8 * tt[1];
     }
     if constexpr (KIND == 2) {
-        const float2 m = *(const float2*)(act.sums + at);
-        mx0 = m.x, mx1 = m.y;
+        const gptr<float> m = global(act.sums + at);
+        mx0 = m[0], mx1 = m[1];
     }
 }
 
@@ -332,6 +361,319 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, A
             dst[(size_t)b * n + row] = bias ? sum + bias[row] : sum;
         }
     }
+}
+
+// ------------------------------------------- lanes, one row, fused quantise
+
+// The quantised form of 4 of a block's 32 activations, held by one lane of
+// an 8-lane group (all 8 lanes active): the group's amax and Σq reduced over
+// the 8 lanes, then quantize_activations' arithmetic (quant.cr:428-442).
+struct Q8Quad {
+    uint32_t packed;  // the 4 int8 values
+    float scale;      // F16(d)
+    float sum;        // F16(float(Σq) · d)
+    int total;        // Σq over the block
+};
+
+__device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, float v3) {
+    float amax = fabsf(v0);
+    amax = fabsf(v1) > amax ? fabsf(v1) : amax;
+    amax = fabsf(v2) > amax ? fabsf(v2) : amax;
+    amax = fabsf(v3) > amax ? fabsf(v3) : amax;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) {
+        float other = __shfl_xor(amax, width, 8);
+        amax = other > amax ? other : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = d == 0.0f ? 0.0f : 1.0f / d;
+    const int q0 = (int8_t)(int)roundf(v0 * id);
+    const int q1 = (int8_t)(int)roundf(v1 * id);
+    const int q2 = (int8_t)(int)roundf(v2 * id);
+    const int q3 = (int8_t)(int)roundf(v3 * id);
+    Q8Quad out;
+    out.packed = (uint32_t)(q0 & 0xff) | (uint32_t)(q1 & 0xff) << 8 | (uint32_t)(q2 & 0xff) << 16 |
+                 (uint32_t)(q3 & 0xff) << 24;
+    int total = q0 + q1 + q2 + q3;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) total += __shfl_xor(total, width, 8);
+    out.total = total;
+    out.scale = round_to_half(d);
+    out.sum = round_to_half((float)total * d);
+    return out;
+}
+
+// Steps of weight loads issued together per thread (a batch of D pairs),
+// by kind: Q8_0 pairs are 17 dwords, Q4_0 9, Q4_1 10.
+template <int KIND>
+struct Depth {
+    static constexpr uint32_t D = KIND == 0 ? 2 : 3;
+};
+
+// x · wᵀ for ONE activation row, quantised inside the workgroup: the
+// activations are quantised once per workgroup into LDS (8 lanes a block),
+// while the first steps of weight loads are already in flight; then the
+// lanes scheme of k_matvec: thread t takes pair j = t % np of row t / np of
+// each step of rpi = 256/np rows, its two contributions go to
+// part[row][block], and thread r adds row r's contributions in block order.
+// Weight loads are issued D steps at a time.
+//
+// LDS: k bytes of int8 values, nb scales, nb extras (Q4_0: -8·Σq; Q4_1:
+// F16(d·Σq)), then tr × stride floats of contributions.
+// Per-thread geometry of one tile of a one-row product. Thread t takes pair
+// j = t % np of row group member rsub = t / np; threads past the last row
+// group (rsub >= rpi) shadow the last member so that every load stays in
+// bounds, and store nothing. Step s of the tile covers row group
+// s * tiles + tile (rpi rows): at any moment all workgroups of a product
+// read one compact window of rows.
+struct TileGeo {
+    uint32_t nb, np, rpi, j, rsub, load_rsub, steps, group_stride, row0;
+    bool lane_on;
+};
+
+__device__ __forceinline__ TileGeo tile_geo(const RowProduct& p, uint32_t tile) {
+    TileGeo g;
+    const uint32_t t = threadIdx.x;
+    g.nb = p.k >> 5;
+    g.np = g.nb >> 1;
+    g.rpi = 256u / g.np;
+    g.j = t % g.np;
+    g.rsub = t / g.np;
+    g.lane_on = g.rsub < g.rpi;
+    g.load_rsub = g.lane_on ? g.rsub : g.rpi - 1u;
+    g.steps = p.tr / g.rpi;
+    g.group_stride = p.tiles * g.rpi;
+    g.row0 = tile * g.rpi;
+    return g;
+}
+
+// Loads steps s0 ... s0 + D - 1 of a tile into u. Every thread loads -- a
+// step past the tile's last, or a row past the product's last, reads the
+// last one again -- so the loads are straight-line code and the compiler's
+// wait counts stay exact (loads complete in issue order).
+template <int KIND, uint32_t D>
+__device__ __forceinline__ void load_steps(const RowProduct& p, const TileGeo& g, uint32_t s0,
+                                           uint32_t (&u)[D][Fmt<KIND>::PW]) {
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+    const uint32_t* wp = (const uint32_t*)p.w + (size_t)g.j * PW;
+    const size_t row_words = (size_t)g.np * PW;
+#pragma unroll
+    for (uint32_t d = 0; d < D; ++d) {
+        const uint32_t s = min(s0 + d, g.steps - 1u);
+        const uint32_t row = min(g.row0 + s * g.group_stride + g.load_rsub, p.n - 1u);
+        load_pair<KIND>(wp + (size_t)row * row_words, u[d]);
+    }
+}
+
+// The pair's activations, read from LDS.
+struct PairActs {
+    uint32_t a[16];
+    float sx0, sx1, mx0, mx1;
+    int e0, e1;
+};
+
+__device__ __forceinline__ void read_acts(const uint8_t* act, uint32_t k, uint32_t j, PairActs& v) {
+    const uint32_t nb = k >> 5;
+    const u32x4* q = (const u32x4*)(act + (size_t)j * 64u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 w = q[i];
+        v.a[4 * i] = w.x, v.a[4 * i + 1] = w.y, v.a[4 * i + 2] = w.z, v.a[4 * i + 3] = w.w;
+    }
+    const float* lsc = (const float*)(act + k);
+    const int32_t* lex = (const int32_t*)(lsc + nb);
+    v.sx0 = lsc[2u * j], v.sx1 = lsc[2u * j + 1u];
+    v.e0 = lex[2u * j], v.e1 = lex[2u * j + 1u];
+    v.mx0 = __int_as_float(v.e0), v.mx1 = __int_as_float(v.e1);
+}
+
+// The contributions of steps s0 ... s0 + D - 1 (weights in u) to LDS
+// part[row of the tile][block]. Every thread computes and stores, without a
+// branch: a thread with no real row (an idle lane, or a step past the
+// tile's last) stores into the spare row past the tile's, which is never
+// folded; rows past the product's last are never folded either.
+template <int KIND, uint32_t D>
+__device__ __forceinline__ void compute_steps(const RowProduct& p, const TileGeo& g, uint32_t s0,
+                                              const uint32_t (&u)[D][Fmt<KIND>::PW], const PairActs& v,
+                                              float* part) {
+#pragma unroll
+    for (uint32_t d = 0; d < D; ++d) {
+        const uint32_t s = s0 + d;
+        float c0, c1;
+        Pair<KIND>::contribute(u[d], v.a, v.sx0, v.sx1, v.e0, v.e1, v.mx0, v.mx1, c0, c1);
+        const uint32_t slot = (g.lane_on && s < g.steps) ? s * g.rpi + g.rsub : p.tr;
+        *(float2*)(part + (size_t)slot * p.stride + 2u * g.j) = make_float2(c0, c1);
+    }
+}
+
+// Adds each row of a tile's contributions in block order -- the host's order
+// -- and writes it plus its bias, already loaded (thread r takes row r).
+__device__ __forceinline__ void fold_tile(const float* part, const RowProduct& p, const TileGeo& g, float bias) {
+    const uint32_t r = threadIdx.x;
+    if (r >= p.tr) return;
+    const uint32_t row = g.row0 + (r / g.rpi) * g.group_stride + r % g.rpi;
+    if (row >= p.n) return;
+    const float* c = part + (size_t)r * p.stride;
+    float sum = 0.0f;
+    uint32_t i = 0;
+    for (; i + 4 <= g.nb; i += 4) {
+        const float4 v = *(const float4*)(c + i);
+        sum += v.x;
+        sum += v.y;
+        sum += v.z;
+        sum += v.w;
+    }
+    for (; i < g.nb; ++i) sum += c[i];
+    *(__attribute__((address_space(1))) float*)(p.dst + row) = p.bias ? sum + bias : sum;
+}
+
+// The bias of the row thread r folds (0 when there is none). Every thread
+// loads -- with no bias, or no row, from a valid stand-in address -- so the
+// load is straight-line code.
+__device__ __forceinline__ float load_bias(const RowProduct& p, const TileGeo& g) {
+    const uint32_t r = min((uint32_t)threadIdx.x, p.tr - 1u);
+    const uint32_t row = min(g.row0 + (r / g.rpi) * g.group_stride + r % g.rpi, p.n - 1u);
+    const float v = *global(p.bias ? p.bias + row : p.x);
+    return p.bias ? v : 0.0f;
+}
+
+// The activations of the first XP quantise passes (32 blocks a pass, 8 lanes
+// a block), loaded ahead of a product's weights.
+constexpr uint32_t XP = 2;
+
+__device__ __forceinline__ void load_x(const float* __restrict__ x, uint32_t k, float4 (&xv)[XP]) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nb = k >> 5;
+    const bool vec = ((uintptr_t)x & 15u) == 0;
+#pragma unroll
+    for (uint32_t p = 0; p < XP; ++p) {
+        const uint32_t g = min(p * 32u + (t >> 3), nb - 1u);
+        xv[p] = load_f4(x + g * 32u + (t & 7u) * 4u, vec);
+    }
+}
+
+// Quantises activation row x (k values) into LDS at act; the first XP
+// passes come from xv. The caller synchronises before reading it.
+template <int KIND>
+__device__ __forceinline__ void quantise_into(uint8_t* act, const float* __restrict__ x, uint32_t k,
+                                              const float4 (&xv)[XP]) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nb = k >> 5;
+    int8_t* lqs = (int8_t*)act;
+    float* lsc = (float*)(act + k);
+    int32_t* lex = (int32_t*)(lsc + nb);
+    const bool vec = ((uintptr_t)x & 15u) == 0;
+    for (uint32_t pass = 0; pass * 32u < nb; ++pass) {
+        const uint32_t g = pass * 32u + (t >> 3), sub = t & 7u;
+        if (g < nb) {
+            float4 v;
+            if (pass < XP) {
+                v = pass == 0 ? xv[0] : xv[1];
+            } else {
+                v = load_f4(x + g * 32u + sub * 4u, vec);
+            }
+            const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
+            *(uint32_t*)(lqs + g * 32u + sub * 4u) = q.packed;
+            if (sub == 0) {
+                lsc[g] = q.scale;
+                lex[g] = KIND == 1 ? -8 * q.total : __float_as_int(q.sum);
+            }
+        }
+    }
+}
+
+// The product of a tile, read with scalar loads (the index is uniform).
+__device__ __forceinline__ uint32_t owner_of(const uint32_t* __restrict__ owner, uint32_t tile) {
+    return __builtin_amdgcn_readfirstlane(*global(owner + tile));
+}
+
+// One-row products, persistent: each workgroup walks tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... of all `total` tiles (tile t belongs to
+// product owner[t] of `table`; with no table, to `single`). A product's
+// activations are quantised into LDS when its first tile on this workgroup
+// comes up. Weights stream in batches of D steps, two batches in flight:
+// batch B loads while batch A computes and the reverse; the last batch of a
+// tile loads the next tile's first steps (and, for a new product, its
+// activations and biases) ahead of this tile's fold. LDS: act_bytes for
+// activations, then the contributions. Every workgroup leaves after its last
+// tile; all loop bounds are uniform over the workgroup.
+template <int KIND, uint32_t D>
+__device__ __forceinline__ void matvec_rows(const RowProduct* __restrict__ table, const uint32_t* __restrict__ owner,
+                                            const RowProduct& single, uint32_t total, uint32_t act_bytes) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+    uint8_t* act = smem;
+    float* part = (float*)(smem + act_bytes);
+    const uint32_t G = gridDim.x;
+    uint32_t tile = blockIdx.x;
+    if (tile >= total) return;
+
+    uint32_t pi = table ? owner_of(owner, tile) : 0u;
+    RowProduct p = table ? table[pi] : single;
+    TileGeo g = tile_geo(p, tile - p.first);
+    float4 xv[XP];
+    load_x(p.x, p.k, xv);
+    float bias = load_bias(p, g);
+    uint32_t ua[D][PW], ub[D][PW];
+    load_steps<KIND, D>(p, g, 0, ua);
+    uint32_t have = 0xffffffffu;
+
+    while (true) {
+        if (pi != have) {
+            quantise_into<KIND>(act, p.x, p.k, xv);
+            __syncthreads();
+            have = pi;
+        }
+        PairActs v;
+        read_acts(act, p.k, g.j, v);
+
+        // The next tile, found with scalar loads before any weight load:
+        // with no next tile, the stand-in is this one (its loads are
+        // issued again and unused), so every path issues the same loads.
+        const uint32_t next = tile + G;
+        const bool more = next < total;
+        uint32_t npi = pi;
+        if (table && more) npi = owner_of(owner, next);
+        const RowProduct q = (table && npi != pi) ? table[npi] : p;
+        const TileGeo h = more ? tile_geo(q, next - q.first) : g;
+
+        // Whole rounds: batch B loads while A computes, then A while B.
+        uint32_t s0 = 0;
+        for (; s0 + 2u * D < g.steps; s0 += 2u * D) {
+            load_steps<KIND, D>(p, g, s0 + D, ub);
+            compute_steps<KIND, D>(p, g, s0, ua, v, part);
+            load_steps<KIND, D>(p, g, s0 + 2u * D, ua);
+            compute_steps<KIND, D>(p, g, s0 + D, ub, v, part);
+        }
+        // The last round: its second batch, then the next tile's first
+        // loads (activations, biases, weights) go out before this tile's
+        // fold.
+        load_steps<KIND, D>(p, g, s0 + D, ub);
+        compute_steps<KIND, D>(p, g, s0, ua, v, part);
+        load_x(q.x, q.k, xv);
+        const float nbias = load_bias(q, h);
+        load_steps<KIND, D>(q, h, 0, ua);
+        compute_steps<KIND, D>(p, g, s0 + D, ub, v, part);
+
+        __syncthreads();  // every contribution of this tile is in `part`
+        fold_tile(part, p, g, bias);
+        if (!more) break;
+        __syncthreads();  // the fold has read `part`; `act` may be replaced
+        tile = next, pi = npi, p = q, g = h, bias = nbias;
+    }
+}
+
+template <int KIND, uint32_t D>
+__global__ __launch_bounds__(256) void k_matvec_rows(const RowProduct* __restrict__ table,
+                                                     const uint32_t* __restrict__ owner, uint32_t total,
+                                                     uint32_t act_bytes) {
+    const RowProduct none{};
+    matvec_rows<KIND, D>(table, owner, none, total, act_bytes);
+}
+
+template <int KIND, uint32_t D>
+__global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_bytes) {
+    matvec_rows<KIND, D>(nullptr, nullptr, p, p.tiles, act_bytes);
 }
 
 // ------------------------------------------------- thread per output
@@ -537,6 +879,118 @@ static hipError_t launch_thread(const uint8_t* w, Activations act, float* dst, c
 static bool lanes_fit(const uint8_t* w, uint32_t k) {
     const uint32_t nb = k >> 5;
     return nb >= 2 && nb % 2 == 0 && nb <= 512 && (uintptr_t)w % 4u == 0;
+}
+
+// LDS of the one-row kernel before its contributions: values, scales, extras.
+static size_t row_act_lds(uint32_t k) { return (size_t)k + 8u * (k >> 5); }
+
+// Weight bytes a workgroup of the one-row kernel aims to stream: enough
+// steps to keep loads in flight and to amortise the workgroup's own
+// quantise pass and fold (TMH_ROW_TILE_BYTES overrides, for tuning).
+static size_t row_tile_bytes() {
+    static const size_t bytes = [] {
+        const char* env = getenv("TMH_ROW_TILE_BYTES");
+        long v = env ? atol(env) : 0;
+        return v > 0 ? (size_t)v : (size_t)48 * 1024;
+    }();
+    return bytes;
+}
+
+// Rows per tile of the one-row kernel: a multiple of the rows one step
+// covers, about row_tile_bytes() of weights, within the LDS limit and 256
+// folds, and small enough to leave at least `min_tiles` tiles when the
+// product has the rows for them.
+static uint32_t row_tile(uint32_t nb, uint32_t n, size_t row_bytes_, uint32_t min_tiles) {
+    const uint32_t np = nb / 2u;
+    const uint32_t rpi = 256u / np;
+    const uint32_t stride = lanes_stride(nb);
+    const size_t base = row_act_lds(nb * 32u);
+    uint32_t m = (uint32_t)(row_tile_bytes() / (row_bytes_ * rpi));
+    if (m < 1) m = 1;
+    const uint32_t fill = n / (rpi * (min_tiles > 0 ? min_tiles : 1u));
+    if (m > fill) m = fill > 0 ? fill : 1;
+    while (m > 1 && (rpi * m > 256u || base + (size_t)(rpi * m + 1u) * stride * 4u > LANES_LDS_LIMIT)) --m;
+    return rpi * m;
+}
+
+bool row_kernel_fits(uint32_t mode, const uint8_t* w, uint32_t k) {
+    if (mode == 1u /* THREAD */ || !lanes_fit(w, k)) return false;
+    const uint32_t nb = k >> 5;
+    const uint32_t rpi = 256u / (nb / 2u);
+    return row_act_lds(k) + (size_t)(rpi + 1u) * lanes_stride(nb) * 4u <= LANES_LDS_LIMIT;
+}
+
+// Workgroups per compute unit of the persistent one-row kernel
+// (TMH_ROW_WGS_PER_CU overrides, for tuning).
+static uint32_t row_wgs_per_cu() {
+    static const uint32_t v = [] {
+        const char* env = getenv("TMH_ROW_WGS_PER_CU");
+        long x = env ? atol(env) : 0;
+        return x > 0 ? (uint32_t)x : 4u;
+    }();
+    return v;
+}
+
+static size_t align16(size_t v) { return (v + 15u) & ~(size_t)15u; }
+
+// Workgroups for `tiles` tiles: at most row_wgs_per_cu() per compute unit
+// (measured: evening out the tiles per workgroup did not pay).
+static uint32_t balanced_grid(uint32_t tiles, int compute_units) {
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    return std::min<uint32_t>(tiles, cus * row_wgs_per_cu());
+}
+
+void plan_row(uint32_t kind, RowProduct& p, int compute_units) {
+    (void)compute_units;
+    const uint32_t nb = p.k >> 5;
+    p.tr = row_tile(nb, p.n, (size_t)nb * block_bytes(kind), 1u);
+    p.stride = lanes_stride(nb);
+    p.tiles = (p.n + p.tr - 1u) / p.tr;
+}
+
+size_t row_act_bytes(const RowProduct& p) { return align16(row_act_lds(p.k)); }
+
+size_t row_part_bytes(const RowProduct& p) { return (size_t)(p.tr + 1u) * p.stride * sizeof(float); }
+
+hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* owner, uint32_t tiles,
+                       size_t act_bytes, size_t part_bytes, int compute_units, hipStream_t stream) {
+    if (tiles == 0) return hipSuccess;
+    const uint32_t grid = balanced_grid(tiles, compute_units);
+    const uint32_t ab = (uint32_t)align16(act_bytes);
+    const size_t lds = ab + part_bytes;
+    if (kind == 0)
+        hipLaunchKernelGGL((k_matvec_rows<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+                           ab);
+    else if (kind == 1)
+        hipLaunchKernelGGL((k_matvec_rows<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+                           ab);
+    else
+        hipLaunchKernelGGL((k_matvec_rows<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+                           ab);
+    return hipGetLastError();
+}
+
+hipError_t launch_row(uint32_t kind, const uint8_t* w, const float* x, float* dst, const float* bias, uint32_t n,
+                      uint32_t k, int compute_units, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    RowProduct p{};
+    p.w = w, p.x = x, p.dst = dst, p.bias = bias, p.n = n, p.k = k;
+    const uint32_t nb = k >> 5;
+    p.tr = row_tile(nb, n, (size_t)nb * block_bytes(kind), cus * row_wgs_per_cu());
+    p.stride = lanes_stride(nb);
+    p.tiles = (n + p.tr - 1u) / p.tr;
+    p.first = 0;
+    const uint32_t grid = balanced_grid(p.tiles, compute_units);
+    const uint32_t ab = (uint32_t)row_act_bytes(p);
+    const size_t lds = ab + row_part_bytes(p);
+    if (kind == 0)
+        hipLaunchKernelGGL((k_matvec_row<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+    else if (kind == 1)
+        hipLaunchKernelGGL((k_matvec_row<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+    else
+        hipLaunchKernelGGL((k_matvec_row<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+    return hipGetLastError();
 }
 
 hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, Activations act, float* dst,

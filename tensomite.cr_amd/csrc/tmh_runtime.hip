@@ -8,6 +8,7 @@
 // into. This is the host side of the reference's `CUDA < HostDevice`
 // (src/tensomite/cuda.cr) and its `BufferPool`/`RetiredList`
 // (src/tensomite/buffer_pool.cr), restated natively for HIP.
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -644,6 +645,13 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     if (ldx < k) return TMH_ERROR_SHAPE;
     if (rows == 0 || n == 0) return TMH_SUCCESS;
     if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
+    const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
+    if (rows == 1 && tmh::row_kernel_fits(mode, wrow, k)) {
+        hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
+                                       d->compute_units, d->stream);
+        if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+        return code(e);
+    }
     std::lock_guard<std::mutex> guard(d->launch);
     if ((err = ensure_scratch(*d, scratch_need(rows, k))) != TMH_SUCCESS) return err;
     float *scales, *sums;
@@ -692,6 +700,99 @@ int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset,
                                       (const int32_t*)ids, count, (float*)dst, d->errors, d->stream);
     if (e == hipSuccess) d->gpu_ops.fetch_add(1);
     return code(e);
+}
+
+namespace {
+
+struct Plan {
+    int device;
+    uint32_t kind;
+    uint32_t count;
+    uint32_t tiles;
+    size_t act_bytes, part_bytes;
+    tmh::RowProduct* table;  // device memory: the products, then each tile's product index
+    uint32_t* owner;
+};
+
+}  // namespace
+
+int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, uint64_t* plan) {
+    if (!plan || (count && !products)) return TMH_ERROR_INVALID_VALUE;
+    if (kind > 2u) return TMH_ERROR_DTYPE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    std::vector<tmh::RowProduct> rows(count);
+    uint32_t first = 0;
+    size_t act_bytes = 0, part_bytes = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const tmh_product& q = products[i];
+        if (q.k == 0 || q.k % 32u != 0 || q.n == 0) return TMH_ERROR_SHAPE;
+        if (!q.w || !q.x || !q.dst) return TMH_ERROR_INVALID_VALUE;
+        const uint8_t* w = (const uint8_t*)(q.w + q.w_byte_offset);
+        if (!tmh::row_kernel_fits(TMH_MODE_LANES, w, q.k)) return TMH_ERROR_SHAPE;
+        tmh::RowProduct& r = rows[i];
+        r.w = w;
+        r.x = (const float*)q.x;
+        r.dst = (float*)q.dst;
+        r.bias = (const float*)q.bias;
+        r.n = q.n;
+        r.k = q.k;
+        tmh::plan_row(kind, r, d->compute_units);
+        r.first = first;
+        if ((uint64_t)first + r.tiles > 0x7fffffffull) return TMH_ERROR_SHAPE;
+        first += r.tiles;
+        act_bytes = std::max(act_bytes, tmh::row_act_bytes(r));
+        part_bytes = std::max(part_bytes, tmh::row_part_bytes(r));
+    }
+    if (act_bytes + part_bytes > 64u * 1024u) return TMH_ERROR_SHAPE;
+    Plan* p = new Plan{d->index, kind, count, first, act_bytes, part_bytes, nullptr, nullptr};
+    if (count) {
+        // One allocation: the product table, then the tile -> product map.
+        std::vector<uint32_t> owner(first);
+        for (uint32_t i = 0; i < count; ++i)
+            for (uint32_t t = 0; t < rows[i].tiles; ++t) owner[rows[i].first + t] = i;
+        const size_t table_bytes = align256(sizeof(tmh::RowProduct) * count);
+        void* mem = nullptr;
+        hipError_t e = device_malloc(&mem, table_bytes + sizeof(uint32_t) * first);
+        if (e == hipSuccess) e = hipMemcpy(mem, rows.data(), sizeof(tmh::RowProduct) * count, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy((uint8_t*)mem + table_bytes, owner.data(), sizeof(uint32_t) * first, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            if (mem) (void)hipFree(mem);
+            delete p;
+            return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
+        }
+        p->table = (tmh::RowProduct*)mem;
+        p->owner = (uint32_t*)((uint8_t*)mem + table_bytes);
+    }
+    *plan = (uint64_t)p;
+    return TMH_SUCCESS;
+}
+
+int tmh_plan_run(uint64_t plan) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    if (!plan) return TMH_ERROR_INVALID_VALUE;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    Plan* p = (Plan*)plan;
+    if (p->device != d->index) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = tmh::launch_rows(p->kind, p->table, p->owner, p->tiles, p->act_bytes, p->part_bytes,
+                                    d->compute_units, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(p->count);
+    return code(e);
+}
+
+int tmh_plan_destroy(uint64_t plan) {
+    if (!plan) return TMH_SUCCESS;
+    Plan* p = (Plan*)plan;
+    int err;
+    Device* d = current(&err);
+    if (d) (void)hipStreamSynchronize(d->stream);
+    if (p->table) (void)hipFree(p->table);
+    delete p;
+    return TMH_SUCCESS;
 }
 
 }  // extern "C"

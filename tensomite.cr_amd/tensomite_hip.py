@@ -73,6 +73,12 @@ class DeviceInfo(ctypes.Structure):
                 ("l2_bytes", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32)]
 
 
+class Product(ctypes.Structure):
+    """tmh_product: one one-row product of a plan."""
+    _fields_ = [("w", ctypes.c_uint64), ("w_byte_offset", ctypes.c_uint64), ("x", ctypes.c_uint64),
+                ("dst", ctypes.c_uint64), ("bias", ctypes.c_uint64), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32)]
+
+
 class Counters(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in
                 ("uploads", "downloads", "gpu_ops", "device_bytes", "pool_held", "pool_limit", "pool_hits",
@@ -113,6 +119,9 @@ SIGNATURES = {
     "tmh_block_matmul": (INT, [U32, U64, U64, U64, U32, U64, U64, U32, U32, U32, U32]),
     "tmh_block_matmul_quantised": (INT, [U32, U64, U64, U64, U64, U64, U64, U64, U64, U32, U32, U32, U32]),
     "tmh_gather_blocks": (INT, [U32, U64, U64, I32, U32, U64, U32, U64]),
+    "tmh_plan_create": (INT, [U32, ctypes.POINTER(Product), U32, ctypes.POINTER(U64)]),
+    "tmh_plan_run": (INT, [U64]),
+    "tmh_plan_destroy": (INT, [U64]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -200,6 +209,27 @@ class Buffer:
                 self.device._retire(self)
             except Exception:
                 pass
+
+
+class Plan:
+    """A recorded list of one-row products run as one launch (tmh_plan_*)."""
+
+    def __init__(self, device: "HIPDevice", handle: int, keep):
+        self.device, self.handle, self._keep = device, handle, keep
+
+    def run(self) -> None:
+        check("tmh_plan_run", self.device.lib.tmh_plan_run(self.handle))
+
+    def destroy(self) -> None:
+        if self.handle:
+            self.device.lib.tmh_plan_destroy(self.handle)
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class HIPDevice:
@@ -346,6 +376,21 @@ class HIPDevice:
         check("tmh_gather_blocks", self.lib.tmh_gather_blocks(
             kk, table.pointer, first_row * rb, table_rows, width, ids.pointer, count, dst.pointer))
         return dst
+
+    # -- plans: many independent one-row products in one launch
+    def plan(self, kind, products) -> "Plan":
+        """products: iterable of (w Buffer, w_row, x Buffer, dst Buffer, bias Buffer|None, n, k)."""
+        kk = kind_of(kind)
+        items = list(products)
+        arr = (Product * max(len(items), 1))()
+        for i, (w, w_row, x, dst, bias, n, k) in enumerate(items):
+            rb = row_bytes(kk, k)
+            if (w_row + n) * rb > w.bytesize or k * 4 > x.bytesize or n * 4 > dst.bytesize:
+                raise ShapeError(f"product {i}: buffers too small for [{n}, {k}]")
+            arr[i] = Product(w.pointer, w_row * rb, x.pointer, dst.pointer, bias.pointer if bias else 0, n, k)
+        handle = U64(0)
+        check("tmh_plan_create", self.lib.tmh_plan_create(kk, arr, len(items), ctypes.byref(handle)))
+        return Plan(self, handle.value, items)
 
     # -- timing on the library's stream
     def event(self) -> int:

@@ -310,3 +310,29 @@ def test_errors_are_typed(dev):
     finally:
         dev.lib.tmh_debug_disable_kernels(0)
     dev.sync()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_plan_equals_products_one_by_one(dev, fmt):
+    # tmh_plan_*: many one-row products in one launch give each product's bits.
+    shapes = [(960, 576), (576, 576), (3072, 576), (576, 1536), (300, 2048), (7, 64), (2304, 768), (100, 8192)]
+    ws, xs, wants = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        wq = weights(fmt, n, k, 500 + i)
+        x = acts(1, k, 600 + i)
+        ws.append(dev.from_array(wq))
+        xs.append(dev.from_array(x))
+        wants.append(oracle.matmul(fmt, x, wq, 1, n, k)[0])
+    ys = [dev.alloc(4 * n) for n, _ in shapes]
+    bias = dev.from_array(np.arange(3072, dtype=np.float32) * 0.25)
+    items = [(ws[i], 0, xs[i], ys[i], bias if i == 2 else None, n, k) for i, (n, k) in enumerate(shapes)]
+    say("plan", fmt)
+    plan = dev.plan(fmt, items)
+    for _ in range(3):
+        plan.run()
+    dev.sync()
+    for i, (n, k) in enumerate(shapes):
+        got = dev.to_array(ys[i], np.float32, n)
+        want = wants[i] + (np.arange(3072, dtype=np.float32)[:n] * 0.25 if i == 2 else 0)
+        assert np.array_equal(bits(got), bits(want.astype(np.float32))), shapes[i]
+    plan.destroy()

@@ -1,0 +1,56 @@
+"""The package's vectorised host quantiser (tensomite.cr_amd/quant_host.py)
+equals the oracle's Quant.quantize byte for byte: on the reference's fixture
+rows, on N(0, 0.02) matrices as the BASELINE configs use, and on edge
+values (signed zeros, ties, subnormal scales, constant blocks)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import quant_host
+from oracle import oracle
+
+FORMATS = ["Q8_0", "Q4_0", "Q4_1"]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_fixture_rows(golden, fmt):
+    with open(os.path.join(golden, "quant", "expected.json")) as f:
+        expected = json.load(f)
+    for i, row in enumerate(expected["rows"]):
+        got = quant_host.quantize(fmt, np.array(row, dtype=np.float32))
+        assert got.tobytes().hex() == expected[fmt]["bytes"][i], i
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_random_matrices_equal_oracle(fmt):
+    rng = np.random.default_rng(42)
+    for std in (0.02, 1.0, 1e-4, 300.0):
+        v = rng.normal(0, std, 64 * 2048).astype(np.float32)
+        assert np.array_equal(quant_host.quantize(fmt, v), oracle.quantize(fmt, v)), std
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_edge_values_equal_oracle(fmt):
+    rng = np.random.default_rng(3)
+    blocks = [
+        np.zeros(32), -np.zeros(32), np.concatenate([[-0.0, 0.0], np.zeros(30)]),
+        np.concatenate([[0.0, -0.0], np.ones(30)]), np.full(32, 0.25), np.full(32, -3.0),
+        np.array([(i - 16) / 2 for i in range(32)]), np.array([127.0] + [j - 15.5 for j in range(1, 32)]),
+        np.array([1e-8 * (i - 7) for i in range(32)]), np.array([6e-5 * ((-1) ** i) for i in range(32)]),
+        rng.uniform(-1, 1, 32) * 1e-30, np.array([65504.0, -65504.0] + [1.0] * 30),
+        np.array([-5.0] + [5.0] * 31), np.array([5.0] + [-5.0] * 31),
+    ]
+    v = np.concatenate([np.asarray(b, dtype=np.float32) for b in blocks])
+    assert np.array_equal(quant_host.quantize(fmt, v), oracle.quantize(fmt, v))
+
+
+def test_f16_bits_match_oracle():
+    rng = np.random.default_rng(9)
+    words = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    values = words.view(np.float32)
+    values = values[~np.isnan(values)]
+    assert np.array_equal(quant_host.f16_bits(values), oracle.f16_bits_many(values))
+    nan = np.array([np.nan, -np.nan], dtype=np.float32)
+    assert quant_host.f16_bits(nan).tolist() == [0x7E00, 0xFE00]
