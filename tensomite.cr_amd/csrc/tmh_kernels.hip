@@ -676,6 +676,207 @@ __global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_b
     matvec_rows<KIND, D>(nullptr, nullptr, p, p.tiles, act_bytes);
 }
 
+// ------------------------------------------------ matrix cores: many rows
+
+// x · wᵀ for many activation rows on the int8 matrix cores. Workgroup tile
+// 64 rows (M) x 64 outputs (N), 4 waves of 32 x 32 (2 x 2 MFMA tiles of
+// 16 x 16). One v_mfma_i32_16x16x32_i8 spans exactly one block of 32, so
+// each block's integer dot product comes out on its own, exact; then every
+// output adds that block's contribution, in the host's expression, to its
+// running f32 sum -- blocks in order, so the bits are the host's:
+//   Q8_0  float(t) * (d * sx)             (t from the MFMA)
+//   Q4_0  (float(t) * d) * sx             (t = MFMA(q, y) - 8·Σy: the MFMA
+//                                          starts from C = -8·Σy)
+//   Q4_1  (d * sx) * float(t) + m * mx
+// Per stage (two blocks) the workgroup stages into LDS: the 64 weight rows'
+// two blocks as aligned int8 (nibbles unpacked), their scales (and Q4_1
+// minimums) as f32, and the 64 activation rows' scales and extras; stages
+// are double-buffered so the next stage's loads fly while this one computes.
+// MFMA operand layout (16x16x32 i8, checked on the device): lane l holds
+// A[l % 16][8 (l / 16) ...] and B[8 (l / 16) ...][l % 16]; the result holds
+// rows 4 (l / 16) + i, column l % 16.
+constexpr uint32_t MM_TILE = 64;
+constexpr uint32_t MM_BROW = 72;  // LDS bytes per weight row (64 values + pad): conflict-free 8-byte reads
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct MmStage {
+    int8_t wq[MM_TILE * MM_BROW];  // [n][2 blocks x 32 values + pad]
+    float wd[2][MM_TILE];          // weight d by [block][n]
+    float wm[2][MM_TILE];          // weight m (Q4_1) by [block][n]
+    float sx[2][MM_TILE];          // activation scale by [block][row]
+    float ex[2][MM_TILE];          // Q4_0: -8·Σq as int; Q4_1: F16(d·Σq)
+};
+
+// Issues the global loads of stage `pair` (blocks 2·pair, 2·pair + 1):
+// threads 0-63 one weight row's pair, 64-191 one activation scale, 128-255
+// one extra. Returns them in registers for stage_store.
+template <int KIND>
+struct MmLoad {
+    uint32_t u[Fmt<KIND>::PW];
+    float sx;
+    int32_t ex;
+};
+
+template <int KIND>
+__device__ __forceinline__ void stage_load(const uint8_t* __restrict__ w, const Activations& act, uint32_t n,
+                                           uint32_t m, uint32_t nb, uint32_t n0, uint32_t m0, uint32_t pair,
+                                           MmLoad<KIND>& L) {
+    const uint32_t t = threadIdx.x;
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+    if (t < MM_TILE) {
+        const uint32_t row = min(n0 + t, n - 1u);
+        const uint32_t* p = (const uint32_t*)w + ((size_t)row * (nb >> 1) + pair) * PW;
+        load_pair<KIND>(p, L.u);
+    }
+    if (t >= 64u && t < 192u) {
+        const uint32_t i = t - 64u, r = min(m0 + (i >> 1), m - 1u), b = 2u * pair + (i & 1u);
+        L.sx = *global(act.scales + (size_t)r * nb + b);
+    }
+    if (t >= 128u) {
+        const uint32_t i = t - 128u, r = min(m0 + (i >> 1), m - 1u), b = 2u * pair + (i & 1u);
+        if constexpr (KIND == 1) L.ex = -8 * *global(act.totals + (size_t)r * nb + b);
+        if constexpr (KIND == 2) L.ex = __float_as_int(*global(act.sums + (size_t)r * nb + b));
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void stage_store(MmStage& S, const MmLoad<KIND>& L) {
+    const uint32_t t = threadIdx.x;
+    if (t < MM_TILE) {
+        uint32_t* q = (uint32_t*)(S.wq + t * MM_BROW);
+        const uint32_t* u = L.u;
+        if constexpr (KIND == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = funnel(u[i + 1], u[i], 2);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[8 + i] = u[9 + i];
+            S.wd[0][t] = half_value(u[0] & 0xffffu);
+            S.wd[1][t] = half_value(u[8] >> 16);
+        } else if constexpr (KIND == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w0 = funnel(u[i + 1], u[i], 2), w1 = u[5 + i];
+                q[i] = w0 & 0x0f0f0f0fu, q[4 + i] = (w0 >> 4) & 0x0f0f0f0fu;
+                q[8 + i] = w1 & 0x0f0f0f0fu, q[12 + i] = (w1 >> 4) & 0x0f0f0f0fu;
+            }
+            S.wd[0][t] = half_value(u[0] & 0xffffu);
+            S.wd[1][t] = half_value(u[4] >> 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                q[i] = u[1 + i] & 0x0f0f0f0fu, q[4 + i] = (u[1 + i] >> 4) & 0x0f0f0f0fu;
+                q[8 + i] = u[6 + i] & 0x0f0f0f0fu, q[12 + i] = (u[6 + i] >> 4) & 0x0f0f0f0fu;
+            }
+            S.wd[0][t] = half_value(u[0] & 0xffffu);
+            S.wm[0][t] = half_value(u[0] >> 16);
+            S.wd[1][t] = half_value(u[5] & 0xffffu);
+            S.wm[1][t] = half_value(u[5] >> 16);
+        }
+    }
+    if (t >= 64u && t < 192u) {
+        const uint32_t i = t - 64u;
+        S.sx[i & 1u][i >> 1] = L.sx;
+    }
+    if (t >= 128u) {
+        const uint32_t i = t - 128u;
+        ((int32_t*)S.ex[i & 1u])[i >> 1] = L.ex;
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_matmul_mfma(const uint8_t* __restrict__ w, Activations act,
+                                                     float* __restrict__ dst, const float* __restrict__ bias,
+                                                     uint32_t m, uint32_t n, uint32_t k) {
+    __shared__ MmStage stage[2];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t nb = k >> 5, pairs = nb >> 1;
+    const uint32_t n0 = blockIdx.x * MM_TILE, m0 = blockIdx.y * MM_TILE;
+    const uint32_t wm0 = (wave >> 1) * 32u, wn0 = (wave & 1u) * 32u;  // this wave's 32 x 32 within the tile
+    const uint32_t lr = lane & 15u, lq = lane >> 4;                    // operand row/column, k quarter
+
+    float acc[2][2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[a][b][i] = 0.0f;
+
+    // A operand rows (activation rows), clamped in bounds.
+    const int8_t* arow[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) arow[a] = act.qs + (size_t)min(m0 + wm0 + 16u * a + lr, m - 1u) * k + lq * 8u;
+
+    MmLoad<KIND> L;
+    stage_load<KIND>(w, act, n, m, nb, n0, m0, 0, L);
+    stage_store<KIND>(stage[0], L);
+    __syncthreads();
+
+    for (uint32_t pair = 0; pair < pairs; ++pair) {
+        const MmStage& S = stage[pair & 1u];
+        const bool more = pair + 1u < pairs;
+        if (more) stage_load<KIND>(w, act, n, m, nb, n0, m0, pair + 1u, L);
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+            const uint32_t blk = 2u * pair + h;
+            long av[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) av[a] = *(const __attribute__((address_space(1))) long*)(arow[a] + blk * 32u);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const uint32_t col = wn0 + 16u * b + lr;
+                const long bv = *(const long*)(S.wq + col * MM_BROW + h * 32u + lq * 8u);
+                const float d = S.wd[h][wn0 + 16u * b + lr];
+                float wmin = 0.0f;
+                if constexpr (KIND == 2) wmin = S.wm[h][wn0 + 16u * b + lr];
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    const uint32_t r0 = wm0 + 16u * a + 4u * lq;  // this lane's 4 rows within the tile
+                    v4i c = {0, 0, 0, 0};
+                    if constexpr (KIND == 1) {
+                        const int* e = (const int*)S.ex[h];
+                        c = v4i{e[r0], e[r0 + 1], e[r0 + 2], e[r0 + 3]};
+                    }
+                    const v4i tv = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[a], bv, c, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float sx = S.sx[h][r0 + i];
+                        float contribution;
+                        if constexpr (KIND == 0) {
+                            const float s = d * sx;
+                            contribution = (float)tv[i] * s;
+                        } else if constexpr (KIND == 1) {
+                            const float p = (float)tv[i] * d;
+                            contribution = p * sx;
+                        } else {
+                            const float s = d * sx;
+                            const float f = s * (float)tv[i];
+                            const float g = wmin * S.ex[h][r0 + i];
+                            contribution = f + g;
+                        }
+                        acc[a][b][i] += contribution;
+                    }
+                }
+            }
+        }
+        if (more) stage_store<KIND>(stage[(pair + 1u) & 1u], L);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint32_t col = n0 + wn0 + 16u * b + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t row = m0 + wm0 + 16u * a + 4u * lq + i;
+                if (row < m && col < n) dst[(size_t)row * n + col] = bias ? acc[a][b][i] + bias[col] : acc[a][b][i];
+            }
+        }
+}
+
 // ------------------------------------------------- thread per output
 
 // One thread per output, adding its blocks in order from byte loads: any
@@ -993,12 +1194,31 @@ hipError_t launch_row(uint32_t kind, const uint8_t* w, const float* x, float* ds
     return hipGetLastError();
 }
 
+template <int KIND>
+static hipError_t launch_mfma(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
+                              uint32_t n, uint32_t k, hipStream_t stream) {
+    const dim3 grid((n + MM_TILE - 1u) / MM_TILE, (rows + MM_TILE - 1u) / MM_TILE);
+    hipLaunchKernelGGL(k_matmul_mfma<KIND>, grid, dim3(256), 0, stream, w, act, dst, bias, rows, n, k);
+    return hipGetLastError();
+}
+
+// Activation rows from which AUTO takes the matrix cores rather than lanes.
+static constexpr uint32_t MATRIX_ROWS = 32;
+
 hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, Activations act, float* dst,
                                const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
                                hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
-    const bool thread = mode == 1u /* THREAD */ || !lanes_fit(w, k) ||
-                        (mode == 0u /* AUTO */ && (uint64_t)rows * n >= 65536u && rows > 16u);
+    const bool fits = lanes_fit(w, k);
+    const bool matrix = fits && (mode == 7u /* MATRIX */ || (mode == 0u /* AUTO */ && rows >= MATRIX_ROWS));
+    if (matrix) {
+        switch (kind) {
+        case 0: return launch_mfma<0>(w, act, dst, bias, rows, n, k, stream);
+        case 1: return launch_mfma<1>(w, act, dst, bias, rows, n, k, stream);
+        default: return launch_mfma<2>(w, act, dst, bias, rows, n, k, stream);
+        }
+    }
+    const bool thread = mode == 1u /* THREAD */ || !fits;
     switch (kind) {
     case 0:
         return thread ? launch_thread<0>(w, act, dst, bias, rows, n, k, stream)

@@ -336,3 +336,37 @@ def test_plan_equals_products_one_by_one(dev, fmt):
         want = wants[i] + (np.arange(3072, dtype=np.float32)[:n] * 0.25 if i == 2 else 0)
         assert np.array_equal(bits(got), bits(want.astype(np.float32))), shapes[i]
     plan.destroy()
+
+
+MATRIX_SHAPES = [
+    # (rows, n, k): config 4 prefill, ragged edges, short k, the 1.7B MLP
+    (512, 2048, 2048), (33, 100, 576), (64, 64, 64), (100, 130, 1024), (128, 8192, 2048), (40, 2048, 8192),
+]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("shape", MATRIX_SHAPES)
+def test_matrix_cores_bit_exact(dev, fmt, shape):
+    # The MFMA path (mode matrix, and auto from 32 rows) gives the host's bits.
+    rows, n, k = shape
+    say("matrix", fmt, rows, n, k)
+    wq = weights(fmt, n, k, 700 + rows + n)
+    x = acts(rows, k, 800 + rows)
+    want = oracle.matmul(fmt, x, wq, rows, n, k)
+    for mode in ("matrix", "auto"):
+        got = run_product(dev, fmt, wq, x, rows, n, k, mode=mode)
+        assert np.array_equal(bits(got), bits(want)), mode
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_matrix_cores_with_bias_and_slice(dev, fmt):
+    rows, n, k = 70, 96, 1280
+    rng = np.random.default_rng(5)
+    wq = oracle.quantize(fmt, rng.uniform(-1, 1, n * k).astype(np.float32))
+    x = rng.uniform(-3, 3, rows * k).astype(np.float32)
+    bias = rng.uniform(-1, 1, 40).astype(np.float32)
+    full = oracle.matmul_reference(fmt, x, wq, rows, n, k)
+    want = oracle.add_bias(np.ascontiguousarray(full[:, 30:70]), bias)
+    say("matrix slice", fmt)
+    got = run_product(dev, fmt, wq, x, rows, 40, k, mode="matrix", bias=bias, w_row=30)
+    assert np.array_equal(bits(got), bits(want))
