@@ -451,15 +451,18 @@ __device__ __forceinline__ TileGeo tile_geo(const RowProduct& p, uint32_t tile) 
 // step past the tile's last, or a row past the product's last, reads the
 // last one again -- so the loads are straight-line code and the compiler's
 // wait counts stay exact (loads complete in issue order).
+// With `idle` (a workgroup with no next tile: p and g are then this tile's),
+// every load reads this tile's last step again, fetched just before and
+// still in cache: the same loads are issued, none reaches HBM.
 template <int KIND, uint32_t D>
 __device__ __forceinline__ void load_steps(const RowProduct& p, const TileGeo& g, uint32_t s0,
-                                           uint32_t (&u)[D][Fmt<KIND>::PW]) {
+                                           uint32_t (&u)[D][Fmt<KIND>::PW], bool idle = false) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
     const uint32_t* wp = (const uint32_t*)p.w + (size_t)g.j * PW;
     const size_t row_words = (size_t)g.np * PW;
 #pragma unroll
     for (uint32_t d = 0; d < D; ++d) {
-        const uint32_t s = min(s0 + d, g.steps - 1u);
+        const uint32_t s = idle ? g.steps - 1u : min(s0 + d, g.steps - 1u);
         const uint32_t row = min(g.row0 + s * g.group_stride + g.load_rsub, p.n - 1u);
         load_pair<KIND>(wp + (size_t)row * row_words, u[d]);
     }
@@ -652,7 +655,7 @@ __device__ __forceinline__ void matvec_rows(const RowProduct* __restrict__ table
         compute_steps<KIND, D>(p, g, s0, ua, v, part);
         load_x(q.x, q.k, xv);
         const float nbias = load_bias(q, h);
-        load_steps<KIND, D>(q, h, 0, ua);
+        load_steps<KIND, D>(q, h, 0, ua, !more);
         compute_steps<KIND, D>(p, g, s0 + D, ub, v, part);
 
         __syncthreads();  // every contribution of this tile is in `part`
