@@ -206,3 +206,158 @@ def set_threads(threads: int, variant: str = "portable") -> None:
 
 def threads(variant: str = "portable") -> int:
     return lib(variant).tmo_threads()
+
+
+# ---------------------------------------------------------------- Llama (tmq_llama.c)
+
+class LlamaConfig(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int32), ("width", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("kv_heads", ctypes.c_int32), ("head_width", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("vocab", ctypes.c_int32), ("context", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("theta", ctypes.c_double), ("kind", ctypes.c_int32)]
+
+
+class LlamaWeights(ctypes.Structure):
+    _fields_ = [("embed", ctypes.c_void_p), ("head", ctypes.c_void_p), ("norm", ctypes.c_void_p),
+                ("attn_norm", ctypes.POINTER(ctypes.c_void_p)), ("ffn_norm", ctypes.POINTER(ctypes.c_void_p)),
+                ("qkv", ctypes.POINTER(ctypes.c_void_p)), ("o", ctypes.POINTER(ctypes.c_void_p)),
+                ("gate_up", ctypes.POINTER(ctypes.c_void_p)), ("down", ctypes.POINTER(ctypes.c_void_p))]
+
+
+def _llama_lib(variant="portable"):
+    so = lib(variant)
+    if not getattr(so, "_llama_ready", False):
+        P = ctypes.c_void_p
+        so.tmo_exp.restype = ctypes.c_float
+        so.tmo_exp.argtypes = [ctypes.c_float]
+        so.tmo_exp_many.argtypes = [P, ctypes.c_int64, P]
+        so.tmo_exp_many.restype = None
+        so.tmo_rmsnorm.argtypes = [P, P, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, P]
+        so.tmo_rmsnorm.restype = None
+        so.tmo_rope_tables.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_double, P, P]
+        so.tmo_rope_tables.restype = None
+        so.tmo_swiglu_many.argtypes = [P, P, ctypes.c_int64, P]
+        so.tmo_swiglu_many.restype = None
+        so.tmo_llama_new.restype = P
+        so.tmo_llama_new.argtypes = [ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaWeights)]
+        so.tmo_llama_free.argtypes = [P]
+        so.tmo_llama_free.restype = None
+        so.tmo_llama_reset.argtypes = [P]
+        so.tmo_llama_reset.restype = None
+        so.tmo_llama_length.argtypes = [P]
+        so.tmo_llama_length.restype = ctypes.c_int32
+        so.tmo_llama_forward.argtypes = [P, P, ctypes.c_int32, ctypes.c_int32, P]
+        so.tmo_llama_forward.restype = ctypes.c_int
+        so.tmo_argmax.argtypes = [P, ctypes.c_int32]
+        so.tmo_argmax.restype = ctypes.c_int32
+        so._llama_ready = True
+    return so
+
+
+def exp_many(x: np.ndarray) -> np.ndarray:
+    """Maths.exp, maths.cr:36-54, elementwise."""
+    v = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(v)
+    _llama_lib().tmo_exp_many(_ptr(v), v.size, _ptr(out))
+    return out
+
+
+def rmsnorm(x: np.ndarray, w, eps: float) -> np.ndarray:
+    """rmsnorm_row, host.cr:374-386, over the rows of x."""
+    v = np.ascontiguousarray(x, dtype=np.float32)
+    n = v.shape[-1]
+    out = np.empty_like(v)
+    wp = _ptr(np.ascontiguousarray(w, dtype=np.float32)) if w is not None else None
+    _llama_lib().tmo_rmsnorm(_ptr(v), wp, v.size // n, n, float(eps), _ptr(out))
+    return out
+
+
+def rope_tables(width: int, context: int, theta: float):
+    """RotaryEmbedding's cos/sin tables, modules.cr:344-351: [context, width] each."""
+    cos = np.empty((context, width), np.float32)
+    sin = np.empty((context, width), np.float32)
+    _llama_lib().tmo_rope_tables(width, context, float(theta), _ptr(cos), _ptr(sin))
+    return cos, sin
+
+
+def swiglu(gate: np.ndarray, value: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    v = np.ascontiguousarray(value, dtype=np.float32)
+    out = np.empty_like(g)
+    _llama_lib().tmo_swiglu_many(_ptr(g), _ptr(v), g.size, _ptr(out))
+    return out
+
+
+def argmax(logits: np.ndarray) -> int:
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(_llama_lib().tmo_argmax(_ptr(v), v.size))
+
+
+class Llama:
+    """The oracle's Llama forward on a host device (tmq_llama.c). Weights: a
+    dict of numpy arrays -- embed [vocab·row bytes] blocks, head (or None when
+    tied), norm [width], and per-layer lists attn_norm, ffn_norm, qkv, o,
+    gate_up, down (block bytes, q/k rows in Hugging Face order)."""
+
+    def __init__(self, config: dict, weights: dict, variant: str = "portable"):
+        self.so = _llama_lib(variant)
+        self.config = dict(config)
+        self._keep = []
+
+        def keep(a, dtype):
+            arr = np.ascontiguousarray(a, dtype=dtype)
+            self._keep.append(arr)
+            return arr.ctypes.data
+
+        def plist(arrays, dtype):
+            ptrs = (ctypes.c_void_p * len(arrays))(*[keep(a, dtype) for a in arrays])
+            self._keep.append(ptrs)
+            return ptrs
+
+        c = LlamaConfig(config["layers"], config["width"], config["heads"], config["kv_heads"],
+                        config["head_width"], config["hidden"], config["vocab"], config["context"],
+                        config["eps"], config["theta"], kind_of(config["kind"]))
+        embed = keep(weights["embed"], np.uint8)
+        head = keep(weights["head"], np.uint8) if weights.get("head") is not None else embed
+        w = LlamaWeights(embed, head, keep(weights["norm"], np.float32),
+                         plist(weights["attn_norm"], np.float32), plist(weights["ffn_norm"], np.float32),
+                         plist(weights["qkv"], np.uint8), plist(weights["o"], np.uint8),
+                         plist(weights["gate_up"], np.uint8), plist(weights["down"], np.uint8))
+        self._keep += [c, w]
+        self.handle = self.so.tmo_llama_new(ctypes.byref(c), ctypes.byref(w))
+
+    def forward(self, ids, last_only: bool = False) -> np.ndarray:
+        idx = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+        rows = 1 if last_only else idx.size
+        out = np.empty((rows, self.config["vocab"]), np.float32)
+        code = self.so.tmo_llama_forward(self.handle, _ptr(idx), idx.size, int(last_only), _ptr(out))
+        if code != 0:
+            raise ValueError(f"tmo_llama_forward failed ({code})")
+        return out
+
+    def reset(self) -> None:
+        self.so.tmo_llama_reset(self.handle)
+
+    @property
+    def length(self) -> int:
+        return self.so.tmo_llama_length(self.handle)
+
+    def generate(self, prompt, count: int):
+        """Generative#generate with the greedy sampler (generative.cr:177-190)."""
+        self.reset()
+        logits = self.forward(prompt, last_only=True)[0]
+        tokens = []
+        for i in range(count):
+            token = argmax(logits)
+            tokens.append(token)
+            if i < count - 1:
+                logits = self.forward([token], last_only=True)[0]
+        return tokens
+
+    def __del__(self):
+        try:
+            if self.handle:
+                self.so.tmo_llama_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass

@@ -1,0 +1,137 @@
+"""The oracle's Llama forward (oracle/tmq_llama.c), pinned by the reference's
+own model-level fixtures and invariants:
+
+* Maths.exp (maths.cr:36-54) within 2 ulp of the correctly rounded exp over
+  its range, with the special values its spec states (spec/maths_spec.cr);
+* the tiny_llama quantised GGUFs against the F32 PyTorch logits of
+  logits.json: Q8_0 strays less than a quarter of Q4_0's error
+  (block_matmul_spec.cr:275-284), and both stay close;
+* prefill gives the bits of one-by-one decode (block_matmul_spec.cr:253-260);
+* forward_last's row equals the full forward's last row;
+* RMSNorm, SwiGLU and the RoPE tables against float64 restatements of their
+  definitions (bounds, not retyped bits).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from llama_fixtures import random_llama, tiny_llama, tiny_llama_from_safetensors
+from oracle import oracle
+
+
+def ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    return np.abs(ia - ib)
+
+
+def test_exp_within_two_ulp_and_special_values():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-87.0, 88.7, 1 << 20), rng.uniform(-1, 1, 1 << 16),
+                        np.linspace(-87.3, 88.7, 100001)]).astype(np.float32)
+    got = oracle.exp_many(x)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    normal = want >= np.float32(1.1754944e-38)
+    assert ulp_distance(got[normal], want[normal]).max() <= 2
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 89.0, -88.0, np.nan], np.float32)
+    s = oracle.exp_many(special)
+    assert s[0] == 1 and s[1] == 1 and np.isinf(s[2]) and s[3] == 0 and np.isinf(s[4]) and s[5] == 0
+    assert np.isnan(s[6])
+
+
+def test_rmsnorm_swiglu_against_definitions():
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, (3, 2048)).astype(np.float32)
+    w = rng.normal(1, 0.1, 2048).astype(np.float32)
+    got = oracle.rmsnorm(x, w, 1e-5).astype(np.float64)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-5) * w
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    # a row of equal values: Σx²/n exact, root exact -> x / root exact
+    ones = np.full((1, 64), 2.0, np.float32)
+    assert np.all(oracle.rmsnorm(ones, None, 0.0) == 1.0)
+    g = rng.normal(0, 3, 10000).astype(np.float32)
+    v = rng.normal(0, 1, 10000).astype(np.float32)
+    gd = g.astype(np.float64)
+    want = gd / (np.exp(-gd) + 1) * v
+    assert np.allclose(oracle.swiglu(g, v), want, rtol=2e-6, atol=1e-7)
+
+
+def test_rope_tables_against_definition():
+    cos, sin = oracle.rope_tables(64, 2048, 10000.0)
+    p = np.arange(2048)[:, None].astype(np.float64)
+    i = np.arange(64)[None, :] % 32
+    freq = 1.0 / 10000.0 ** (2 * i / 64)
+    assert np.allclose(cos, np.cos(p * freq), atol=2e-4)  # angles are rounded to f32 first
+    assert np.allclose(sin, np.sin(p * freq), atol=2e-4)
+    assert np.all(cos[0] == 1) and np.all(sin[0] == 0)
+
+
+@pytest.fixture(scope="module")
+def fixture_logits(golden):
+    with open(os.path.join(golden, "tiny_llama", "logits.json")) as f:
+        return json.load(f)
+
+
+def test_tiny_llama_q8_0_strays_less_than_q4_0(golden, fixture_logits):
+    # block_matmul_spec.cr:275-284 on the oracle's forward.
+    prompt = fixture_logits["prompt_ids"]
+    reference = np.array(fixture_logits["logits"], np.float64)
+    errors = {}
+    for fmt in ("Q8_0", "Q4_0"):
+        config, weights = tiny_llama(golden, fmt)
+        model = oracle.Llama(config, weights)
+        logits = model.forward(prompt)
+        errors[fmt] = np.abs(logits - reference).mean()
+    assert errors["Q8_0"] < errors["Q4_0"] / 4
+    # and Q8_0 stays near the F32 model: a sign or index slip anywhere in the
+    # forward sends the error to the logits' own scale (mean |logit| ~1.4)
+    assert errors["Q8_0"] < 0.15
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0"])
+def test_gguf_equals_safetensors_quantised(golden, fixture_logits, fmt):
+    # block_matmul_spec.cr:243-250: the llama.cpp-permuted GGUF, unpermuted on
+    # load, equals the F32 model quantised here, in every weight byte and in
+    # the forward's bits; this pins the q/k row order.
+    config, from_gguf = tiny_llama(golden, fmt)
+    _, quantised = tiny_llama_from_safetensors(golden, fmt)
+    for name in ("embed", "head", "norm"):
+        assert np.array_equal(from_gguf[name], quantised[name]), name
+    for name in ("qkv", "o", "gate_up", "down", "attn_norm", "ffn_norm"):
+        for a, b in zip(from_gguf[name], quantised[name]):
+            assert np.array_equal(a, b), name
+    prompt = fixture_logits["prompt_ids"]
+    got = oracle.Llama(config, from_gguf).forward(prompt)
+    want = oracle.Llama(config, quantised).forward(prompt)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0"])
+def test_prefill_equals_one_by_one_decode(golden, fixture_logits, fmt):
+    # block_matmul_spec.cr:253-260
+    prompt = fixture_logits["prompt_ids"]
+    config, weights = tiny_llama(golden, fmt)
+    model = oracle.Llama(config, weights)
+    prefill = model.forward(prompt)
+    model.reset()
+    one_by_one = np.concatenate([model.forward([i]) for i in prompt])
+    assert np.array_equal(prefill.view(np.uint32), one_by_one.view(np.uint32))
+    model.reset()
+    last = model.forward(prompt, last_only=True)
+    assert np.array_equal(last[0].view(np.uint32), prefill[-1].view(np.uint32))
+
+
+def test_random_model_generates_deterministically():
+    config = dict(layers=2, width=128, heads=4, kv_heads=2, head_width=32, hidden=256, vocab=512, context=64,
+                  eps=1e-5, theta=10000.0, kind="Q4_0")
+    weights = random_llama(config, seed=3)
+    model = oracle.Llama(config, weights)
+    prompt = list(np.random.default_rng(4).integers(0, 512, 12))
+    a = model.generate(prompt, 20)
+    b = model.generate(prompt, 20)
+    assert a == b and len(a) == 20
