@@ -265,6 +265,127 @@ int tmh_plan_run(uint64_t plan);
 
 int tmh_plan_destroy(uint64_t plan);
 
+/* ------------------------------------------------- the rest of the decode graph
+ *
+ * The F32 ops a Llama decode step runs besides its products, each with the
+ * bits of the reference's host kernel for the op (the ops the reference's GPU
+ * devices leave to that host kernel, cuda.cr:395-415). All arrays are F32 in
+ * device memory unless stated; rows are dense unless a leading dimension is
+ * given. Kernel-detected index errors are reported at tmh_sync, as a gather's. */
+
+/* Op::RMSNorm, host.cr:374-386: dst[r] = x[r] / sqrt(Σ_j x[r,j]² / n + eps) · weight,
+ * the sum folded from 0 in index order. `weight` may be 0 (no weight). x rows
+ * are `ldx` apart; dst must not overlap x. */
+int tmh_rmsnorm(uint64_t x, uint32_t ldx, uint64_t weight, uint32_t rows, uint32_t n, float eps, uint64_t dst);
+
+/* Op::Rope (host.cr:448-466) of the q and k heads and Op::WriteRows
+ * (host.cr:586-597) of the rotated k and the v heads, for `tokens` rows of x
+ * (`ldx` apart) each holding [heads q | kv_heads k | kv_heads v] heads of
+ * `width` (a merged qkv product's output, modules.cr:484-493). Token t sits at
+ * slots[t] (int32, device) = cache row · capacity + position; its rotation is
+ * row `position` of the cos/sin tables ([table_rows, width], RotaryEmbedding,
+ * modules.cr:344-351). Writes q_dst [tokens, heads, width] and the caches
+ * keys/values [cache_rows, kv_heads, capacity, width]. A slot out of range is
+ * an index error. */
+int tmh_rope_write(uint64_t x, uint32_t ldx, uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t width,
+                   uint64_t cos, uint64_t sin, uint32_t table_rows, uint64_t slots, uint32_t cache_rows,
+                   uint32_t capacity, uint64_t q_dst, uint64_t keys, uint64_t values);
+
+/* Attention of `tokens` query rows against the caches, with the bits of
+ * host.cr:408-440 (Op::Attention; the composite of composite.cr:190-199 and
+ * Op::RaggedAttention have the same): per token and head, scores q·k_p in
+ * column order, · scale, -inf past the token's last position, the first
+ * highest, Maths.exp(x - top), their total in position order, then
+ * Σ_p (e_p / total)·v_p in position order. Query head h reads kv head
+ * h / (heads / kv_heads). `table` (int32, device) holds per token its cache
+ * row, the last position it sees and the positions its row holds
+ * (composite.cr:201-212). q rows are `ldq` apart ([heads, width] each), dst
+ * rows `ld_dst` apart. width must be a multiple of 4; capacity at most 16,000. */
+int tmh_attention(uint64_t q, uint32_t ldq, uint32_t tokens, uint32_t heads, uint64_t keys, uint64_t values,
+                  uint32_t cache_rows, uint32_t kv_heads, uint32_t capacity, uint32_t width, uint64_t table,
+                  float scale, uint64_t dst, uint32_t ld_dst);
+
+/* SwiGLU, kernels.cr:18: dst[r, j] = gate[r, j] / (Maths.exp(-gate[r, j]) + 1) · value[r, j];
+ * gate and value rows `ld` apart (the two halves of a merged gate_up row,
+ * modules.cr:515-522), dst dense [rows, n]. */
+int tmh_swiglu(uint64_t gate, uint64_t value, uint32_t ld, uint32_t rows, uint32_t n, uint64_t dst);
+
+/* Binary Add of two dense F32 arrays, host.cr:159-180: dst = a + b (dst may be a). */
+int tmh_add(uint64_t a, uint64_t b, uint64_t dst, uint64_t count);
+
+/* Sampler.greedy, sampler.cr:35-36: ids[r] (int32, device) = the first index
+ * of the highest value of row r (rows `ldx` apart). */
+int tmh_argmax(uint64_t x, uint32_t ldx, uint32_t rows, uint32_t n, uint64_t ids);
+
+/* ------------------------------------------------------------ Llama decoding
+ *
+ * A Llama whose forward runs entirely on the device: Llama#forward /
+ * #forward_last and Generative#generate with the greedy sampler
+ * (llama.cr:256-303, generative.cr:155-190) over `rows` sequences, each with
+ * a KV cache row of `capacity` positions. Every product and op is one of the
+ * entry points above (tmh_block_matmul's kernels, tmh_gather_blocks,
+ * tmh_rmsnorm, tmh_rope_write, tmh_attention, tmh_swiglu, tmh_add,
+ * tmh_argmax), so the logits and tokens are the host's bits. A decode step
+ * keeps its state (ids, slots, attention table) on the device, so steps can
+ * be replayed from one captured HIP graph without host round trips. */
+
+typedef struct tmh_llama_config {
+    int32_t layers, width, heads, kv_heads, head_width, hidden, vocab, context;
+    float eps;    /* RMSNorm epsilon */
+    double theta; /* RoPE base */
+    uint32_t kind; /* TMH_Q8_0 / TMH_Q4_0 / TMH_Q4_1: every matrix and the embedding table */
+} tmh_llama_config;
+
+/* Device addresses of the weights, which stay the caller's: the embedding
+ * table [vocab, width] blocks; the head [vocab, width] blocks (0: tied to the
+ * embedding); the final norm [width]; and per layer (arrays of `layers`
+ * addresses) the norms [width], the merged qkv [(heads + 2·kv_heads)·head_width,
+ * width] with q and k rows in Hugging Face order (llama.cr:226-235), o
+ * [width, heads·head_width], the merged gate_up [2·hidden, width] and down
+ * [width, hidden]. The arrays are read during tmh_llama_create only. */
+typedef struct tmh_llama_weights {
+    uint64_t embed, head, norm;
+    const uint64_t* attn_norm;
+    const uint64_t* ffn_norm;
+    const uint64_t* qkv;
+    const uint64_t* o;
+    const uint64_t* gate_up;
+    const uint64_t* down;
+} tmh_llama_weights;
+
+/* Makes a decoder for `rows` sequences of at most `capacity` positions
+ * (≤ context), running at most `max_tokens` tokens per forward. Allocates its
+ * caches, activations and rotation tables (RotaryEmbedding's, in F32 by
+ * powf/cosf/sinf). */
+int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* weights, uint32_t rows,
+                     uint32_t capacity, uint32_t max_tokens, uint64_t* model);
+
+/* Runs `count` ids (host int32) of sequence `row` at the positions after its
+ * cached ones and appends their keys and values (Generative#forward,
+ * generative.cr:155-160); with `last_only`, only the last position's final
+ * norm and head run (#forward_last, 162-172). Writes the logits, [count or 1,
+ * vocab], to `logits` (host) unless it is null. Waits for the device. */
+int tmh_llama_forward(uint64_t model, uint32_t row, const int32_t* ids, uint32_t count, uint32_t last_only,
+                      float* logits);
+
+/* Greedy generation for every row at once (Generative#generate with
+ * Sampler.greedy, generative.cr:177-190): from each row's last forward's
+ * logits, `steps` tokens per row, each chosen then run as the row's next
+ * position (the last one chosen is not run). Writes tokens[row·steps + i]
+ * (host). With `graph`, each decode step is one launch of a HIP graph
+ * captured on first use. Every row must have run a forward first. */
+int tmh_llama_generate(uint64_t model, uint32_t steps, int32_t* tokens, uint32_t graph);
+
+/* Positions held by `row`'s cache; and emptying it (Cache#reset, modules.cr:157-161). */
+int tmh_llama_length(uint64_t model, uint32_t row, int32_t* length);
+int tmh_llama_reset(uint64_t model, uint32_t row);
+
+/* Queues one decode step of every row with the device-held state, for timing
+ * (the step tmh_llama_generate repeats); `graph` as there. Does not wait. */
+int tmh_llama_step(uint64_t model, uint32_t graph);
+
+int tmh_llama_destroy(uint64_t model);
+
 #ifdef __cplusplus
 }
 #endif

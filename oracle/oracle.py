@@ -250,6 +250,11 @@ def _llama_lib(variant="portable"):
         so.tmo_llama_forward.restype = ctypes.c_int
         so.tmo_argmax.argtypes = [P, ctypes.c_int32]
         so.tmo_argmax.restype = ctypes.c_int32
+        I = ctypes.c_int32
+        so.tmo_attention.argtypes = [P, I, I, P, P, I, I, I, P, ctypes.c_float, P]
+        so.tmo_attention.restype = None
+        so.tmo_rope.argtypes = [P, I, I, I, I, P, P, P, P]
+        so.tmo_rope.restype = None
         so._llama_ready = True
     return so
 
@@ -291,6 +296,37 @@ def swiglu(gate: np.ndarray, value: np.ndarray) -> np.ndarray:
 def argmax(logits: np.ndarray) -> int:
     v = np.ascontiguousarray(logits, dtype=np.float32)
     return int(_llama_lib().tmo_argmax(_ptr(v), v.size))
+
+
+def attention(q: np.ndarray, keys: np.ndarray, values: np.ndarray, table, scale: float) -> np.ndarray:
+    """The Attention op on a host device (host.cr:408-440): q [tokens, heads,
+    width]; keys/values [rows, kv_heads, capacity, width]; table [tokens, 3] of
+    (cache row, last position seen, positions held)."""
+    qv = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.float32)
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    t = np.ascontiguousarray(table, dtype=np.int32).reshape(-1, 3)
+    tokens, heads, width = qv.shape
+    rows, kv_heads, capacity, _ = k.shape
+    assert t.shape[0] == tokens and np.all((t[:, 0] >= 0) & (t[:, 0] < rows))
+    assert np.all((t[:, 2] > 0) & (t[:, 2] <= capacity) & (t[:, 1] >= 0) & (t[:, 1] < t[:, 2]))
+    out = np.empty_like(qv)
+    _llama_lib().tmo_attention(_ptr(qv), tokens, heads, _ptr(k), _ptr(v), kv_heads, capacity, width, _ptr(t),
+                               float(scale), _ptr(out))
+    return out
+
+
+def rope(x: np.ndarray, heads: int, width: int, cos: np.ndarray, sin: np.ndarray, positions) -> np.ndarray:
+    """The Rope op (host.cr:448-466) on the first `heads` heads of each row of
+    x [tokens, ≥ heads·width], row t at table row positions[t]: [tokens, heads, width]."""
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    c = np.ascontiguousarray(cos, dtype=np.float32)
+    s_ = np.ascontiguousarray(sin, dtype=np.float32)
+    assert np.all((pos >= 0) & (pos < c.shape[0]))
+    out = np.empty((xv.shape[0], heads, width), np.float32)
+    _llama_lib().tmo_rope(_ptr(xv), xv.shape[1], xv.shape[0], heads, width, _ptr(c), _ptr(s_), _ptr(pos), _ptr(out))
+    return out
 
 
 class Llama:

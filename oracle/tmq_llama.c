@@ -14,8 +14,9 @@
  *     q, k = rope(q), rope(k) at their positions    host.cr:448-466; tables modules.cr:344-351
  *     cache[past...] = k, v                         Tensor#write (Cache#append, modules.cr:164-176)
  *     scores = q · kᵀ (index order), softmax(scale, mask), · v
- *                                                   Tensor.attention composite, composite.cr:190-199;
- *                                                   matmul host.cr:700-721; softmax host.cr:363-383
+ *                                                   the Attention op, host.cr:408-440 (the composite
+ *                                                   of composite.cr:190-199 rounds alike: matmul
+ *                                                   host.cr:700-721, softmax host.cr:363-383)
  *     x = x + attended · Woᵀ                        binary Add, host.cr:159-180
  *     h = rmsnorm(x) · w2; gu = h · Wguᵀ
  *     x = x + swiglu(gate, up) · Wdownᵀ             kernels.cr:18 (gate / (exp(-gate) + 1) · up)
@@ -194,46 +195,57 @@ int32_t tmo_llama_length(const tmo_llama* m) { return m->length; }
 const float* tmo_llama_cos(const tmo_llama* m) { return m->cos; }
 const float* tmo_llama_sin(const tmo_llama* m) { return m->sin; }
 
-/* Attention of `count` new rows of one layer after `past` cached positions,
- * the composite of composite.cr:190-199 on a host device: for query head h
- * (key head h / group) and row i, scores[p] = (q · k_p) in index order, then
- * scaled_softmax_row (x·scale, + mask: 0 or -inf, max, exp(x - max) summed
- * in order, each / total), then out[c] = Σ_p w[p] · v[p][c] in order. */
-static void attention(const tmo_llama* m, int32_t layer, const float* q, int32_t count, int32_t past, float* out) {
-    const tmo_llama_config* c = &m->c;
-    int32_t hw = c->head_width, group = c->heads / c->kv_heads, positions = past + count;
-    float scale = (float)(1.0 / sqrt((double)hw));
-    const float* keys = m->keys + (size_t)layer * c->kv_heads * c->context * hw;
-    const float* values = m->values + (size_t)layer * c->kv_heads * c->context * hw;
-    float* scores = malloc(sizeof(float) * (size_t)positions);
-    for (int32_t h = 0; h < c->heads; h++) {
-        int32_t kv = h / group;
-        const float* kh = keys + (size_t)kv * c->context * hw;
-        const float* vh = values + (size_t)kv * c->context * hw;
-        for (int32_t i = 0; i < count; i++) {
-            const float* qi = q + ((size_t)i * c->heads + h) * hw;
+/* The Attention op on a host device, host.cr:408-440, for `tokens` packed
+ * query rows q [tokens, heads, width] against caches [rows, kv_heads,
+ * capacity, width]: token t reads cache row table[3t] up to table[3t+2]
+ * positions and sees positions up to table[3t+1] (the causal mask,
+ * composite.cr:282-290). Per head h (kv head h / group): scores[p] = (q · k_p)
+ * in column order, · scale, + mask (-inf past the last seen position), top =
+ * the first highest, e_p = Maths.exp(scores[p] - top), total in position
+ * order, out[c] = Σ_p (e_p / total) · v_p[c] in position order. */
+void tmo_attention(const float* q, int32_t tokens, int32_t heads, const float* keys, const float* values,
+                   int32_t kv_heads, int32_t capacity, int32_t width, const int32_t* table, float scale, float* out) {
+    int32_t group = heads / kv_heads;
+    float* scores = malloc(sizeof(float) * (size_t)capacity);
+    for (int32_t t = 0; t < tokens; t++) {
+        int32_t row = table[3 * t], last = table[3 * t + 1], positions = table[3 * t + 2];
+        for (int32_t h = 0; h < heads; h++) {
+            int32_t kv = h / group;
+            const float* kh = keys + ((size_t)row * kv_heads + kv) * capacity * width;
+            const float* vh = values + ((size_t)row * kv_heads + kv) * capacity * width;
+            const float* qi = q + ((size_t)t * heads + h) * width;
+            float top = 0.0f;
             for (int32_t p = 0; p < positions; p++) {
                 float dot = 0.0f;
-                for (int32_t col = 0; col < hw; col++) dot += qi[col] * kh[(size_t)p * hw + col];
+                for (int32_t col = 0; col < width; col++) dot += qi[col] * kh[(size_t)p * width + col];
                 float x = dot * scale;
-                float mask = p > i + past ? -INFINITY : 0.0f;
-                scores[p] = x + mask;
+                float mask = p > last ? -INFINITY : 0.0f;
+                x = x + mask;
+                scores[p] = x;
+                if (p == 0 || x > top) top = x;
             }
-            float top = scores[0];
-            for (int32_t p = 1; p < positions; p++) top = scores[p] > top ? scores[p] : top;
-            for (int32_t p = 0; p < positions; p++) scores[p] = tmo_exp(scores[p] - top);
             float total = 0.0f;
-            for (int32_t p = 0; p < positions; p++) total += scores[p];
-            for (int32_t p = 0; p < positions; p++) scores[p] = scores[p] / total;
-            float* oi = out + ((size_t)i * c->heads + h) * hw;
-            for (int32_t col = 0; col < hw; col++) {
+            for (int32_t p = 0; p < positions; p++) total += (scores[p] = tmo_exp(scores[p] - top));
+            float* oi = out + ((size_t)t * heads + h) * width;
+            for (int32_t col = 0; col < width; col++) {
                 float acc = 0.0f;
-                for (int32_t p = 0; p < positions; p++) acc += scores[p] * vh[(size_t)p * hw + col];
+                for (int32_t p = 0; p < positions; p++) acc += scores[p] / total * vh[(size_t)p * width + col];
                 oi[col] = acc;
             }
         }
     }
     free(scores);
+}
+
+/* The Rope op, host.cr:448-466, on `heads` heads of `width` per token (token
+ * rows `ldx` apart), token t rotated by table row positions[t]; out is
+ * [tokens, heads, width]. */
+void tmo_rope(const float* x, int32_t ldx, int32_t tokens, int32_t heads, int32_t width, const float* cos,
+              const float* sin, const int32_t* positions, float* out) {
+    for (int32_t t = 0; t < tokens; t++)
+        for (int32_t h = 0; h < heads; h++)
+            rope_row(x + (size_t)t * ldx + (size_t)h * width, width, cos + (size_t)positions[t] * width,
+                     sin + (size_t)positions[t] * width, out + ((size_t)t * heads + h) * width);
 }
 
 /* Llama#logits then #head (llama.cr:265-303) for `count` new ids after the
@@ -244,6 +256,8 @@ int tmo_llama_forward(tmo_llama* m, const int32_t* ids, int32_t count, int32_t l
     const tmo_llama_config* c = &m->c;
     int32_t past = m->length;
     if (count <= 0 || past + count > c->context) return -1;
+    for (int32_t i = 0; i < count; i++)
+        if (ids[i] < 0 || ids[i] >= c->vocab) return -2;
     int32_t W = c->width, hw = c->head_width, H = c->hidden;
     int32_t qn = c->heads * hw, kvn = c->kv_heads * hw, nqkv = qn + 2 * kvn;
     int64_t row_bytes = (int64_t)W / 32 * tmo_block_bytes(c->kind);
@@ -255,8 +269,12 @@ int tmo_llama_forward(tmo_llama* m, const int32_t* ids, int32_t count, int32_t l
     float* o = malloc(sizeof(float) * (size_t)count * W);
     float* gu = malloc(sizeof(float) * (size_t)count * 2 * H);
     float* a = malloc(sizeof(float) * (size_t)count * H);
+    int32_t* table = malloc(sizeof(int32_t) * 3 * (size_t)count);
+    float scale = (float)(1.0 / sqrt((double)hw));
     for (int32_t i = 0; i < count; i++) {
-        if (ids[i] < 0 || ids[i] >= c->vocab) return -2;
+        table[3 * i] = 0;
+        table[3 * i + 1] = past + i;
+        table[3 * i + 2] = past + count;
         tmo_dequantize(c->kind, m->w.embed + ids[i] * row_bytes, W, x + (size_t)i * W);
     }
     for (int32_t layer = 0; layer < c->layers; layer++) {
@@ -275,7 +293,7 @@ int tmo_llama_forward(tmo_llama* m, const int32_t* ids, int32_t count, int32_t l
                 memcpy(values + ((size_t)kv * c->context + pos) * hw, row + qn + kvn + kv * hw, sizeof(float) * hw);
             }
         }
-        attention(m, layer, q, count, past, att);
+        tmo_attention(q, count, c->heads, keys, values, c->kv_heads, c->context, hw, table, scale, att);
         tmo_matmul(c->kind, att, m->w.o[layer], count, W, qn, o);
         for (int64_t j = 0; j < (int64_t)count * W; j++) x[j] = x[j] + o[j];
         tmo_rmsnorm(x, m->w.ffn_norm[layer], count, W, c->eps, h);
@@ -299,6 +317,7 @@ int tmo_llama_forward(tmo_llama* m, const int32_t* ids, int32_t count, int32_t l
     free(o);
     free(gu);
     free(a);
+    free(table);
     return 0;
 }
 

@@ -1,5 +1,7 @@
-// Declarations shared by the runtime (tmh_runtime.hip) and the kernels
-// (tmh_kernels.hip) of libtensomite_hip.so. Not part of the C ABI.
+// Declarations shared by the sources of libtensomite_hip.so: the runtime
+// (tmh_runtime.hip), the product kernels (tmh_kernels.hip), the decode-graph
+// kernels (tmh_decode.hip) and the decoder (tmh_llama.hip). Not part of the
+// C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -66,5 +68,74 @@ hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* o
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);
+
+// ------------------------------------------------- the rest of the decode graph
+// (tmh_decode.hip)
+
+// RMSNorm of `rows` rows of n (x rows ldx apart, dst rows ld_dst apart);
+// `w` may be null (no weight).
+hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
+                          float* dst, uint32_t ld_dst, hipStream_t stream);
+
+// RoPE of q and k heads and the cache write of k and v, for tokens whose
+// rows of `x` hold [heads q | kv_heads k | kv_heads v] of `width` each.
+struct RopeWrite {
+    const float* x;
+    uint32_t ldx;
+    uint32_t heads, kv_heads, width;
+    const float* cos;  // [capacity or more, width]
+    const float* sin;
+    const int32_t* slots;  // per token: cache row · capacity + position
+    uint32_t cache_rows, capacity;
+    float* q_dst;   // [tokens, heads, width]
+    float* keys;    // [cache_rows, kv_heads, capacity, width]
+    float* values;  // likewise
+    int32_t* errors;
+};
+hipError_t launch_rope_write(const RopeWrite& a, uint32_t tokens, hipStream_t stream);
+
+// Attention of `tokens` query rows of `heads` heads against the cache; per
+// token the table holds (cache row, last position it sees, positions held).
+struct Attention {
+    const float* q;
+    uint32_t ldq;  // token t's heads start at q + t·ldq
+    const float* keys;
+    const float* values;
+    uint32_t cache_rows, kv_heads, capacity, width, heads;
+    const int32_t* table;
+    float scale;
+    float* dst;
+    uint32_t ld_dst;
+    int32_t* errors;
+};
+size_t attention_lds(uint32_t width, uint32_t capacity);
+hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream);
+
+hipError_t launch_swiglu(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n, float* dst,
+                         hipStream_t stream);
+hipError_t launch_add(const float* a, const float* b, float* dst, uint32_t count, hipStream_t stream);
+hipError_t launch_argmax(const float* x, uint32_t ldx, uint32_t rows, uint32_t n, int32_t* ids, hipStream_t stream);
+hipError_t launch_advance(uint32_t rows, const int32_t* chosen, int32_t* log, uint32_t log_stride, int32_t* steps,
+                          int32_t* slots, int32_t* table, uint32_t capacity, hipStream_t stream);
+
+// ------------------------------------------------- the runtime, for other sources
+
+// The calling thread's device: its ordered stream, compute units and error
+// buffer; returns a TMH_* code (0 on success).
+struct DeviceContext {
+    int index;
+    hipStream_t stream;
+    int compute_units;
+    int32_t* errors;
+};
+int device_context(DeviceContext* out, bool kernels);
+// Marks the error buffer as possibly written, for the next sync to check,
+// and counts `ops` kernel ops.
+void note_launch(int index, int ops, bool errors);
+// Device allocation honouring the allocation-failure test hook.
+hipError_t device_malloc(void** p, size_t bytes);
+// Bytes the quantise pass writes for `rows` rows of k, and its carving.
+size_t scratch_need(uint32_t rows, uint32_t k);
+Activations carve_scratch(uint8_t* base, uint32_t rows, uint32_t k);
 
 }  // namespace tmh

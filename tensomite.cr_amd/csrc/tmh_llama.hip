@@ -1,0 +1,558 @@
+// The C ABI of the decode-graph ops (tmh_rmsnorm ... tmh_argmax) and the
+// device-resident Llama decoder (tmh_llama_*): Llama#forward,
+// #forward_last and Generative#generate (src/tensomite/models/llama.cr:256-303,
+// generative.cr:155-190) as a fixed sequence of this library's launches.
+//
+// The decoder keeps everything a step reads on the device -- the ids to run,
+// each token's cache slot and attention entry -- and a step ends by choosing
+// the next ids and moving those entries on, so consecutive steps need no host
+// round trip and one captured HIP graph replays any number of them.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/tensomite_hip.h"
+#include "tmh_internal.h"
+
+namespace {
+
+using tmh::DeviceContext;
+
+int code(hipError_t e) { return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : (int)e; }
+
+constexpr uint32_t ATTENTION_CAPACITY = 16000;
+
+int check_rope(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t table_rows, uint32_t capacity) {
+    if (width == 0 || width % 2u != 0 || heads == 0 || kv_heads == 0 || capacity == 0) return TMH_ERROR_SHAPE;
+    if (capacity > table_rows) return TMH_ERROR_SHAPE;
+    return TMH_SUCCESS;
+}
+
+int check_attention(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t capacity) {
+    if (width == 0 || width % 4u != 0 || heads == 0 || kv_heads == 0 || heads % kv_heads != 0) return TMH_ERROR_SHAPE;
+    if (capacity == 0 || capacity > ATTENTION_CAPACITY) return TMH_ERROR_SHAPE;
+    return TMH_SUCCESS;
+}
+
+// ------------------------------------------------------------------ decoder
+
+struct Llama {
+    int device = 0;
+    tmh_llama_config c{};
+    uint32_t rows = 0, capacity = 0, max_tokens = 0;
+    uint32_t qn = 0, kvn = 0, nqkv = 0;
+    size_t row_bytes = 0;  // bytes of one weight row of `width` inputs
+
+    // weights (the caller's)
+    const uint8_t* embed = nullptr;
+    const uint8_t* head = nullptr;
+    const float* norm = nullptr;
+    std::vector<const float*> attn_norm, ffn_norm;
+    std::vector<const uint8_t*> qkv, o, gate_up, down;
+
+    // device memory (one allocation), carved below
+    uint8_t* memory = nullptr;
+    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *q = nullptr, *att = nullptr, *o_out = nullptr;
+    float *gu = nullptr, *act = nullptr, *logits = nullptr;
+    float *cos = nullptr, *sin = nullptr;
+    float *keys = nullptr, *values = nullptr;  // [layers][rows][kv_heads][capacity][head_width]
+    int32_t *ids = nullptr, *slots = nullptr, *table = nullptr, *steps = nullptr, *log = nullptr;
+    uint8_t* scratch = nullptr;
+    size_t layer_cache = 0;  // floats of one layer's keys
+
+    std::vector<int32_t> length;   // positions held, per row
+    std::vector<char> has_logits;  // whether row r's logits row holds its last forward's
+    bool generating = false;       // the device state continues a generation
+
+    hipGraphExec_t graph = nullptr;
+};
+
+// One product x[rows, k] · wᵀ (+ addend) into dst: the fused one-row kernel
+// for a single row, else the quantise pass into the decoder's scratch and
+// the product kernel. With `addend` == dst the product adds itself into dst
+// (one row only: the bias is per output, shared by rows).
+hipError_t product(const Llama& m, const DeviceContext& ctx, const uint8_t* w, const float* xin, uint32_t rows,
+                   uint32_t n, uint32_t k, float* dst, const float* addend) {
+    if (rows == 1 && tmh::row_kernel_fits(TMH_MODE_AUTO, w, k))
+        return tmh::launch_row(m.c.kind, w, xin, dst, addend, n, k, ctx.compute_units, ctx.stream);
+    tmh::Activations a = tmh::carve_scratch(m.scratch, rows, k);
+    hipError_t e = tmh::launch_quantize(xin, k, rows, k, (float*)a.scales, (float*)a.sums, (int32_t*)a.totals,
+                                        (int8_t*)a.qs, ctx.stream);
+    if (e != hipSuccess) return e;
+    return tmh::launch_block_matmul(m.c.kind, TMH_MODE_AUTO, w, a, dst, addend, rows, n, k, ctx.compute_units,
+                                    ctx.stream);
+}
+
+// Residual: x[rows] += x_in · wᵀ, as the host's `x + product` (one rounding
+// per element either way round).
+hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, const float* xin, uint32_t rows,
+                    uint32_t n, uint32_t k) {
+    if (rows == 1) return product(m, ctx, w, xin, 1, n, k, m.x, m.x);
+    hipError_t e = product(m, ctx, w, xin, rows, n, k, m.o_out, nullptr);
+    if (e != hipSuccess) return e;
+    return tmh::launch_add(m.x, m.o_out, m.x, rows * n, ctx.stream);
+}
+
+// The forward of `tokens` ids already on the device (m.ids), whose slots
+// and attention entries are on the device too; then the final norm and the
+// head over `final_rows` rows from x row `final_from`, into logits rows from
+// `logits_row`.
+hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tokens, uint32_t final_from,
+                          uint32_t final_rows, uint32_t logits_row) {
+    const tmh_llama_config& c = m.c;
+    const uint32_t W = (uint32_t)c.width, H = (uint32_t)c.hidden, hw = (uint32_t)c.head_width;
+    hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x, ctx.errors, ctx.stream);
+    const float scale = (float)(1.0 / std::sqrt((double)hw));
+    for (int32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
+        float* keys = m.keys + (size_t)l * m.layer_cache;
+        float* values = m.values + (size_t)l * m.layer_cache;
+        e = tmh::launch_rmsnorm(m.x, W, m.attn_norm[l], tokens, W, c.eps, m.h, W, ctx.stream);
+        if (e == hipSuccess) e = product(m, ctx, m.qkv[l], m.h, tokens, m.nqkv, W, m.qkv_out, nullptr);
+        if (e == hipSuccess) {
+            tmh::RopeWrite r{m.qkv_out, m.nqkv, (uint32_t)c.heads, (uint32_t)c.kv_heads, hw, m.cos, m.sin,
+                             m.slots, m.rows, m.capacity, m.q, keys, values, ctx.errors};
+            e = tmh::launch_rope_write(r, tokens, ctx.stream);
+        }
+        if (e == hipSuccess) {
+            tmh::Attention a{m.q, m.qn, keys, values, m.rows, (uint32_t)c.kv_heads, m.capacity, hw,
+                             (uint32_t)c.heads, m.table, scale, m.att, m.qn, ctx.errors};
+            e = tmh::launch_attention(a, tokens, ctx.stream);
+        }
+        if (e == hipSuccess) e = residual(m, ctx, m.o[l], m.att, tokens, W, m.qn);
+        if (e == hipSuccess) e = tmh::launch_rmsnorm(m.x, W, m.ffn_norm[l], tokens, W, c.eps, m.h, W, ctx.stream);
+        if (e == hipSuccess) e = product(m, ctx, m.gate_up[l], m.h, tokens, 2u * H, W, m.gu, nullptr);
+        if (e == hipSuccess) e = tmh::launch_swiglu(m.gu, m.gu + H, 2u * H, tokens, H, m.act, ctx.stream);
+        if (e == hipSuccess) e = residual(m, ctx, m.down[l], m.act, tokens, W, H);
+    }
+    if (e == hipSuccess)
+        e = tmh::launch_rmsnorm(m.x + (size_t)final_from * W, W, m.norm, final_rows, W, c.eps, m.h, W, ctx.stream);
+    if (e == hipSuccess)
+        e = product(m, ctx, m.head, m.h, final_rows, (uint32_t)c.vocab, W, m.logits + (size_t)logits_row * c.vocab,
+                    nullptr);
+    return e;
+}
+
+// One decode step of every row from the device-held state: run each row's
+// chosen id, choose the next, log it and move the row on.
+hipError_t decode_step(const Llama& m, const DeviceContext& ctx) {
+    hipError_t e = forward_tokens(m, ctx, m.rows, 0, m.rows, 0);
+    if (e == hipSuccess) e = tmh::launch_argmax(m.logits, (uint32_t)m.c.vocab, m.rows, (uint32_t)m.c.vocab, m.ids, ctx.stream);
+    if (e == hipSuccess)
+        e = tmh::launch_advance(m.rows, m.ids, m.log, m.capacity, m.steps, m.slots, m.table, m.capacity, ctx.stream);
+    return e;
+}
+
+int run_step(Llama& m, const DeviceContext& ctx, bool graph) {
+    if (!graph) return code(decode_step(m, ctx));
+    if (!m.graph) {
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamBeginCapture(ctx.stream, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return code(e);
+        hipError_t step = decode_step(m, ctx);
+        e = hipStreamEndCapture(ctx.stream, &g);
+        if (step != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return code(step);
+        }
+        if (e != hipSuccess) return code(e);
+        e = hipGraphInstantiate(&m.graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m.graph = nullptr;
+            return code(e);
+        }
+    }
+    return code(hipGraphLaunch(m.graph, ctx.stream));
+}
+
+Llama* model_of(uint64_t handle, const DeviceContext& ctx, int* err) {
+    Llama* m = (Llama*)handle;
+    if (!m) {
+        *err = TMH_ERROR_INVALID_VALUE;
+        return nullptr;
+    }
+    if (m->device != ctx.index) {
+        *err = TMH_ERROR_INVALID_VALUE;
+        return nullptr;
+    }
+    *err = TMH_SUCCESS;
+    return m;
+}
+
+size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
+
+}  // namespace
+
+extern "C" {
+
+// ----------------------------------------------------------------- the ops
+
+int tmh_rmsnorm(uint64_t x, uint32_t ldx, uint64_t weight, uint32_t rows, uint32_t n, float eps, uint64_t dst) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if (n == 0 || ldx < n) return TMH_ERROR_SHAPE;
+    if (rows == 0) return TMH_SUCCESS;
+    if (!x || !dst) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)rows * ldx > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    hipError_t e = tmh::launch_rmsnorm((const float*)x, ldx, (const float*)weight, rows, n, eps, (float*)dst, n,
+                                       ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, false);
+    return code(e);
+}
+
+int tmh_rope_write(uint64_t x, uint32_t ldx, uint32_t tokens, uint32_t heads, uint32_t kv_heads, uint32_t width,
+                   uint64_t cos, uint64_t sin, uint32_t table_rows, uint64_t slots, uint32_t cache_rows,
+                   uint32_t capacity, uint64_t q_dst, uint64_t keys, uint64_t values) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if ((err = check_rope(heads, kv_heads, width, table_rows, capacity)) != TMH_SUCCESS) return err;
+    if (ldx < (heads + 2u * kv_heads) * width || cache_rows == 0) return TMH_ERROR_SHAPE;
+    if (tokens == 0) return TMH_SUCCESS;
+    if (!x || !cos || !sin || !slots || !q_dst || !keys || !values) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)tokens * (heads + 2u * kv_heads) * width > 0x7fffffffull ||
+        (uint64_t)cache_rows * capacity > 0x7fffffffull)
+        return TMH_ERROR_SHAPE;
+    tmh::RopeWrite a{(const float*)x, ldx, heads, kv_heads, width, (const float*)cos, (const float*)sin,
+                     (const int32_t*)slots, cache_rows, capacity, (float*)q_dst, (float*)keys, (float*)values,
+                     ctx.errors};
+    hipError_t e = tmh::launch_rope_write(a, tokens, ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, true);
+    return code(e);
+}
+
+int tmh_attention(uint64_t q, uint32_t ldq, uint32_t tokens, uint32_t heads, uint64_t keys, uint64_t values,
+                  uint32_t cache_rows, uint32_t kv_heads, uint32_t capacity, uint32_t width, uint64_t table,
+                  float scale, uint64_t dst, uint32_t ld_dst) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if ((err = check_attention(heads, kv_heads, width, capacity)) != TMH_SUCCESS) return err;
+    if (ldq < heads * width || ld_dst < heads * width || cache_rows == 0) return TMH_ERROR_SHAPE;
+    if (tokens == 0) return TMH_SUCCESS;
+    if (!q || !keys || !values || !table || !dst) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)tokens * heads > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    tmh::Attention a{(const float*)q, ldq, (const float*)keys, (const float*)values, cache_rows, kv_heads, capacity,
+                     width, heads, (const int32_t*)table, scale, (float*)dst, ld_dst, ctx.errors};
+    hipError_t e = tmh::launch_attention(a, tokens, ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, true);
+    return code(e);
+}
+
+int tmh_swiglu(uint64_t gate, uint64_t value, uint32_t ld, uint32_t rows, uint32_t n, uint64_t dst) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if (ld < n) return TMH_ERROR_SHAPE;
+    if (rows == 0 || n == 0) return TMH_SUCCESS;
+    if (!gate || !value || !dst) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)rows * ld > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    hipError_t e = tmh::launch_swiglu((const float*)gate, (const float*)value, ld, rows, n, (float*)dst, ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, false);
+    return code(e);
+}
+
+int tmh_add(uint64_t a, uint64_t b, uint64_t dst, uint64_t count) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if (count == 0) return TMH_SUCCESS;
+    if (!a || !b || !dst) return TMH_ERROR_INVALID_VALUE;
+    if (count > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    hipError_t e = tmh::launch_add((const float*)a, (const float*)b, (float*)dst, (uint32_t)count, ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, false);
+    return code(e);
+}
+
+int tmh_argmax(uint64_t x, uint32_t ldx, uint32_t rows, uint32_t n, uint64_t ids) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    if (n == 0 || ldx < n) return TMH_ERROR_SHAPE;
+    if (rows == 0) return TMH_SUCCESS;
+    if (!x || !ids) return TMH_ERROR_INVALID_VALUE;
+    if ((uint64_t)rows * ldx > 0x7fffffffull) return TMH_ERROR_SHAPE;
+    hipError_t e = tmh::launch_argmax((const float*)x, ldx, rows, n, (int32_t*)ids, ctx.stream);
+    if (e == hipSuccess) tmh::note_launch(ctx.index, 1, false);
+    return code(e);
+}
+
+// ------------------------------------------------------------- the decoder
+
+int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* weights, uint32_t rows,
+                     uint32_t capacity, uint32_t max_tokens, uint64_t* model) {
+    if (!config || !weights || !model) return TMH_ERROR_INVALID_VALUE;
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    const tmh_llama_config& c = *config;
+    if (c.kind > 2u) return TMH_ERROR_DTYPE;
+    if (c.layers <= 0 || c.width <= 0 || c.width % 32 != 0 || c.hidden <= 0 || c.hidden % 32 != 0 || c.heads <= 0 ||
+        c.kv_heads <= 0 || c.heads % c.kv_heads != 0 || c.head_width <= 0 || c.vocab <= 0 || c.context <= 0)
+        return TMH_ERROR_SHAPE;
+    if ((c.heads * c.head_width) % 32 != 0) return TMH_ERROR_SHAPE;
+    if (rows == 0 || max_tokens == 0 || capacity == 0 || capacity > (uint32_t)c.context) return TMH_ERROR_SHAPE;
+    if ((err = check_rope(c.heads, c.kv_heads, c.head_width, capacity, capacity)) != TMH_SUCCESS) return err;
+    if ((err = check_attention(c.heads, c.kv_heads, c.head_width, capacity)) != TMH_SUCCESS) return err;
+    if (!weights->embed || !weights->norm || !weights->attn_norm || !weights->ffn_norm || !weights->qkv ||
+        !weights->o || !weights->gate_up || !weights->down)
+        return TMH_ERROR_INVALID_VALUE;
+
+    Llama* m = new Llama();
+    m->device = ctx.index;
+    m->c = c;
+    m->rows = rows;
+    m->capacity = capacity;
+    m->max_tokens = max_tokens;
+    m->qn = (uint32_t)(c.heads * c.head_width);
+    m->kvn = (uint32_t)(c.kv_heads * c.head_width);
+    m->nqkv = m->qn + 2u * m->kvn;
+    m->row_bytes = (size_t)c.width / 32u * tmh::block_bytes(c.kind);
+    m->embed = (const uint8_t*)weights->embed;
+    m->head = (const uint8_t*)(weights->head ? weights->head : weights->embed);
+    m->norm = (const float*)weights->norm;
+    for (int32_t l = 0; l < c.layers; ++l) {
+        if (!weights->attn_norm[l] || !weights->ffn_norm[l] || !weights->qkv[l] || !weights->o[l] ||
+            !weights->gate_up[l] || !weights->down[l]) {
+            delete m;
+            return TMH_ERROR_INVALID_VALUE;
+        }
+        m->attn_norm.push_back((const float*)weights->attn_norm[l]);
+        m->ffn_norm.push_back((const float*)weights->ffn_norm[l]);
+        m->qkv.push_back((const uint8_t*)weights->qkv[l]);
+        m->o.push_back((const uint8_t*)weights->o[l]);
+        m->gate_up.push_back((const uint8_t*)weights->gate_up[l]);
+        m->down.push_back((const uint8_t*)weights->down[l]);
+    }
+    m->length.assign(rows, 0);
+    m->has_logits.assign(rows, 0);
+
+    // One allocation, carved 256-byte aligned.
+    const size_t R = std::max(rows, max_tokens);
+    const size_t W = (size_t)c.width, H = (size_t)c.hidden, hw = (size_t)c.head_width;
+    m->layer_cache = (size_t)rows * c.kv_heads * capacity * hw;
+    const uint32_t widest = (uint32_t)std::max<size_t>({W, H, (size_t)m->qn});
+    struct Part {
+        void** at;
+        size_t bytes;
+    } parts[] = {
+        {(void**)&m->x, R * W * 4},
+        {(void**)&m->h, R * W * 4},
+        {(void**)&m->qkv_out, R * m->nqkv * 4},
+        {(void**)&m->q, R * m->qn * 4},
+        {(void**)&m->att, R * m->qn * 4},
+        {(void**)&m->o_out, R * W * 4},
+        {(void**)&m->gu, R * 2 * H * 4},
+        {(void**)&m->act, R * H * 4},
+        {(void**)&m->logits, R * (size_t)c.vocab * 4},
+        {(void**)&m->cos, (size_t)capacity * hw * 4},
+        {(void**)&m->sin, (size_t)capacity * hw * 4},
+        {(void**)&m->ids, R * 4},
+        {(void**)&m->slots, R * 4},
+        {(void**)&m->table, R * 3 * 4},
+        {(void**)&m->steps, (size_t)rows * 4},
+        {(void**)&m->log, (size_t)rows * capacity * 4},
+        {(void**)&m->scratch, tmh::scratch_need((uint32_t)R, widest)},
+        {(void**)&m->keys, m->layer_cache * c.layers * 4},
+        {(void**)&m->values, m->layer_cache * c.layers * 4},
+    };
+    size_t total = 0;
+    for (const Part& p : parts) total += align256(p.bytes);
+    void* mem = nullptr;
+    hipError_t e = tmh::device_malloc(&mem, total);
+    if (e != hipSuccess) {
+        delete m;
+        return code(e);
+    }
+    m->memory = (uint8_t*)mem;
+    size_t at = 0;
+    for (const Part& p : parts) {
+        *p.at = m->memory + at;
+        at += align256(p.bytes);
+    }
+
+    // RotaryEmbedding's tables (modules.cr:344-351), in F32 as there:
+    // frequency i = 1 / θ^(2i/width) by powf, then cosf/sinf of p·frequency.
+    const uint32_t half = (uint32_t)hw / 2u;
+    std::vector<float> freq(half), cs((size_t)capacity * hw), sn((size_t)capacity * hw);
+    const float theta = (float)c.theta;
+    for (uint32_t i = 0; i < half; ++i) freq[i] = 1.0f / powf(theta, (float)(2u * i) / (float)hw);
+    for (uint32_t p = 0; p < capacity; ++p)
+        for (uint32_t i = 0; i < hw; ++i) {
+            const float angle = (float)p * freq[i % half];
+            cs[(size_t)p * hw + i] = cosf(angle);
+            sn[(size_t)p * hw + i] = sinf(angle);
+        }
+    e = hipMemcpyAsync(m->cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx.stream);
+    if (e != hipSuccess) {
+        (void)hipFree(m->memory);
+        delete m;
+        return code(e);
+    }
+    *model = (uint64_t)m;
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_forward(uint64_t model, uint32_t row, const int32_t* ids, uint32_t count, uint32_t last_only,
+                      float* logits) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (row >= m->rows || !ids) return TMH_ERROR_INVALID_VALUE;
+    if (count == 0 || count > m->max_tokens) return TMH_ERROR_SHAPE;
+    const int32_t past = m->length[row];
+    if ((uint64_t)past + count > m->capacity) return TMH_ERROR_SHAPE;
+    for (uint32_t i = 0; i < count; ++i)
+        if (ids[i] < 0 || ids[i] >= m->c.vocab) return TMH_ERROR_INVALID_VALUE;
+    // ids, slots, then the attention table, in one upload
+    std::vector<int32_t> host((size_t)count * 5);
+    for (uint32_t i = 0; i < count; ++i) {
+        host[i] = ids[i];
+        host[count + i] = (int32_t)(row * m->capacity) + past + (int32_t)i;
+        host[2 * count + 3 * i] = (int32_t)row;
+        host[2 * count + 3 * i + 1] = past + (int32_t)i;
+        host[2 * count + 3 * i + 2] = past + (int32_t)count;
+    }
+    m->generating = false;
+    hipError_t e = hipMemcpyAsync(m->ids, host.data(), (size_t)count * 4, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->slots, host.data() + count, (size_t)count * 4, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->table, host.data() + 2 * count, (size_t)count * 12, hipMemcpyHostToDevice, ctx.stream);
+    const uint32_t final_rows = last_only ? 1u : count;
+    // A last-only forward leaves its logits in the row's logits row, where
+    // generation starts from.
+    const uint32_t logits_row = last_only ? row : 0u;
+    if (e == hipSuccess) e = forward_tokens(*m, ctx, count, last_only ? count - 1u : 0u, final_rows, logits_row);
+    if (e != hipSuccess) return code(e);
+    tmh::note_launch(ctx.index, 0, true);
+    m->length[row] = past + (int32_t)count;
+    const size_t vocab = (size_t)m->c.vocab;
+    if (logits) {
+        e = hipMemcpyAsync(logits, m->logits + (size_t)logits_row * vocab, (size_t)final_rows * vocab * 4,
+                           hipMemcpyDeviceToHost, ctx.stream);
+        if (e != hipSuccess) return code(e);
+    }
+    if (!last_only) {
+        // The logits filled rows 0..count-1, over other rows' last logits;
+        // the last one moves to the row's own logits row.
+        for (uint32_t r = 0; r < std::min(count, m->rows); ++r) m->has_logits[r] = 0;
+        if (count - 1u != row) {
+            e = hipMemcpyAsync(m->logits + (size_t)row * vocab, m->logits + (size_t)(count - 1u) * vocab, vocab * 4,
+                               hipMemcpyDeviceToDevice, ctx.stream);
+            if (e != hipSuccess) return code(e);
+        }
+    }
+    m->has_logits[row] = 1;
+    return tmh_sync();
+}
+
+int tmh_llama_generate(uint64_t model, uint32_t steps, int32_t* tokens, uint32_t graph) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (steps == 0) return TMH_SUCCESS;
+    if (!tokens) return TMH_ERROR_INVALID_VALUE;
+    for (uint32_t r = 0; r < m->rows; ++r) {
+        if (!m->has_logits[r]) return TMH_ERROR_INVALID_VALUE;
+        if ((uint64_t)m->length[r] + steps - 1u > m->capacity) return TMH_ERROR_SHAPE;
+    }
+    if (steps > m->capacity) return TMH_ERROR_SHAPE;
+    // Each row as if its last forward's token had just been run: the step's
+    // advance then points it at its next position.
+    std::vector<int32_t> host((size_t)m->rows * 5);
+    for (uint32_t r = 0; r < m->rows; ++r) {
+        const int32_t len = m->length[r];
+        host[r] = (int32_t)(r * m->capacity) + len - 1;
+        host[m->rows + 3 * r] = (int32_t)r;
+        host[m->rows + 3 * r + 1] = len - 1;
+        host[m->rows + 3 * r + 2] = len;
+        host[4 * m->rows + r] = 0;
+    }
+    hipError_t e = hipMemcpyAsync(m->slots, host.data(), (size_t)m->rows * 4, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->table, host.data() + m->rows, (size_t)m->rows * 12, hipMemcpyHostToDevice, ctx.stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->steps, host.data() + 4 * m->rows, (size_t)m->rows * 4, hipMemcpyHostToDevice, ctx.stream);
+    // the first token of each row from its last forward's logits
+    if (e == hipSuccess)
+        e = tmh::launch_argmax(m->logits, (uint32_t)m->c.vocab, m->rows, (uint32_t)m->c.vocab, m->ids, ctx.stream);
+    if (e == hipSuccess)
+        e = tmh::launch_advance(m->rows, m->ids, m->log, m->capacity, m->steps, m->slots, m->table, m->capacity,
+                                ctx.stream);
+    if (e != hipSuccess) return code(e);
+    tmh::note_launch(ctx.index, 0, true);
+    for (uint32_t i = 1; i < steps; ++i) {
+        if ((err = run_step(*m, ctx, graph != 0)) != TMH_SUCCESS) return err;
+        for (uint32_t r = 0; r < m->rows; ++r) m->length[r] += 1;
+    }
+    std::fill(m->has_logits.begin(), m->has_logits.end(), 1);
+    m->generating = true;
+    std::vector<int32_t> log((size_t)m->rows * m->capacity);
+    e = hipMemcpyAsync(log.data(), m->log, log.size() * 4, hipMemcpyDeviceToHost, ctx.stream);
+    if (e != hipSuccess) return code(e);
+    if ((err = tmh_sync()) != TMH_SUCCESS) return err;
+    for (uint32_t r = 0; r < m->rows; ++r)
+        std::memcpy(tokens + (size_t)r * steps, log.data() + (size_t)r * m->capacity, (size_t)steps * 4);
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_step(uint64_t model, uint32_t graph) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (!m->generating) return TMH_ERROR_INVALID_VALUE;
+    for (uint32_t r = 0; r < m->rows; ++r)
+        if ((uint64_t)m->length[r] + 1u > m->capacity) return TMH_ERROR_SHAPE;
+    if ((err = run_step(*m, ctx, graph != 0)) != TMH_SUCCESS) return err;
+    for (uint32_t r = 0; r < m->rows; ++r) m->length[r] += 1;
+    tmh::note_launch(ctx.index, 0, true);
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_length(uint64_t model, uint32_t row, int32_t* length) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, false);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (row >= m->rows || !length) return TMH_ERROR_INVALID_VALUE;
+    *length = m->length[row];
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_reset(uint64_t model, uint32_t row) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, false);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (row >= m->rows) return TMH_ERROR_INVALID_VALUE;
+    m->length[row] = 0;
+    m->has_logits[row] = 0;
+    m->generating = false;
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_destroy(uint64_t model) {
+    if (!model) return TMH_SUCCESS;
+    DeviceContext ctx;
+    Llama* m = (Llama*)model;
+    if (tmh::device_context(&ctx, false) == TMH_SUCCESS) (void)hipStreamSynchronize(ctx.stream);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    if (m->memory) (void)hipFree(m->memory);
+    delete m;
+    return TMH_SUCCESS;
+}
+
+}  // extern "C"

@@ -21,6 +21,39 @@
 #include "tmh_internal.h"
 
 namespace {
+std::atomic<int> g_fail_allocations{0};
+}  // namespace
+
+namespace tmh {
+
+hipError_t device_malloc(void** p, size_t bytes) {
+    int left = g_fail_allocations.load();
+    while (left > 0) {
+        if (g_fail_allocations.compare_exchange_weak(left, left - 1)) return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
+size_t scratch_need(uint32_t rows, uint32_t k) {
+    const size_t nb = k / 32u;
+    const size_t per = ((size_t)rows * nb * 4u + 255u) & ~(size_t)255u;
+    return 3 * per + (((size_t)rows * k + 255u) & ~(size_t)255u);
+}
+
+// The quantise pass's four outputs for `rows` rows of k, carved from `base`.
+Activations carve_scratch(uint8_t* base, uint32_t rows, uint32_t k) {
+    const size_t nb = k / 32u;
+    const size_t per = ((size_t)rows * nb * 4u + 255u) & ~(size_t)255u;
+    return Activations{(const float*)base, (const float*)(base + per), (const int32_t*)(base + 2 * per),
+                       (const int8_t*)(base + 3 * per)};
+}
+
+}  // namespace tmh
+
+namespace {
+
+using tmh::device_malloc;
+using tmh::scratch_need;
 
 constexpr int MAX_DEVICES = 16;
 
@@ -173,20 +206,10 @@ struct Device {
 
 Device g_devices[MAX_DEVICES];
 std::atomic<int> g_count{-1};
-std::atomic<int> g_fail_allocations{0};
 std::atomic<bool> g_kernels_off{false};
 thread_local int t_device = 0;
 
 int code(hipError_t e) { return (int)e; }
-
-// Device allocation honouring the test hook.
-hipError_t device_malloc(void** p, size_t bytes) {
-    int left = g_fail_allocations.load();
-    while (left > 0) {
-        if (g_fail_allocations.compare_exchange_weak(left, left - 1)) return hipErrorOutOfMemory;
-    }
-    return hipMalloc(p, bytes);
-}
 
 int count_devices() {
     int n = g_count.load();
@@ -271,24 +294,6 @@ int ensure_scratch(Device& d, size_t bytes) {
 
 size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
 
-// Carves the scratch into the quantise pass's four outputs for `rows` rows of k.
-tmh::Activations carve(Device& d, uint32_t rows, uint32_t k, float** scales, float** sums, int32_t** totals,
-                       int8_t** qs) {
-    const size_t nb = k / 32u;
-    const size_t per = align256((size_t)rows * nb * 4u);
-    uint8_t* base = d.scratch;
-    *scales = (float*)base;
-    *sums = (float*)(base + per);
-    *totals = (int32_t*)(base + 2 * per);
-    *qs = (int8_t*)(base + 3 * per);
-    return tmh::Activations{*scales, *sums, *totals, *qs};
-}
-
-size_t scratch_need(uint32_t rows, uint32_t k) {
-    const size_t nb = k / 32u;
-    return 3 * align256((size_t)rows * nb * 4u) + align256((size_t)rows * k);
-}
-
 const char* library_name(int c) {
     switch (c) {
     case TMH_SUCCESS: return "TMH_SUCCESS";
@@ -320,6 +325,29 @@ const char* library_string(int c) {
 }
 
 }  // namespace
+
+namespace tmh {
+
+int device_context(DeviceContext* out, bool kernels) {
+    if (kernels && g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    out->index = d->index;
+    out->stream = d->stream;
+    out->compute_units = d->compute_units;
+    out->errors = d->errors;
+    return TMH_SUCCESS;
+}
+
+void note_launch(int index, int ops, bool errors) {
+    if (index < 0 || index >= MAX_DEVICES) return;
+    Device& d = g_devices[index];
+    if (errors) d.errors_pending.store(true);
+    d.gpu_ops.fetch_add(ops);
+}
+
+}  // namespace tmh
 
 extern "C" {
 
@@ -654,11 +682,9 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     }
     std::lock_guard<std::mutex> guard(d->launch);
     if ((err = ensure_scratch(*d, scratch_need(rows, k))) != TMH_SUCCESS) return err;
-    float *scales, *sums;
-    int32_t* totals;
-    int8_t* qs;
-    tmh::Activations act = carve(*d, rows, k, &scales, &sums, &totals, &qs);
-    hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, scales, sums, totals, qs, d->stream);
+    tmh::Activations act = tmh::carve_scratch(d->scratch, rows, k);
+    hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, (float*)act.scales, (float*)act.sums,
+                                        (int32_t*)act.totals, (int8_t*)act.qs, d->stream);
     if (e == hipSuccess)
         e = tmh::launch_block_matmul(kind, mode, (const uint8_t*)(w + w_byte_offset), act, (float*)dst,
                                      (const float*)bias, rows, n, k, d->compute_units, d->stream);

@@ -85,9 +85,23 @@ class Counters(ctypes.Structure):
                  "pool_misses", "frees")]
 
 
+class LlamaConfig(ctypes.Structure):
+    """tmh_llama_config."""
+    _fields_ = [("layers", ctypes.c_int32), ("width", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("kv_heads", ctypes.c_int32), ("head_width", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("vocab", ctypes.c_int32), ("context", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("theta", ctypes.c_double), ("kind", ctypes.c_uint32)]
+
+
+class LlamaWeights(ctypes.Structure):
+    """tmh_llama_weights: device addresses."""
+    _fields_ = [("embed", ctypes.c_uint64), ("head", ctypes.c_uint64), ("norm", ctypes.c_uint64)] + [
+        (name, ctypes.POINTER(ctypes.c_uint64)) for name in ("attn_norm", "ffn_norm", "qkv", "o", "gate_up", "down")]
+
+
 # Every symbol include/tensomite_hip.h declares, with (restype, argtypes).
 U32, I32, U64, I64 = ctypes.c_uint32, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int64
-VP, INT = ctypes.c_void_p, ctypes.c_int
+VP, INT, F32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "tmh_init": (INT, [ctypes.POINTER(I32)]),
     "tmh_device_info_get": (INT, [I32, ctypes.POINTER(DeviceInfo)]),
@@ -122,6 +136,20 @@ SIGNATURES = {
     "tmh_plan_create": (INT, [U32, ctypes.POINTER(Product), U32, ctypes.POINTER(U64)]),
     "tmh_plan_run": (INT, [U64]),
     "tmh_plan_destroy": (INT, [U64]),
+    "tmh_rmsnorm": (INT, [U64, U32, U64, U32, U32, F32, U64]),
+    "tmh_rope_write": (INT, [U64, U32, U32, U32, U32, U32, U64, U64, U32, U64, U32, U32, U64, U64, U64]),
+    "tmh_attention": (INT, [U64, U32, U32, U32, U64, U64, U32, U32, U32, U32, U64, F32, U64, U32]),
+    "tmh_swiglu": (INT, [U64, U64, U32, U32, U32, U64]),
+    "tmh_add": (INT, [U64, U64, U64, U64]),
+    "tmh_argmax": (INT, [U64, U32, U32, U32, U64]),
+    "tmh_llama_create": (INT, [ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaWeights), U32, U32, U32,
+                               ctypes.POINTER(U64)]),
+    "tmh_llama_forward": (INT, [U64, U32, VP, U32, U32, VP]),
+    "tmh_llama_generate": (INT, [U64, U32, VP, U32]),
+    "tmh_llama_length": (INT, [U64, U32, ctypes.POINTER(I32)]),
+    "tmh_llama_reset": (INT, [U64, U32]),
+    "tmh_llama_step": (INT, [U64, U32]),
+    "tmh_llama_destroy": (INT, [U64]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -287,12 +315,15 @@ class HIPDevice:
     def sync(self) -> None:
         """Waits, recycles retired memory, and raises ExecutionError for an index
         a kernel reported out of range (CUDA#sync, cuda.cr:419-428)."""
-        code = self.lib.tmh_sync()
+        self.check_synced("tmh_sync", self.lib.tmh_sync())
+
+    def check_synced(self, call: str, code: int) -> None:
+        """check() for calls that end in tmh_sync: an index error is an ExecutionError."""
         if code == ERROR_EXECUTION:
             report = (I32 * 3)()
             check("tmh_error_report", self.lib.tmh_error_report(report))
             raise ExecutionError(f"index {report[1]} out of range for {report[2]} rows")
-        check("tmh_sync", code)
+        check(call, code)
 
     def shape_invariant(self) -> bool:
         """Each output depends only on its own row and column (quant.cr:120-121)."""
@@ -392,6 +423,71 @@ class HIPDevice:
         check("tmh_plan_create", self.lib.tmh_plan_create(kk, arr, len(items), ctypes.byref(handle)))
         return Plan(self, handle.value, items)
 
+    # -- the rest of the decode graph (F32 buffers)
+    def rmsnorm(self, x: Buffer, weight: Optional[Buffer], rows: int, n: int, eps: float,
+                dst: Optional[Buffer] = None, ldx: Optional[int] = None) -> Buffer:
+        """Op::RMSNorm (host.cr:374-386), queued."""
+        stride = n if ldx is None else ldx
+        if rows and ((rows - 1) * stride + n) * 4 > x.bytesize or (weight is not None and n * 4 > weight.bytesize):
+            raise ShapeError(f"rmsnorm of {rows} rows of {n}: buffers too small")
+        dst = dst or self.alloc(max(4 * rows * n, 4))
+        check("tmh_rmsnorm", self.lib.tmh_rmsnorm(x.pointer, stride, weight.pointer if weight is not None else 0,
+                                                  rows, n, eps, dst.pointer))
+        return dst
+
+    def rope_write(self, x: Buffer, ldx: int, tokens: int, heads: int, kv_heads: int, width: int, cos: Buffer,
+                   sin: Buffer, table_rows: int, slots: Buffer, cache_rows: int, capacity: int, q_dst: Buffer,
+                   keys: Buffer, values: Buffer) -> None:
+        """Op::Rope of q and k and Op::WriteRows of k and v into the caches, queued."""
+        cache = cache_rows * kv_heads * capacity * width * 4
+        if (tokens and ((tokens - 1) * ldx + (heads + 2 * kv_heads) * width) * 4 > x.bytesize
+                or table_rows * width * 4 > min(cos.bytesize, sin.bytesize) or tokens * 4 > slots.bytesize
+                or tokens * heads * width * 4 > q_dst.bytesize or cache > min(keys.bytesize, values.bytesize)):
+            raise ShapeError("rope_write: buffers too small")
+        check("tmh_rope_write", self.lib.tmh_rope_write(
+            x.pointer, ldx, tokens, heads, kv_heads, width, cos.pointer, sin.pointer, table_rows, slots.pointer,
+            cache_rows, capacity, q_dst.pointer, keys.pointer, values.pointer))
+
+    def attention(self, q: Buffer, tokens: int, heads: int, keys: Buffer, values: Buffer, cache_rows: int,
+                  kv_heads: int, capacity: int, width: int, table: Buffer, scale: float,
+                  dst: Optional[Buffer] = None) -> Buffer:
+        """Attention of packed queries [tokens, heads, width] against the caches (host.cr:408-440), queued."""
+        cache = cache_rows * kv_heads * capacity * width * 4
+        if tokens * heads * width * 4 > q.bytesize or cache > min(keys.bytesize, values.bytesize) \
+                or tokens * 12 > table.bytesize:
+            raise ShapeError("attention: buffers too small")
+        dst = dst or self.alloc(max(4 * tokens * heads * width, 4))
+        check("tmh_attention", self.lib.tmh_attention(
+            q.pointer, heads * width, tokens, heads, keys.pointer, values.pointer, cache_rows, kv_heads, capacity,
+            width, table.pointer, scale, dst.pointer, heads * width))
+        return dst
+
+    def swiglu(self, gate: Buffer, value: Buffer, ld: int, rows: int, n: int, dst: Optional[Buffer] = None,
+               gate_offset: int = 0, value_offset: int = 0) -> Buffer:
+        """SwiGLU (kernels.cr:18) of row-strided gate and value, queued; offsets in elements."""
+        if rows and ((rows - 1) * ld + n + gate_offset) * 4 > gate.bytesize or \
+                rows and ((rows - 1) * ld + n + value_offset) * 4 > value.bytesize:
+            raise ShapeError("swiglu: buffers too small")
+        dst = dst or self.alloc(max(4 * rows * n, 4))
+        check("tmh_swiglu", self.lib.tmh_swiglu(gate.pointer + 4 * gate_offset, value.pointer + 4 * value_offset,
+                                                ld, rows, n, dst.pointer))
+        return dst
+
+    def add(self, a: Buffer, b: Buffer, count: int, dst: Optional[Buffer] = None) -> Buffer:
+        if count * 4 > min(a.bytesize, b.bytesize):
+            raise ShapeError("add: buffers too small")
+        dst = dst or self.alloc(max(4 * count, 4))
+        check("tmh_add", self.lib.tmh_add(a.pointer, b.pointer, dst.pointer, count))
+        return dst
+
+    def argmax(self, x: Buffer, rows: int, n: int, ids: Optional[Buffer] = None) -> Buffer:
+        """Sampler.greedy per row (sampler.cr:35-36), queued: int32 ids."""
+        if rows * n * 4 > x.bytesize:
+            raise ShapeError("argmax: buffer too small")
+        ids = ids or self.alloc(max(4 * rows, 4))
+        check("tmh_argmax", self.lib.tmh_argmax(x.pointer, n, rows, n, ids.pointer))
+        return ids
+
     # -- timing on the library's stream
     def event(self) -> int:
         ev = U64(0)
@@ -405,3 +501,84 @@ class HIPDevice:
         ms = ctypes.c_float(0)
         check("tmh_event_elapsed_ms", self.lib.tmh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
         return ms.value
+
+
+LLAMA_LAYER_KEYS = ("attn_norm", "ffn_norm", "qkv", "o", "gate_up", "down")
+
+
+class HIPLlama:
+    """A Llama decoded on the device (tmh_llama_*): Llama#forward /
+    #forward_last and Generative#generate with the greedy sampler
+    (llama.cr:256-303, generative.cr:155-190), over `rows` sequences.
+
+    `weights` is a dict as the oracle's Llama takes it: embed and head (None
+    when tied) block bytes, norm, and per-layer lists attn_norm, ffn_norm (F32),
+    qkv, o, gate_up, down (block bytes; q/k rows in Hugging Face order). They
+    are uploaded once to device buffers this object owns."""
+
+    def __init__(self, device: HIPDevice, config: dict, weights: dict, rows: int = 1,
+                 capacity: Optional[int] = None, max_tokens: int = 128, asynchronous: bool = True):
+        self.device = device
+        self.config = dict(config)
+        c = self.config
+        self.rows = rows
+        self.capacity = capacity or c["context"]
+        up = lambda a, dt: device.from_array(np.ascontiguousarray(a, dtype=dt), asynchronous)
+        self.buffers = {"embed": up(weights["embed"], np.uint8), "norm": up(weights["norm"], np.float32)}
+        if weights.get("head") is not None:
+            self.buffers["head"] = up(weights["head"], np.uint8)
+        for key in LLAMA_LAYER_KEYS:
+            dt = np.float32 if key.endswith("norm") else np.uint8
+            self.buffers[key] = [up(a, dt) for a in weights[key]]
+        ptrs = lambda key: (U64 * c["layers"])(*[b.pointer for b in self.buffers[key]])
+        self._arrays = {key: ptrs(key) for key in LLAMA_LAYER_KEYS}
+        cfg = LlamaConfig(c["layers"], c["width"], c["heads"], c["kv_heads"], c["head_width"], c["hidden"],
+                          c["vocab"], c["context"], c["eps"], c["theta"], kind_of(c["kind"]))
+        head = self.buffers["head"].pointer if "head" in self.buffers else 0
+        w = LlamaWeights(self.buffers["embed"].pointer, head, self.buffers["norm"].pointer,
+                         *[self._arrays[k] for k in LLAMA_LAYER_KEYS])
+        handle = U64(0)
+        device.bind()
+        check("tmh_llama_create", device.lib.tmh_llama_create(ctypes.byref(cfg), ctypes.byref(w), rows,
+                                                              self.capacity, max_tokens, ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def forward(self, ids, row: int = 0, last_only: bool = False) -> np.ndarray:
+        """Logits [len(ids) or 1, vocab] of ids run after the row's cached positions."""
+        idx = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+        out = np.empty((1 if last_only else idx.size, self.config["vocab"]), np.float32)
+        self.device.bind()
+        self.device.check_synced("tmh_llama_forward", self.device.lib.tmh_llama_forward(
+            self.handle, row, idx.ctypes.data, idx.size, 1 if last_only else 0, out.ctypes.data))
+        return out
+
+    def generate(self, steps: int, graph: bool = True) -> np.ndarray:
+        """[rows, steps] greedy tokens from every row's last forward."""
+        out = np.empty((self.rows, steps), np.int32)
+        self.device.bind()
+        self.device.check_synced("tmh_llama_generate", self.device.lib.tmh_llama_generate(
+            self.handle, steps, out.ctypes.data, 1 if graph else 0))
+        return out
+
+    def step(self, graph: bool = True) -> None:
+        check("tmh_llama_step", self.device.lib.tmh_llama_step(self.handle, 1 if graph else 0))
+
+    def length(self, row: int = 0) -> int:
+        n = I32(0)
+        check("tmh_llama_length", self.device.lib.tmh_llama_length(self.handle, row, ctypes.byref(n)))
+        return n.value
+
+    def reset(self, row: Optional[int] = None) -> None:
+        for r in (range(self.rows) if row is None else [row]):
+            check("tmh_llama_reset", self.device.lib.tmh_llama_reset(self.handle, r))
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", 0):
+            self.device.lib.tmh_llama_destroy(self.handle)
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass

@@ -1,0 +1,298 @@
+"""The decode graph on the GPU against the oracle, bit for bit (runs on an MI355X).
+
+Op by op (RMSNorm, RoPE + cache write, attention, SwiGLU, add, argmax) on
+seeded inputs with the edge cases the host kernels define (NaN at index 0,
+ties, the causal mask, grouped heads, several cache rows), then whole
+forwards: the reference's tiny_llama GGUFs, prefill == one-by-one decode
+(block_matmul_spec.cr:253-260), and greedy generation at the 1.7B shape
+with the same tokens as the CPU, eager and from a
+captured HIP graph, at batch 1 and batch 8.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from llama_fixtures import SMOLLM2_1P7B, random_block_llama, random_llama, tiny_llama
+from oracle import oracle
+import tensomite_hip as th
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return th.HIPDevice(0)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def f32(dev, buf, count):
+    out = dev.to_array(buf, np.float32, count)
+    dev.sync()
+    return out
+
+
+@pytest.mark.parametrize("n", [1, 3, 32, 576, 2048, 8192, 20000])
+def test_rmsnorm_bit_exact(dev, n):
+    say("rmsnorm n", n)
+    rng = np.random.default_rng(n)
+    rows = 7
+    x = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    x[1] *= 1e-20  # tiny squares
+    x[2] *= 1e18   # squares past f32 range: root inf, all zeros out
+    x[3] = 0.0     # root sqrt(eps)
+    w = rng.normal(1, 0.1, n).astype(np.float32)
+    for weight in (w, None):
+        got = f32(dev, dev.rmsnorm(dev.from_array(x), dev.from_array(weight) if weight is not None else None,
+                                   rows, n, 1e-5), rows * n).reshape(rows, n)
+        want = oracle.rmsnorm(x, weight, 1e-5)
+        assert np.array_equal(bits(got), bits(want))
+
+
+def test_rmsnorm_square_root_rounding(dev):
+    # Rows of one value a: root = sqrt(a·a/1 + eps), out = a / root; over a
+    # million magnitudes every rounding of the square root and the division
+    # shows in the output bits.
+    rng = np.random.default_rng(11)
+    a = (rng.uniform(0.5, 2.0, 1 << 20) * 2.0 ** rng.integers(-60, 60, 1 << 20)).astype(np.float32)
+    got = f32(dev, dev.rmsnorm(dev.from_array(a), None, a.size, 1, 1e-5), a.size)
+    want = oracle.rmsnorm(a.reshape(-1, 1), None, 1e-5).reshape(-1)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_rmsnorm_strided_rows(dev):
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 1, (5, 100)).astype(np.float32)
+    w = rng.normal(1, 0.1, 64).astype(np.float32)
+    got = f32(dev, dev.rmsnorm(dev.from_array(x), dev.from_array(w), 5, 64, 1e-6, ldx=100), 5 * 64)
+    want = oracle.rmsnorm(x[:, :64], w, 1e-6).reshape(-1)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_swiglu_bit_exact(dev):
+    rng = np.random.default_rng(13)
+    rows, n, ld = 3, 5000, 11000
+    gu = rng.normal(0, 4, (rows, ld)).astype(np.float32)
+    gu[0, :12] = [0.0, -0.0, 88.0, -88.0, 89.0, -89.0, 100.0, -100.0, np.inf, -np.inf, 87.3, -87.4]
+    gu[1, 0] = np.nan
+    got = f32(dev, dev.swiglu(dev.from_array(gu), dev.from_array(gu), ld, rows, n, value_offset=6000), rows * n)
+    want = oracle.swiglu(gu[:, :n], gu[:, 6000:6000 + n]).reshape(-1)
+    assert np.array_equal(bits(got), bits(want))
+    # Maths.exp through swiglu(g, 1) = g / (exp(-g) + 1) at every exponent
+    g = np.linspace(-100, 100, 200001).astype(np.float32)
+    ones = np.ones_like(g)
+    got = f32(dev, dev.swiglu(dev.from_array(g), dev.from_array(ones), g.size, 1, g.size), g.size)
+    assert np.array_equal(bits(got), bits(oracle.swiglu(g, ones)))
+
+
+def test_add(dev):
+    rng = np.random.default_rng(14)
+    a = rng.normal(0, 1, 10007).astype(np.float32)
+    b = rng.normal(0, 1, 10007).astype(np.float32)
+    ab, bb = dev.from_array(a), dev.from_array(b)
+    dev.add(ab, bb, a.size, dst=ab)  # in place, as the residual is
+    assert np.array_equal(bits(f32(dev, ab, a.size)), bits(a + b))
+
+
+def test_argmax_first_highest(dev):
+    rng = np.random.default_rng(15)
+    rows, n = 9, 49152
+    x = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    x[1, [5, 700, 40000]] = 9.0                 # ties: the first
+    x[2, 0] = np.nan                            # NaN first: index 0
+    x[3, [3, 9]] = [np.nan, 50.0]               # NaN later: skipped
+    x[4] = -np.inf
+    x[5] = 0.0
+    x[5, 100] = -0.0
+    x[6, n - 1] = np.inf
+    x[7] = np.float32(-3.0)
+    x[8, [17, 18]] = [0.0, -0.0]
+    x[8] = np.where(np.arange(n) < 17, -1.0, x[8]).astype(np.float32)
+    got = dev.to_array(dev.argmax(dev.from_array(x), rows, n), np.int32, rows)
+    dev.sync()
+    want = [oracle.argmax(x[r]) for r in range(rows)]
+    assert list(got) == want
+
+
+@pytest.mark.parametrize("heads,kv_heads,width", [(4, 2, 8), (32, 32, 64), (8, 2, 64)])
+def test_rope_write_bit_exact(dev, heads, kv_heads, width):
+    say("rope_write", heads, kv_heads, width)
+    rng = np.random.default_rng(heads * 100 + width)
+    tokens, cache_rows, capacity = 6, 3, 40
+    units = heads + 2 * kv_heads
+    ldx = units * width + 8
+    x = rng.normal(0, 1, (tokens, ldx)).astype(np.float32)
+    cos, sin = oracle.rope_tables(width, capacity, 10000.0)
+    slots = np.array([0, 1, 2, capacity + 5, 2 * capacity + 39, capacity], np.int32)
+    keys0 = rng.normal(0, 1, (cache_rows, kv_heads, capacity, width)).astype(np.float32)
+    values0 = rng.normal(0, 1, keys0.shape).astype(np.float32)
+    kb, vb = dev.from_array(keys0), dev.from_array(values0)
+    qb = dev.alloc(tokens * heads * width * 4)
+    dev.rope_write(dev.from_array(x), ldx, tokens, heads, kv_heads, width, dev.from_array(cos),
+                   dev.from_array(sin), capacity, dev.from_array(slots), cache_rows, capacity, qb, kb, vb)
+    q = f32(dev, qb, tokens * heads * width).reshape(tokens, heads, width)
+    keys = f32(dev, kb, keys0.size).reshape(keys0.shape)
+    values = f32(dev, vb, values0.size).reshape(values0.shape)
+    pos = slots % capacity
+    rows = slots // capacity
+    assert np.array_equal(bits(q), bits(oracle.rope(x, heads, width, cos, sin, pos)))
+    k_rot = oracle.rope(x[:, heads * width:], kv_heads, width, cos, sin, pos)
+    want_k, want_v = keys0.copy(), values0.copy()
+    for t in range(tokens):
+        want_k[rows[t], :, pos[t]] = k_rot[t]
+        want_v[rows[t], :, pos[t]] = x[t, (heads + kv_heads) * width:units * width].reshape(kv_heads, width)
+    assert np.array_equal(bits(keys), bits(want_k))
+    assert np.array_equal(bits(values), bits(want_v))
+
+
+def test_rope_write_slot_out_of_range(dev):
+    width, capacity = 8, 16
+    x = np.zeros((1, 4 * width), np.float32)
+    cos, sin = oracle.rope_tables(width, capacity, 10000.0)
+    kb, vb, qb = dev.alloc(capacity * width * 4), dev.alloc(capacity * width * 4), dev.alloc(2 * width * 4)
+    dev.rope_write(dev.from_array(x), 4 * width, 1, 2, 1, width, dev.from_array(cos), dev.from_array(sin), capacity,
+                   dev.from_array(np.array([capacity], np.int32)), 1, capacity, qb, kb, vb)
+    with pytest.raises(th.ExecutionError):
+        dev.sync()
+    dev.sync()  # reported once
+
+
+@pytest.mark.parametrize("heads,kv_heads,width,capacity", [(4, 2, 8, 64), (32, 32, 64, 2048), (8, 2, 64, 700)])
+def test_attention_bit_exact(dev, heads, kv_heads, width, capacity):
+    say("attention", heads, kv_heads, width, capacity)
+    rng = np.random.default_rng(heads + width + capacity)
+    rows = 3
+    k = rng.normal(0, 1, (rows, kv_heads, capacity, width)).astype(np.float32)
+    v = rng.normal(0, 1, (rows, kv_heads, capacity, width)).astype(np.float32)
+    table = [[0, 0, 1], [1, capacity - 1, capacity], [2, 4, 9], [0, capacity // 2, capacity // 2 + 1],
+             [1, 2, capacity], [2, capacity - 2, capacity - 1], [0, 5, 6], [2, 30 % capacity, capacity]]
+    q = rng.normal(0, 1, (len(table), heads, width)).astype(np.float32)
+    q[2] *= 40.0  # sharp softmax: many exponentials underflow to 0
+    scale = float(np.float32(1.0 / np.sqrt(width)))
+    got = dev.attention(dev.from_array(q), len(table), heads, dev.from_array(k), dev.from_array(v), rows, kv_heads,
+                        capacity, width, dev.from_array(np.array(table, np.int32)), scale)
+    got = f32(dev, got, q.size).reshape(q.shape)
+    want = oracle.attention(q, k, v, table, scale)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_attention_bad_table_entry(dev):
+    width, capacity = 8, 16
+    k = dev.from_array(np.zeros((1, 1, capacity, width), np.float32))
+    q = dev.from_array(np.ones((1, 1, width), np.float32))
+    out = dev.attention(q, 1, 1, k, k, 1, 1, capacity, width, dev.from_array(np.array([0, 3, capacity + 1], np.int32)),
+                        1.0)
+    with pytest.raises(th.ExecutionError):
+        dev.sync()
+    assert np.all(dev.to_array(out, np.float32, width) == 0)
+
+
+# ------------------------------------------------------------ whole forwards
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0"])
+def test_tiny_llama_forward_bit_exact(dev, golden, fmt):
+    import json
+    import os
+    with open(os.path.join(golden, "tiny_llama", "logits.json")) as f:
+        prompt = json.load(f)["prompt_ids"]
+    config, weights = tiny_llama(golden, fmt)
+    cpu = oracle.Llama(config, weights)
+    want = cpu.forward(prompt)
+    gpu = th.HIPLlama(dev, config, weights, max_tokens=64)
+    got = gpu.forward(prompt)
+    assert np.array_equal(bits(got), bits(want))
+    # prefill == one-by-one decode (block_matmul_spec.cr:253-260), on the GPU
+    gpu.reset()
+    one_by_one = np.concatenate([gpu.forward([i]) for i in prompt])
+    assert np.array_equal(bits(one_by_one), bits(want))
+    # greedy generation, eager and from a graph
+    for graph in (False, True):
+        gpu.reset()
+        gpu.forward(prompt[:10], last_only=True)
+        tokens = gpu.generate(20, graph=graph)[0]
+        assert list(tokens) == cpu.generate(prompt[:10], 20), graph
+
+
+def small_config(kind, **kw):
+    c = dict(layers=2, width=128, heads=4, kv_heads=2, head_width=32, hidden=256, vocab=512, context=96, eps=1e-5,
+             theta=10000.0, kind=kind)
+    c.update(kw)
+    return c
+
+
+@pytest.mark.parametrize("kind", ["Q8_0", "Q4_0", "Q4_1"])
+def test_small_llama_generate_matches_cpu(dev, kind):
+    say("small llama", kind)
+    config = small_config(kind)
+    weights = random_llama(config, seed=21, norm_jitter=0.1)
+    cpu = oracle.Llama(config, weights)
+    prompt = list(np.random.default_rng(22).integers(0, 512, 12))
+    gpu = th.HIPLlama(dev, config, weights, max_tokens=16)
+    logits = gpu.forward(prompt, last_only=True)
+    assert np.array_equal(bits(logits), bits(cpu.forward(prompt, last_only=True)))
+    tokens = gpu.generate(30, graph=True)[0]
+    assert list(tokens) == cpu.generate(prompt, 30)
+    assert gpu.length() == len(prompt) + 29
+
+
+def test_batch_rows_decode_matches_each_sequence(dev):
+    # rows of different prompt lengths decoded together: each row's tokens
+    # are those of its sequence alone (a row alone == in a batch).
+    config = small_config("Q4_0", layers=3)
+    weights = random_llama(config, seed=23, norm_jitter=0.1)
+    rng = np.random.default_rng(24)
+    prompts = [list(rng.integers(0, 512, n)) for n in (5, 12, 1, 9)]
+    gpu = th.HIPLlama(dev, config, weights, rows=len(prompts), max_tokens=16)
+    for r, p in enumerate(prompts):
+        gpu.forward(p, row=r, last_only=True)
+    got = gpu.generate(25, graph=True)
+    for r, p in enumerate(prompts):
+        assert list(got[r]) == oracle.Llama(config, weights).generate(p, 25), r
+
+
+def test_decoder_limits(dev):
+    config = small_config("Q8_0", context=32)
+    weights = random_llama(config, seed=25)
+    gpu = th.HIPLlama(dev, config, weights, capacity=20, max_tokens=8)
+    with pytest.raises(th.ShapeError):
+        gpu.forward(list(range(9)))          # more than max_tokens
+    with pytest.raises(th.DeviceError):
+        gpu.forward([config["vocab"]])        # an id out of range
+    gpu.forward(list(range(8)), last_only=True)
+    with pytest.raises(th.ShapeError):
+        gpu.generate(14)                      # 8 + 13 positions > 20
+    tokens = gpu.generate(13)
+    assert tokens.shape == (1, 13) and gpu.length() == 20
+
+
+@pytest.mark.parametrize("layers,rows", [(2, 1), (2, 8), (24, 1)])
+def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
+    # BASELINE config 5's shape (width 2048, 32 heads of 64, hidden 8192,
+    # vocab 49152, tied head): greedy tokens from the GPU, through a captured
+    # graph, equal the CPU's; and the eager path gives the graph's tokens.
+    say("1.7B shape", layers, "layers", rows, "rows")
+    config = dict(SMOLLM2_1P7B, layers=layers, context=256)
+    weights = random_block_llama(config, seed=30 + layers)
+    rng = np.random.default_rng(31)
+    prompts = [list(rng.integers(0, config["vocab"], 16 - r)) for r in range(rows)]
+    steps = 8
+    gpu = th.HIPLlama(dev, config, weights, rows=rows, capacity=64, max_tokens=16)
+    for r, p in enumerate(prompts):
+        gpu.forward(p, row=r, last_only=True)
+    got = gpu.generate(steps, graph=True)
+    cpu = oracle.Llama(config, weights)
+    for r, p in enumerate(prompts[:2]):
+        assert list(got[r]) == cpu.generate(p, steps), r
+    gpu.reset()
+    for r, p in enumerate(prompts):
+        gpu.forward(p, row=r, last_only=True)
+    assert np.array_equal(gpu.generate(steps, graph=False), got)

@@ -135,3 +135,38 @@ def test_random_model_generates_deterministically():
     a = model.generate(prompt, 20)
     b = model.generate(prompt, 20)
     assert a == b and len(a) == 20
+
+
+def test_attention_against_float64_definition():
+    # host.cr:408-440 against softmax(q·kᵀ·scale + mask)·v in float64, over
+    # grouped heads, several cache rows and causal masks; a transposed
+    # operand, a wrong kv head or a mask off by one fails the bound.
+    rng = np.random.default_rng(5)
+    heads, kv_heads, width, capacity, rows = 4, 2, 8, 40, 3
+    q = rng.normal(0, 1, (6, heads, width)).astype(np.float32)
+    k = rng.normal(0, 1, (rows, kv_heads, capacity, width)).astype(np.float32)
+    v = rng.normal(0, 1, (rows, kv_heads, capacity, width)).astype(np.float32)
+    table = [[0, 4, 10], [1, 39, 40], [2, 0, 1], [0, 9, 10], [1, 20, 30], [2, 7, 8]]
+    got = oracle.attention(q, k, v, table, 0.35)
+    for t, (r, last, n) in enumerate(table):
+        for h in range(heads):
+            kv = h // (heads // kv_heads)
+            s = k[r, kv, :n].astype(np.float64) @ q[t, h].astype(np.float64) * 0.35
+            s[np.arange(n) > last] = -np.inf
+            e = np.exp(s - s.max())
+            want = (e / e.sum()) @ v[r, kv, :n].astype(np.float64)
+            assert np.allclose(got[t, h], want, atol=2e-6), (t, h)
+
+
+def test_rope_against_definition():
+    # host.cr:448-466: x·cos + rotate_half(x)·sin, rotate_half = [-x2, x1]
+    rng = np.random.default_rng(6)
+    cos, sin = oracle.rope_tables(8, 32, 10000.0)
+    x = rng.normal(0, 1, (5, 3 * 8)).astype(np.float32)
+    pos = [0, 3, 31, 7, 7]
+    got = oracle.rope(x, 3, 8, cos, sin, pos)
+    xd = x.reshape(5, 3, 8).astype(np.float64)
+    rot = np.concatenate([-xd[..., 4:], xd[..., :4]], -1)
+    want = xd * cos[pos][:, None, :] + rot * sin[pos][:, None, :]
+    assert np.allclose(got, want, atol=1e-6)
+    assert np.array_equal(got[0], x[0].reshape(3, 8))  # position 0: cos 1, sin 0
