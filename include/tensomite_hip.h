@@ -300,7 +300,9 @@ int tmh_rope_write(uint64_t x, uint32_t ldx, uint32_t tokens, uint32_t heads, ui
  * h / (heads / kv_heads). `table` (int32, device) holds per token its cache
  * row, the last position it sees and the positions its row holds
  * (composite.cr:201-212). q rows are `ldq` apart ([heads, width] each), dst
- * rows `ld_dst` apart. width must be a multiple of 4; capacity at most 16,000. */
+ * rows `ld_dst` apart. width must be a multiple of 4, and the positions and
+ * staged values must fit the kernel's 64 KB of LDS: (4·width + capacity +
+ * 8192) floats (capacity up to 7,936 at width 64). */
 int tmh_attention(uint64_t q, uint32_t ldq, uint32_t tokens, uint32_t heads, uint64_t keys, uint64_t values,
                   uint32_t cache_rows, uint32_t kv_heads, uint32_t capacity, uint32_t width, uint64_t table,
                   float scale, uint64_t dst, uint32_t ld_dst);
@@ -342,7 +344,8 @@ typedef struct tmh_llama_config {
  * addresses) the norms [width], the merged qkv [(heads + 2·kv_heads)·head_width,
  * width] with q and k rows in Hugging Face order (llama.cr:226-235), o
  * [width, heads·head_width], the merged gate_up [2·hidden, width] and down
- * [width, hidden]. The arrays are read during tmh_llama_create only. */
+ * [width, hidden]. The norms must be 16-byte aligned. The arrays are read
+ * during tmh_llama_create only. */
 typedef struct tmh_llama_weights {
     uint64_t embed, head, norm;
     const uint64_t* attn_norm;

@@ -26,6 +26,7 @@
 //
 // Built, like every source of the library, with -ffp-contract=off and
 // correctly rounded f32 division and square root.
+#include "tmh_device.h"
 #include "tmh_internal.h"
 
 namespace tmh {
@@ -70,31 +71,112 @@ __device__ __forceinline__ void report(int32_t* errors, int32_t value, int32_t l
     }
 }
 
+// ------------------------------------------------------------ ordered sums
+
+// Σ v[0..n) in index order from 0.0f, read from LDS by broadcast (every lane
+// computes the same sum). The adds form one dependent chain, the only
+// instructions on it; the reads of the next 32 values are issued before
+// the adds of the current 32, from two register buffers used in turn.
+__device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s += b[i].x;
+        s += b[i].y;
+        s += b[i].z;
+        s += b[i].w;
+    }
+}
+
+__device__ __forceinline__ void read32(float4 (&b)[8], const float4* v4, uint32_t j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = v4[j + i];
+}
+
+__device__ __forceinline__ float ordered_sum(const float* v, uint32_t n) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    const uint32_t n4 = n >> 2;
+    float s = 0.0f;
+    uint32_t j = 0;
+    if (n4 >= 16) {
+        float4 a[8], b[8];
+        read32(a, v4, 0);
+        for (j = 0; j + 32 <= n4; j += 16) {
+            read32(b, v4, j + 8);
+            add32(s, a);
+            read32(a, v4, j + 16);
+            add32(s, b);
+        }
+        // a holds [j, j + 8); [j + 8, n4) remain
+        if (j + 16 <= n4) {
+            read32(b, v4, j + 8);
+            add32(s, a);
+            add32(s, b);
+            j += 16;
+        } else {
+            add32(s, a);
+            j += 8;
+        }
+    }
+    for (; j < n4; ++j) {
+        const float4 c = v4[j];
+        s += c.x;
+        s += c.y;
+        s += c.z;
+        s += c.w;
+    }
+    for (uint32_t i = n4 << 2; i < n; ++i) s += v[i];
+    return s;
+}
+
+// ordered_sum by one lane (an LDS read then feeds one lane, not 256), the
+// result shared through LDS. Every thread calls it.
+__device__ __forceinline__ float shared_sum(const float* v, uint32_t n) {
+    __shared__ float result;
+    if (threadIdx.x == 0) result = ordered_sum(v, n);
+    __syncthreads();
+    return result;
+}
+
 // ------------------------------------------------------------------ RMSNorm
 
-// One workgroup per row. The row is staged in LDS; every wave then folds
-// the squares in index order (ds_read_b128 broadcasts, four adds each), so
-// each wave holds the root without another barrier.
+// Largest row the LDS kernels stage: the row and its squares, 64 KB.
+constexpr uint32_t RMSNORM_LDS_ROW = 8192;
+
+// Stages row x (n values) and its squares in LDS, then returns the root
+// sqrt(Σx²/n + eps), the squares folded in index order by every wave.
+__device__ __forceinline__ float stage_root(const float* __restrict__ xr, uint32_t n, float eps, float* row,
+                                            float* sq) {
+    // four loads in flight per thread before any store
+    for (uint32_t j0 = threadIdx.x; j0 < n; j0 += 1024u) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = j0 + 256u * u;
+            v[u] = j < n ? xr[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = j0 + 256u * u;
+            if (j < n) {
+                row[j] = v[u];
+                sq[j] = v[u] * v[u];
+            }
+        }
+    }
+    __syncthreads();
+    const float squares = shared_sum(sq, n);
+    return __builtin_sqrtf(squares / (float)n + eps);
+}
+
+// One workgroup per row: the squares in parallel, their ordered sum, then
+// x / root · w in parallel.
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, uint32_t ldx,
                                                  const float* __restrict__ w, uint32_t n, float eps,
                                                  float* __restrict__ dst, uint32_t ld_dst) {
-    extern __shared__ float4 row4[];
-    float* row = reinterpret_cast<float*>(row4);
-    const float* xr = x + (size_t)blockIdx.x * ldx;
-    for (uint32_t j = threadIdx.x; j < n; j += 256u) row[j] = xr[j];
-    __syncthreads();
-    float squares = 0.0f;
-    const uint32_t n4 = n >> 2;
-#pragma unroll 8
-    for (uint32_t j = 0; j < n4; ++j) {
-        const float4 v = row4[j];
-        squares += v.x * v.x;
-        squares += v.y * v.y;
-        squares += v.z * v.z;
-        squares += v.w * v.w;
-    }
-    for (uint32_t j = n4 << 2; j < n; ++j) squares += row[j] * row[j];
-    const float root = __builtin_sqrtf(squares / (float)n + eps);
+    extern __shared__ float4 lds4[];
+    float* row = reinterpret_cast<float*>(lds4);
+    float* sq = row + ((n + 3u) & ~3u);
+    const float root = stage_root(x + (size_t)blockIdx.x * ldx, n, eps, row, sq);
     float* out = dst + (size_t)blockIdx.x * ld_dst;
     if (w) {
         for (uint32_t j = threadIdx.x; j < n; j += 256u) {
@@ -103,6 +185,50 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, ui
         }
     } else {
         for (uint32_t j = threadIdx.x; j < n; j += 256u) out[j] = row[j] / root;
+    }
+}
+
+// RMSNorm then the activation quantiser, one workgroup per row: each
+// 8-lane group normalises 4 values a lane of a block of 32 and quantises the
+// block (quantize_activations, quant.cr:428-442, on the normalised row), into
+// `act` laid out as the quantise pass lays it out (n must be a multiple of 32).
+__global__ __launch_bounds__(256) void k_rmsnorm_quantise(const float* __restrict__ x, uint32_t ldx,
+                                                          const float* __restrict__ w, uint32_t n, float eps,
+                                                          Activations act) {
+    extern __shared__ float4 lds4[];
+    float* row = reinterpret_cast<float*>(lds4);
+    float* sq = row + n;
+    const uint32_t r = blockIdx.x;
+    const uint32_t nb = n >> 5, sub = threadIdx.x & 7u;
+    // this lane's weights, loaded before the fold (n ≤ 8192: at most 8 passes)
+    float4 wv[RMSNORM_LDS_ROW / 1024];
+#pragma unroll
+    for (uint32_t pass = 0; pass < RMSNORM_LDS_ROW / 1024; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        wv[pass] = (w && blk < nb) ? *reinterpret_cast<const float4*>(w + blk * 32u + sub * 4u)
+                                   : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    const float root = stage_root(x + (size_t)r * ldx, n, eps, row, sq);
+#pragma unroll
+    for (uint32_t pass = 0; pass < RMSNORM_LDS_ROW / 1024; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        if (blk >= nb) break;
+        const uint32_t j = blk * 32u + sub * 4u;
+        const float wj[4] = {wv[pass].x, wv[pass].y, wv[pass].z, wv[pass].w};
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q = row[j + i] / root;
+            v[i] = w ? q * wj[i] : q;
+        }
+        const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+        *(uint32_t*)((int8_t*)act.qs + (size_t)r * n + j) = q.packed;
+        if (sub == 0) {
+            const size_t g = (size_t)r * nb + blk;
+            ((float*)act.scales)[g] = q.scale;
+            ((float*)act.sums)[g] = q.sum;
+            ((int32_t*)act.totals)[g] = q.total;
+        }
     }
 }
 
@@ -122,18 +248,26 @@ __global__ __launch_bounds__(256) void k_rmsnorm_wide(const float* __restrict__ 
     }
 }
 
-// Largest row the LDS kernel stages (64 KB).
-constexpr uint32_t RMSNORM_LDS_ROW = 16384;
-
 hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
                           float* dst, uint32_t ld_dst, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (n <= RMSNORM_LDS_ROW) {
-        const size_t lds = ((size_t)n + 3u) / 4u * 16u;
+        const size_t lds = 2u * (((size_t)n + 3u) & ~(size_t)3u) * sizeof(float);
         hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), lds, stream, x, ldx, w, n, eps, dst, ld_dst);
     } else {
         hipLaunchKernelGGL(k_rmsnorm_wide, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, dst, ld_dst);
     }
+    return hipGetLastError();
+}
+
+bool rmsnorm_quantise_fits(uint32_t n) { return n > 0 && n % 32u == 0 && n <= RMSNORM_LDS_ROW; }
+
+hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
+                                   Activations act, hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    if (!rmsnorm_quantise_fits(n)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm_quantise, dim3(rows), dim3(256), 2u * (size_t)n * sizeof(float), stream, x, ldx, w,
+                       n, eps, act);
     return hipGetLastError();
 }
 
@@ -202,18 +336,213 @@ __device__ __forceinline__ float wave_top(float top) {
     return top;
 }
 
-// One workgroup per (query token, head). Scores of all positions in
-// parallel (each a column-order dot product), the top by a tree of
-// comparisons (a maximum is exact in any order; a NaN only counts at
-// position 0, as the host's `position == 0 || x > top` has it), the
-// exponentials in parallel, then the total and the weighted values as
-// position-order folds.
+// Bytes of one staged chunk of values: positions × width floats.
+constexpr uint32_t ATT_CHUNK_FLOATS = 4096;
+
+__device__ __forceinline__ uint32_t chunk_positions(uint32_t width) {
+    const uint32_t ch = ATT_CHUNK_FLOATS / width;
+    return ch >= 8u ? ch & ~3u : 4u;
+}
+
+// LDS layout of the attention kernels, in floats: q, the current key and
+// value, the row's attended outputs, the scores, then two value chunks.
+struct AttLds {
+    float *q, *kcur, *vcur, *out, *sc, *vbuf;
+};
+
+__device__ __forceinline__ AttLds att_lds(float* base, uint32_t width, uint32_t capacity) {
+    const uint32_t w4 = (width + 3u) & ~3u;
+    AttLds l;
+    l.q = base;
+    l.kcur = base + w4;
+    l.vcur = base + 2u * w4;
+    l.out = base + 3u * w4;
+    l.sc = base + 4u * w4;
+    l.vbuf = l.sc + ((capacity + 3u) & ~3u);
+    return l;
+}
+
+size_t attention_lds(uint32_t width, uint32_t capacity) {
+    const size_t w4 = (width + 3u) & ~3u;
+    const size_t ch = ATT_CHUNK_FLOATS / width >= 8u ? (ATT_CHUNK_FLOATS / width) & ~3u : 4u;
+    return (4u * w4 + ((capacity + 3u) & ~3u) + 2u * ch * width) * sizeof(float);
+}
+
+// Writes the products weight_p · v_p[c] of value positions [p0, p0 + count)
+// of one head into `dst`, rows of `width` (each product rounded once, as
+// the host's `scores[p] / total * v` rounds it), position `cur` (if in range)
+// from `vcur` instead of the cache; threads from `first` on, `stride` apart,
+// take float4s.
+__device__ __forceinline__ void stage_products(float* dst, const float* __restrict__ vb, const float* wts,
+                                               uint32_t width, uint32_t p0, uint32_t count, int32_t cur,
+                                               const float* vcur, uint32_t first, uint32_t stride) {
+    const uint32_t per = width >> 2;
+    const uint32_t total = count * per;
+    constexpr int U = 8;  // loads in flight per thread before any store
+    for (uint32_t i0 = threadIdx.x - first; i0 < total; i0 += U * stride) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t i = i0 + u * stride;
+            const uint32_t p = p0 + i / per, c = (i % per) * 4u;
+            if (i < total)
+                v[u] = *reinterpret_cast<const float4*>((int32_t)p == cur ? vcur + c : vb + (size_t)p * width + c);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t i = i0 + u * stride;
+            if (i < total) {
+                const uint32_t p = p0 + i / per, c = (i % per) * 4u;
+                const float w = wts[p];
+                float4 prod;
+                prod.x = w * v[u].x;
+                prod.y = w * v[u].y;
+                prod.z = w * v[u].z;
+                prod.w = w * v[u].w;
+                *reinterpret_cast<float4*>(dst + (size_t)(p - p0) * width + c) = prod;
+            }
+        }
+    }
+}
+
+// acc + Σ_{p < cnt} pc[p·stride], in order: the reads of the next 16 values
+// are issued before the adds of the current 16, from two register buffers.
+__device__ __forceinline__ float fold_column(float acc, const float* pc, uint32_t stride, uint32_t cnt) {
+    float a[16], b[16];
+    uint32_t p = 0;
+    if (cnt >= 32u) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = pc[(size_t)i * stride];
+        for (; p + 48u <= cnt; p += 32u) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) b[i] = pc[(size_t)(p + 16u + i) * stride];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc += a[i];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) a[i] = pc[(size_t)(p + 32u + i) * stride];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc += b[i];
+        }
+        // a holds [p, p + 16)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc += a[i];
+        p += 16u;
+    }
+    for (; p < cnt; ++p) acc += pc[(size_t)p * stride];
+    return acc;
+}
+
+// The attention of one query row and head, with the host's bits
+// (host.cr:408-440): q in l.q; keys and values of positions [0, n) in the
+// cache at kb/vb, but position `cur` (if ≥ 0) in l.kcur/l.vcur; positions
+// past `last` masked. Leaves the outputs in l.out. Every thread calls it.
+__device__ void attend(const AttLds& l, const float* __restrict__ kb, const float* __restrict__ vb, uint32_t width,
+                       uint32_t n, int32_t last, int32_t cur, float scale) {
+    __shared__ float tops[4];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t w4n = width >> 2;
+    const float4* q4 = reinterpret_cast<const float4*>(l.q);
+
+    // scores, one position a thread: q·k in column order, ·scale, mask
+    float top = -__builtin_inff();
+    for (uint32_t p = tid; p < n; p += 256u) {
+        const float4* k4 = reinterpret_cast<const float4*>((int32_t)p == cur ? l.kcur : kb + (size_t)p * width);
+        float dot = 0.0f;
+        // the key row in pieces of 16 float4, each piece's loads issued together
+        for (uint32_t c0 = 0; c0 < w4n; c0 += 16u) {
+            float4 k[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (c0 + u < w4n) k[u] = k4[c0 + u];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (c0 + u < w4n) {
+                    const float4 q = q4[c0 + u];
+                    dot += q.x * k[u].x;
+                    dot += q.y * k[u].y;
+                    dot += q.z * k[u].z;
+                    dot += q.w * k[u].w;
+                }
+            }
+        }
+        float x = dot * scale;
+        // The causal mask adds -inf past the last position seen; its 0
+        // elsewhere only turns a -0 score into +0, which changes no later bit.
+        if ((int32_t)p > last) x = x + -__builtin_inff();
+        l.sc[p] = x;
+        top = x > top ? x : top;
+    }
+    top = wave_top(top);
+    if ((tid & 63u) == 0) tops[tid >> 6] = top;
+    __syncthreads();
+    top = tops[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) top = tops[i] > top ? tops[i] : top;
+    if (l.sc[0] != l.sc[0]) top = l.sc[0];  // the host's top is a NaN at position 0
+
+    for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = maths_exp(l.sc[p] - top);
+    __syncthreads();
+    const float total = shared_sum(l.sc, n);
+    for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = l.sc[p] / total;
+    __syncthreads();
+
+    // Σ_p weight_p · v_p[c] in position order, one lane per column: the
+    // products are formed in parallel as the values stage through LDS in
+    // chunks (the waves not folding stage the next chunk while the folding
+    // waves add up this one), so the fold is a chain of adds.
+    const uint32_t ch = chunk_positions(width);
+    const uint32_t chunks = (n + ch - 1u) / ch;
+    const uint32_t folding = ((width + 63u) >> 6) << 6;  // threads of the folding waves
+    const bool overlap = folding < 256u;
+    const uint32_t first_loader = overlap ? folding : 0u;
+    stage_products(l.vbuf, vb, l.sc, width, 0, min(ch, n), cur, l.vcur, 0, 256u);
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t k = 0; k < chunks; ++k) {
+        const uint32_t p0 = k * ch, cnt = min(ch, n - p0);
+        const float* buf = l.vbuf + (size_t)(k & 1u) * ch * width;
+        if (k + 1u < chunks && (!overlap || tid >= first_loader)) {
+            const uint32_t q0 = p0 + ch;
+            stage_products(l.vbuf + (size_t)((k + 1u) & 1u) * ch * width, vb, l.sc, width, q0, min(ch, n - q0), cur,
+                           l.vcur, first_loader, 256u - first_loader);
+        }
+        if (!overlap) __syncthreads();
+        if (tid < width) acc = fold_column(acc, buf + tid, width, cnt);
+        __syncthreads();
+    }
+    if (tid < width) l.out[tid] = acc;
+    __syncthreads();
+}
+
+// Writes the row's attended outputs (l.out, `width`) for token t, head h:
+// the F32 values, and, when act.qs is set, their quantised blocks as
+// quantize_activations makes them for the o product's row (width a
+// multiple of 32; the row holds heads · width values).
+__device__ __forceinline__ void emit(const AttLds& l, float* out, uint32_t width, Activations act, uint32_t t,
+                                     uint32_t h, uint32_t heads) {
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t c = tid; c < width; c += 256u) out[c] = l.out[c];
+    if (!act.qs) return;
+    const uint32_t blocks = width >> 5;
+    const uint32_t k = heads * width, nb = k >> 5;
+    const uint32_t blk = tid >> 3, sub = tid & 7u;
+    if (blk < blocks) {
+        const float4 v = *reinterpret_cast<const float4*>(l.out + blk * 32u + sub * 4u);
+        const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
+        const uint32_t g = h * blocks + blk;
+        *(uint32_t*)((int8_t*)act.qs + (size_t)t * k + g * 32u + sub * 4u) = q.packed;
+        if (sub == 0) {
+            ((float*)act.scales)[(size_t)t * nb + g] = q.scale;
+            ((float*)act.sums)[(size_t)t * nb + g] = q.sum;
+            ((int32_t*)act.totals)[(size_t)t * nb + g] = q.total;
+        }
+    }
+}
+
+// One workgroup per (query token, head) of cached keys and values.
 __global__ __launch_bounds__(256) void k_attention(Attention a) {
     extern __shared__ float4 lds4[];
-    float* qv = reinterpret_cast<float*>(lds4);
-    const uint32_t w4 = (a.width + 3u) & ~3u;
-    float* sc = qv + w4;
-    __shared__ float tops[4];
+    const AttLds l = att_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
     const uint32_t tid = threadIdx.x;
     const uint32_t t = blockIdx.x / a.heads;
     const uint32_t h = blockIdx.x - t * a.heads;
@@ -227,93 +556,77 @@ __global__ __launch_bounds__(256) void k_attention(Attention a) {
     }
     const uint32_t kv = h / (a.heads / a.kv_heads);
     const size_t base = ((size_t)row * a.kv_heads + kv) * a.capacity * a.width;
-    const float* kb = a.keys + base;
-    const float* vb = a.values + base;
     const float* qh = a.q + (size_t)t * a.ldq + (size_t)h * a.width;
-    for (uint32_t c = tid; c < a.width; c += 256u) qv[c] = qh[c];
+    for (uint32_t c = tid; c < a.width; c += 256u) l.q[c] = qh[c];
     __syncthreads();
-
-    const uint32_t n = (uint32_t)length;
-    const float4* q4 = reinterpret_cast<const float4*>(qv);
-    float top = -__builtin_inff();
-    for (uint32_t p = tid; p < n; p += 256u) {
-        const float4* k4 = reinterpret_cast<const float4*>(kb + (size_t)p * a.width);
-        float dot = 0.0f;
-        for (uint32_t c = 0; c < (a.width >> 2); ++c) {
-            const float4 q = q4[c];
-            const float4 k = k4[c];
-            dot += q.x * k.x;
-            dot += q.y * k.y;
-            dot += q.z * k.z;
-            dot += q.w * k.w;
-        }
-        float x = dot * a.scale;
-        // The causal mask adds -inf past the row's last position; its 0
-        // elsewhere only turns a -0 score into +0, which changes no later bit.
-        if ((int32_t)p > last) x = x + -__builtin_inff();
-        sc[p] = x;
-        top = x > top ? x : top;
-    }
-    top = wave_top(top);
-    if ((tid & 63u) == 0) tops[tid >> 6] = top;
-    __syncthreads();
-    top = tops[0];
-#pragma unroll
-    for (int i = 1; i < 4; ++i) top = tops[i] > top ? tops[i] : top;
-    if (sc[0] != sc[0]) top = sc[0];
-
-    for (uint32_t p = tid; p < n; p += 256u) sc[p] = maths_exp(sc[p] - top);
-    __syncthreads();
-
-    // The total, in position order, by every wave.
-    const float4* s4 = reinterpret_cast<const float4*>(sc);
-    float total = 0.0f;
-    const uint32_t n4 = n >> 2;
-#pragma unroll 8
-    for (uint32_t j = 0; j < n4; ++j) {
-        const float4 e = s4[j];
-        total += e.x;
-        total += e.y;
-        total += e.z;
-        total += e.w;
-    }
-    for (uint32_t j = n4 << 2; j < n; ++j) total += sc[j];
-    __syncthreads();
-    for (uint32_t p = tid; p < n; p += 256u) sc[p] = sc[p] / total;
-    __syncthreads();
-
-    // Σ_p weight_p · v_p[c], in position order: one lane per column.
-    for (uint32_t c = tid; c < a.width; c += 256u) {
-        const float* vc = vb + c;
-        float acc = 0.0f;
-        uint32_t p = 0;
-        for (; p + 8u <= n; p += 8u) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = vc[(size_t)(p + i) * a.width];
-            const float4 w0 = s4[p >> 2], w1 = s4[(p >> 2) + 1u];
-            acc += w0.x * v[0];
-            acc += w0.y * v[1];
-            acc += w0.z * v[2];
-            acc += w0.w * v[3];
-            acc += w1.x * v[4];
-            acc += w1.y * v[5];
-            acc += w1.z * v[6];
-            acc += w1.w * v[7];
-        }
-        for (; p < n; ++p) acc += sc[p] * vc[(size_t)p * a.width];
-        out[c] = acc;
-    }
-}
-
-size_t attention_lds(uint32_t width, uint32_t capacity) {
-    return ((size_t)((width + 3u) & ~3u) + ((capacity + 3u) & ~3u)) * sizeof(float);
+    attend(l, a.keys + base, a.values + base, a.width, (uint32_t)length, last, -1, a.scale);
+    emit(l, out, a.width, a.act, t, h, a.heads);
 }
 
 hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream) {
     if (tokens == 0 || a.heads == 0) return hipSuccess;
     const size_t lds = attention_lds(a.width, a.capacity);
     hipLaunchKernelGGL(k_attention, dim3(tokens * a.heads), dim3(256), lds, stream, a);
+    return hipGetLastError();
+}
+
+// A decode step's attention with its RoPE and cache write fused: token t
+// is its cache row's one new position (slot = row·capacity + position,
+// table (row, position, position + 1)). The workgroup of query head h
+// rotates its q head and its kv head's new key, takes the new value, and --
+// the first query head of the group only -- writes both into the caches;
+// the new position is attended from LDS, earlier ones from the caches.
+__global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite r) {
+    extern __shared__ float4 lds4[];
+    const AttLds l = att_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
+    const uint32_t tid = threadIdx.x;
+    const uint32_t t = blockIdx.x / a.heads;
+    const uint32_t h = blockIdx.x - t * a.heads;
+    const uint32_t width = a.width;
+    const int32_t slot = r.slots[t];
+    const int32_t row = a.table[3u * t], last = a.table[3u * t + 1u], length = a.table[3u * t + 2u];
+    const int32_t cap = (int32_t)a.capacity;
+    float* out = a.dst + (size_t)t * a.ld_dst + (size_t)h * width;
+    if (slot < 0 || slot >= (int32_t)a.cache_rows * cap || row != slot / cap || last != slot % cap ||
+        length != last + 1) {
+        for (uint32_t c = tid; c < width; c += 256u) out[c] = 0.0f;
+        if (tid == 0 && h == 0) report(a.errors, slot, (int32_t)a.cache_rows * cap);
+        return;
+    }
+    const uint32_t group = a.heads / a.kv_heads, kv = h / group;
+    const uint32_t pos = (uint32_t)last, half = width >> 1;
+    const float* src = r.x + (size_t)t * r.ldx;
+    const float* cs = r.cos + (size_t)pos * width;
+    const float* sn = r.sin + (size_t)pos * width;
+    const float* qs = src + (size_t)h * width;
+    const float* ks = src + (size_t)(a.heads + kv) * width;
+    const float* vs = src + (size_t)(a.heads + a.kv_heads + kv) * width;
+    const size_t base = ((size_t)row * a.kv_heads + kv) * a.capacity * width;
+    for (uint32_t c = tid; c < width; c += 256u) {
+        const uint32_t o = c < half ? c + half : c - half;
+        const float qp = qs[o], kp = ks[o];
+        const float qr = c < half ? qp * -1.0f : qp;
+        const float kr = c < half ? kp * -1.0f : kp;
+        const float ql = qs[c] * cs[c], qg = qr * sn[c];
+        const float kl = ks[c] * cs[c], kg = kr * sn[c];
+        l.q[c] = ql + qg;
+        const float k = kl + kg, v = vs[c];
+        l.kcur[c] = k;
+        l.vcur[c] = v;
+        if (h % group == 0) {
+            r.keys[base + (size_t)pos * width + c] = k;
+            r.values[base + (size_t)pos * width + c] = v;
+        }
+    }
+    __syncthreads();
+    attend(l, a.keys + base, a.values + base, width, (uint32_t)length, last, last, a.scale);
+    emit(l, out, width, a.act, t, h, a.heads);
+}
+
+hipError_t launch_attention_decode(const Attention& a, const RopeWrite& r, uint32_t tokens, hipStream_t stream) {
+    if (tokens == 0 || a.heads == 0) return hipSuccess;
+    const size_t lds = attention_lds(a.width, a.capacity);
+    hipLaunchKernelGGL(k_attention_decode, dim3(tokens * a.heads), dim3(256), lds, stream, a, r);
     return hipGetLastError();
 }
 
@@ -330,6 +643,46 @@ __global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ gate, 
     const float d = e + 1.0f;
     const float q = g / d;
     dst[i] = q * value[(size_t)r * ld + j];
+}
+
+// SwiGLU then the activation quantiser: each 8-lane group takes a block of
+// 32 outputs of a row (4 a lane) and quantises it into `act` (n a multiple
+// of 32), as the quantise pass would quantise SwiGLU's output.
+__global__ __launch_bounds__(256) void k_swiglu_quantise(const float* __restrict__ gate,
+                                                         const float* __restrict__ value, uint32_t ld, uint32_t n,
+                                                         uint32_t blocks, Activations act) {
+    const uint32_t g = (blockIdx.x * 256u + threadIdx.x) >> 3;
+    const uint32_t sub = threadIdx.x & 7u;
+    if (g >= blocks) return;  // all 8 lanes of a block leave together
+    const uint32_t nb = n >> 5;
+    const uint32_t r = g / nb, blk = g - r * nb;
+    const uint32_t j = blk * 32u + sub * 4u;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float gt = gate[(size_t)r * ld + j + i];
+        const float e = maths_exp(-gt);
+        const float d = e + 1.0f;
+        const float q = gt / d;
+        v[i] = q * value[(size_t)r * ld + j + i];
+    }
+    const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+    *(uint32_t*)((int8_t*)act.qs + (size_t)r * n + j) = q.packed;
+    if (sub == 0) {
+        ((float*)act.scales)[g] = q.scale;
+        ((float*)act.sums)[g] = q.sum;
+        ((int32_t*)act.totals)[g] = q.total;
+    }
+}
+
+hipError_t launch_swiglu_quantise(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n,
+                                  Activations act, hipStream_t stream) {
+    const uint64_t blocks = (uint64_t)rows * (n >> 5);
+    if (blocks == 0) return hipSuccess;
+    if (n % 32u != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_swiglu_quantise, dim3((uint32_t)((blocks * 8u + 255u) / 256u)), dim3(256), 0, stream, gate,
+                       value, ld, n, (uint32_t)blocks, act);
+    return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n, float* dst,
@@ -365,18 +718,15 @@ __device__ __forceinline__ void better(float& v, int32_t& i, float ov, int32_t o
     }
 }
 
-// One workgroup per row: each thread the first highest of its strided
-// elements, then a tree over candidates. As the host's loop (`x[i] >
-// x[best]` from best = 0) never moves to a NaN, NaNs are no candidates, and
-// a NaN at index 0 keeps index 0.
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, uint32_t ldx, uint32_t n,
-                                                int32_t* __restrict__ ids) {
+// The first highest of elements [j0, j1) of row xr across the workgroup
+// (NaNs are no candidates: the host's `x[i] > x[best]` never moves to one).
+__device__ __forceinline__ void block_best(const float* __restrict__ xr, uint32_t j0, uint32_t j1, float& v,
+                                           int32_t& i) {
     __shared__ float vs[4];
     __shared__ int32_t is[4];
-    const float* xr = x + (size_t)blockIdx.x * ldx;
-    float v = 0.0f;
-    int32_t i = -1;
-    for (uint32_t j = threadIdx.x; j < n; j += 256u) {
+    v = 0.0f;
+    i = -1;
+    for (uint32_t j = j0 + threadIdx.x; j < j1; j += 256u) {
         const float e = xr[j];
         if (e == e && (i < 0 || e > v)) {
             v = e;
@@ -394,8 +744,17 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, uin
         is[threadIdx.x >> 6] = i;
     }
     __syncthreads();
+    for (int k = 0; k < 4; ++k) better(v, i, vs[k], is[k]);
+}
+
+// One workgroup per row: as the host's loop, a NaN at index 0 keeps index 0.
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, uint32_t ldx, uint32_t n,
+                                                int32_t* __restrict__ ids) {
+    const float* xr = x + (size_t)blockIdx.x * ldx;
+    float v;
+    int32_t i;
+    block_best(xr, 0, n, v, i);
     if (threadIdx.x == 0) {
-        for (int k = 1; k < 4; ++k) better(v, i, vs[k], is[k]);
         const float first = xr[0];
         ids[blockIdx.x] = (first != first || i < 0) ? 0 : i;
     }
@@ -407,21 +766,51 @@ hipError_t launch_argmax(const float* x, uint32_t ldx, uint32_t rows, uint32_t n
     return hipGetLastError();
 }
 
+// Elements of a row per workgroup of the split argmax.
+constexpr uint32_t ARGMAX_CHUNK = 2048;
+
+uint32_t argmax_chunks(uint32_t n) { return (n + ARGMAX_CHUNK - 1u) / ARGMAX_CHUNK; }
+
+// Split argmax, first half: workgroup (row, chunk) writes the first highest
+// of its chunk (value, index or -1).
+__global__ __launch_bounds__(256) void k_argmax_chunks(const float* __restrict__ x, uint32_t ldx, uint32_t n,
+                                                       uint32_t chunks, float* __restrict__ values,
+                                                       int32_t* __restrict__ index) {
+    const uint32_t r = blockIdx.x / chunks, c = blockIdx.x - r * chunks;
+    const uint32_t j0 = c * ARGMAX_CHUNK, j1 = min(n, j0 + ARGMAX_CHUNK);
+    float v;
+    int32_t i;
+    block_best(x + (size_t)r * ldx, j0, j1, v, i);
+    if (threadIdx.x == 0) {
+        values[blockIdx.x] = v;
+        index[blockIdx.x] = i;
+    }
+}
+
 // ------------------------------------------------------------- decode step
 
 // After a decode step over `rows` sequences (token r of the step belongs to
-// cache row r): logs each chosen id, and moves each row's slot and
-// attention entry one position on. A row whose cache is full gets a slot
-// of -1 and an entry one past its capacity, so a step that would run it
-// anyway is reported by the RoPE and attention kernels instead of writing
-// into the next row.
-__global__ void k_advance(uint32_t rows, const int32_t* __restrict__ chosen, int32_t* __restrict__ log,
-                          uint32_t log_stride, int32_t* __restrict__ steps, int32_t* __restrict__ slots,
-                          int32_t* __restrict__ table, uint32_t capacity) {
+// cache row r): picks each row's token from the split argmax's chunks (in
+// chunk order, so ties keep the lower index; a NaN logit at index 0 keeps
+// index 0), logs it, and moves the row's slot and attention entry one
+// position on. A row whose cache is full gets a slot of -1 and an entry one
+// past its capacity, so a step that would run it anyway is reported by the
+// RoPE and attention kernels instead of writing into the next row.
+__global__ void k_advance(uint32_t rows, const float* __restrict__ logits, uint32_t vocab, uint32_t chunks,
+                          const float* __restrict__ values, const int32_t* __restrict__ index,
+                          int32_t* __restrict__ ids, int32_t* __restrict__ log, uint32_t log_stride,
+                          int32_t* __restrict__ steps, int32_t* __restrict__ slots, int32_t* __restrict__ table,
+                          uint32_t capacity) {
     const uint32_t r = blockIdx.x * 64u + threadIdx.x;
     if (r >= rows) return;
+    float v = 0.0f;
+    int32_t i = -1;
+    for (uint32_t c = 0; c < chunks; ++c) better(v, i, values[r * chunks + c], index[r * chunks + c]);
+    const float first = logits[(size_t)r * vocab];
+    const int32_t chosen = (first != first || i < 0) ? 0 : i;
+    ids[r] = chosen;
     const int32_t step = steps[r];
-    if (step >= 0 && step < (int32_t)log_stride) log[(size_t)r * log_stride + step] = chosen[r];
+    if (step >= 0 && step < (int32_t)log_stride) log[(size_t)r * log_stride + step] = chosen;
     steps[r] = step + 1;
     const int32_t length = table[3u * r + 2u];
     const bool full = length < 0 || length >= (int32_t)capacity;
@@ -430,11 +819,15 @@ __global__ void k_advance(uint32_t rows, const int32_t* __restrict__ chosen, int
     table[3u * r + 2u] = full ? (int32_t)capacity + 1 : length + 1;
 }
 
-hipError_t launch_advance(uint32_t rows, const int32_t* chosen, int32_t* log, uint32_t log_stride, int32_t* steps,
-                          int32_t* slots, int32_t* table, uint32_t capacity, hipStream_t stream) {
+hipError_t launch_choose_advance(const float* logits, uint32_t rows, uint32_t vocab, float* values, int32_t* index,
+                                 int32_t* ids, int32_t* log, uint32_t log_stride, int32_t* steps, int32_t* slots,
+                                 int32_t* table, uint32_t capacity, hipStream_t stream) {
     if (rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_advance, dim3((rows + 63u) / 64u), dim3(64), 0, stream, rows, chosen, log, log_stride, steps,
-                       slots, table, capacity);
+    const uint32_t chunks = argmax_chunks(vocab);
+    hipLaunchKernelGGL(k_argmax_chunks, dim3(rows * chunks), dim3(256), 0, stream, logits, vocab, vocab, chunks, values,
+                       index);
+    hipLaunchKernelGGL(k_advance, dim3((rows + 63u) / 64u), dim3(64), 0, stream, rows, logits, vocab, chunks, values,
+                       index, ids, log, log_stride, steps, slots, table, capacity);
     return hipGetLastError();
 }
 

@@ -1,0 +1,79 @@
+// Device helpers shared by the kernel sources of libtensomite_hip.so: F16
+// conversions and the activation quantiser's arithmetic for one lane of an
+// 8-lane block group.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tmh {
+
+// ------------------------------------------------------------------ halves
+
+// Returns the half with bits `bits` (low 16 bits) as a float: exact for every
+// half that is not a NaN (F16#to_f32, f16.cr:44-57).
+__device__ __forceinline__ float half_value(uint32_t bits) {
+    union {
+        uint16_t u;
+        _Float16 h;
+    } v;
+    v.u = (uint16_t)bits;
+    return (float)v.h;
+}
+
+// Returns x rounded to the nearest half, ties to even, as a float: F16.new
+// (f16.cr:29-41) -- NaN becomes 0x7e00, values from 65520 up overflow,
+// subnormals are x * 2^24 rounded to even.
+__device__ __forceinline__ float round_to_half(float x) {
+    uint32_t word = __float_as_uint(x);
+    uint32_t sign = (word >> 16) & 0x8000u;
+    uint32_t magnitude = word & 0x7fffffffu;
+    uint32_t h;
+    if (magnitude >= 0x7f800000u) h = sign | (magnitude > 0x7f800000u ? 0x7e00u : 0x7c00u);
+    else if (magnitude >= 0x477ff000u) h = sign | 0x7c00u;
+    else if (magnitude < 0x38800000u) h = sign | (uint32_t)__builtin_rintf(__uint_as_float(magnitude) * 16777216.0f);
+    else h = sign | ((magnitude - 0x38000000u + 0xfffu + ((magnitude >> 13) & 1u)) >> 13);
+    return half_value(h);
+}
+
+// ------------------------------------------------------ activation quantise
+
+// The quantised form of 4 of a block's 32 activations, held by one lane of
+// an 8-lane group (all 8 lanes active): the group's amax and Σq reduced over
+// the 8 lanes, then quantize_activations' arithmetic (quant.cr:428-442).
+struct Q8Quad {
+    uint32_t packed;  // the 4 int8 values
+    float scale;      // F16(d)
+    float sum;        // F16(float(Σq) · d)
+    int total;        // Σq over the block
+};
+
+__device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, float v3) {
+    float amax = fabsf(v0);
+    amax = fabsf(v1) > amax ? fabsf(v1) : amax;
+    amax = fabsf(v2) > amax ? fabsf(v2) : amax;
+    amax = fabsf(v3) > amax ? fabsf(v3) : amax;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) {
+        float other = __shfl_xor(amax, width, 8);
+        amax = other > amax ? other : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = d == 0.0f ? 0.0f : 1.0f / d;
+    const int q0 = (int8_t)(int)roundf(v0 * id);
+    const int q1 = (int8_t)(int)roundf(v1 * id);
+    const int q2 = (int8_t)(int)roundf(v2 * id);
+    const int q3 = (int8_t)(int)roundf(v3 * id);
+    Q8Quad out;
+    out.packed = (uint32_t)(q0 & 0xff) | (uint32_t)(q1 & 0xff) << 8 | (uint32_t)(q2 & 0xff) << 16 |
+                 (uint32_t)(q3 & 0xff) << 24;
+    int total = q0 + q1 + q2 + q3;
+#pragma unroll
+    for (int width = 1; width < 8; width <<= 1) total += __shfl_xor(total, width, 8);
+    out.total = total;
+    out.scale = round_to_half(d);
+    out.sum = round_to_half((float)total * d);
+    return out;
+}
+
+}  // namespace tmh

@@ -107,16 +107,34 @@ struct Attention {
     float* dst;
     uint32_t ld_dst;
     int32_t* errors;
+    Activations act;  // with qs set, the outputs are also quantised here (width a multiple of 32)
 };
 size_t attention_lds(uint32_t width, uint32_t capacity);
 hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream);
+// A decode step's attention with the RoPE and cache write of `r` fused: each
+// token is its cache row's one new position.
+hipError_t launch_attention_decode(const Attention& a, const RopeWrite& r, uint32_t tokens, hipStream_t stream);
+
+// RMSNorm then quantisation into `act`, one launch; for n a multiple of 32
+// up to the LDS limit.
+bool rmsnorm_quantise_fits(uint32_t n);
+hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
+                                   Activations act, hipStream_t stream);
+hipError_t launch_swiglu_quantise(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n,
+                                  Activations act, hipStream_t stream);
 
 hipError_t launch_swiglu(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n, float* dst,
                          hipStream_t stream);
 hipError_t launch_add(const float* a, const float* b, float* dst, uint32_t count, hipStream_t stream);
 hipError_t launch_argmax(const float* x, uint32_t ldx, uint32_t rows, uint32_t n, int32_t* ids, hipStream_t stream);
-hipError_t launch_advance(uint32_t rows, const int32_t* chosen, int32_t* log, uint32_t log_stride, int32_t* steps,
-                          int32_t* slots, int32_t* table, uint32_t capacity, hipStream_t stream);
+// The greedy choice of every row of a decode step and the move to the next
+// position: a split argmax over `logits` [rows, vocab] through values/index
+// (rows · argmax_chunks(vocab) entries each), then ids, the log and the
+// device-held slots and attention entries.
+uint32_t argmax_chunks(uint32_t n);
+hipError_t launch_choose_advance(const float* logits, uint32_t rows, uint32_t vocab, float* values, int32_t* index,
+                                 int32_t* ids, int32_t* log, uint32_t log_stride, int32_t* steps, int32_t* slots,
+                                 int32_t* table, uint32_t capacity, hipStream_t stream);
 
 // ------------------------------------------------- the runtime, for other sources
 

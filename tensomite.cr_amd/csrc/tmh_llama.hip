@@ -21,7 +21,6 @@ using tmh::DeviceContext;
 
 int code(hipError_t e) { return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : (int)e; }
 
-constexpr uint32_t ATTENTION_CAPACITY = 16000;
 
 int check_rope(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t table_rows, uint32_t capacity) {
     if (width == 0 || width % 2u != 0 || heads == 0 || kv_heads == 0 || capacity == 0) return TMH_ERROR_SHAPE;
@@ -31,7 +30,7 @@ int check_rope(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t table
 
 int check_attention(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t capacity) {
     if (width == 0 || width % 4u != 0 || heads == 0 || kv_heads == 0 || heads % kv_heads != 0) return TMH_ERROR_SHAPE;
-    if (capacity == 0 || capacity > ATTENTION_CAPACITY) return TMH_ERROR_SHAPE;
+    if (capacity == 0 || tmh::attention_lds(width, capacity) > 64u * 1024u) return TMH_ERROR_SHAPE;
     return TMH_SUCCESS;
 }
 
@@ -53,12 +52,15 @@ struct Llama {
 
     // device memory (one allocation), carved below
     uint8_t* memory = nullptr;
-    float *x = nullptr, *h = nullptr, *qkv_out = nullptr, *q = nullptr, *att = nullptr, *o_out = nullptr;
+    float* x[2] = {nullptr, nullptr};  // the residual stream, ping-ponged by one-row residual products
+    float *h = nullptr, *qkv_out = nullptr, *q = nullptr, *att = nullptr, *o_out = nullptr;
     float *gu = nullptr, *act = nullptr, *logits = nullptr;
     float *cos = nullptr, *sin = nullptr;
     float *keys = nullptr, *values = nullptr;  // [layers][rows][kv_heads][capacity][head_width]
     int32_t *ids = nullptr, *slots = nullptr, *table = nullptr, *steps = nullptr, *log = nullptr;
-    uint8_t* scratch = nullptr;
+    float* best_values = nullptr;  // the split argmax's chunks
+    int32_t* best_index = nullptr;
+    uint8_t* scratch[2] = {nullptr, nullptr};  // quantised activations: a product's input, and the next one's
     size_t layer_cache = 0;  // floats of one layer's keys
 
     std::vector<int32_t> length;   // positions held, per row
@@ -68,79 +70,105 @@ struct Llama {
     hipGraphExec_t graph = nullptr;
 };
 
-// One product x[rows, k] · wᵀ (+ addend) into dst: the fused one-row kernel
-// for a single row, else the quantise pass into the decoder's scratch and
-// the product kernel. With `addend` == dst the product adds itself into dst
-// (one row only: the bias is per output, shared by rows).
-hipError_t product(const Llama& m, const DeviceContext& ctx, const uint8_t* w, const float* xin, uint32_t rows,
-                   uint32_t n, uint32_t k, float* dst, const float* addend) {
-    if (rows == 1 && tmh::row_kernel_fits(TMH_MODE_AUTO, w, k))
-        return tmh::launch_row(m.c.kind, w, xin, dst, addend, n, k, ctx.compute_units, ctx.stream);
-    tmh::Activations a = tmh::carve_scratch(m.scratch, rows, k);
-    hipError_t e = tmh::launch_quantize(xin, k, rows, k, (float*)a.scales, (float*)a.sums, (int32_t*)a.totals,
-                                        (int8_t*)a.qs, ctx.stream);
-    if (e != hipSuccess) return e;
-    return tmh::launch_block_matmul(m.c.kind, TMH_MODE_AUTO, w, a, dst, addend, rows, n, k, ctx.compute_units,
+// dst[rows, n] = act · wᵀ (+ bias) over quantised activations.
+hipError_t product(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
+                   uint32_t n, uint32_t k, float* dst, const float* bias) {
+    return tmh::launch_block_matmul(m.c.kind, TMH_MODE_AUTO, w, act, dst, bias, rows, n, k, ctx.compute_units,
                                     ctx.stream);
 }
 
-// Residual: x[rows] += x_in · wᵀ, as the host's `x + product` (one rounding
-// per element either way round).
-hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, const float* xin, uint32_t rows,
-                    uint32_t n, uint32_t k) {
-    if (rows == 1) return product(m, ctx, w, xin, 1, n, k, m.x, m.x);
-    hipError_t e = product(m, ctx, w, xin, rows, n, k, m.o_out, nullptr);
-    if (e != hipSuccess) return e;
-    return tmh::launch_add(m.x, m.o_out, m.x, rows * n, ctx.stream);
+// Quantises rows of f32 activations into act.
+hipError_t quantise(const DeviceContext& ctx, const float* x, uint32_t rows, uint32_t k, tmh::Activations act) {
+    return tmh::launch_quantize(x, k, rows, k, (float*)act.scales, (float*)act.sums, (int32_t*)act.totals,
+                                (int8_t*)act.qs, ctx.stream);
+}
+
+// RMSNorm of x's rows, quantised into act: one launch where the row fits.
+hipError_t norm_quantise(const Llama& m, const DeviceContext& ctx, const float* x, const float* w, uint32_t rows,
+                         tmh::Activations act) {
+    const uint32_t W = (uint32_t)m.c.width;
+    if (tmh::rmsnorm_quantise_fits(W)) return tmh::launch_rmsnorm_quantise(x, W, w, rows, W, m.c.eps, act, ctx.stream);
+    hipError_t e = tmh::launch_rmsnorm(x, W, w, rows, W, m.c.eps, m.h, W, ctx.stream);
+    return e == hipSuccess ? quantise(ctx, m.h, rows, W, act) : e;
+}
+
+// The residual update x += act · wᵀ, as the host's `x + product` (one
+// rounding per element either way round): for one row the product adds x
+// as its bias and writes the other residual buffer; for more rows it is a
+// product and an add.
+hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
+                    uint32_t k, int& cur) {
+    const uint32_t W = (uint32_t)m.c.width;
+    if (rows == 1) {
+        hipError_t e = product(m, ctx, w, act, 1, W, k, m.x[cur ^ 1], m.x[cur]);
+        cur ^= 1;
+        return e;
+    }
+    hipError_t e = product(m, ctx, w, act, rows, W, k, m.o_out, nullptr);
+    return e == hipSuccess ? tmh::launch_add(m.x[cur], m.o_out, m.x[cur], rows * W, ctx.stream) : e;
 }
 
 // The forward of `tokens` ids already on the device (m.ids), whose slots
 // and attention entries are on the device too; then the final norm and the
-// head over `final_rows` rows from x row `final_from`, into logits rows from
-// `logits_row`.
+// head over `final_rows` rows from row `final_from`, into logits rows from
+// `logits_row`. With `decode`, token t is cache row t's one new position, and
+// its RoPE and cache write run inside the attention launch.
 hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tokens, uint32_t final_from,
-                          uint32_t final_rows, uint32_t logits_row) {
+                          uint32_t final_rows, uint32_t logits_row, bool decode) {
     const tmh_llama_config& c = m.c;
     const uint32_t W = (uint32_t)c.width, H = (uint32_t)c.hidden, hw = (uint32_t)c.head_width;
-    hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x, ctx.errors, ctx.stream);
     const float scale = (float)(1.0 / std::sqrt((double)hw));
+    const bool quant_att = hw % 32u == 0;
+    int cur = 0;
+    hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x[cur], ctx.errors, ctx.stream);
+    const tmh::Activations a_in = tmh::carve_scratch(m.scratch[0], tokens, W);
     for (int32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
         float* keys = m.keys + (size_t)l * m.layer_cache;
         float* values = m.values + (size_t)l * m.layer_cache;
-        e = tmh::launch_rmsnorm(m.x, W, m.attn_norm[l], tokens, W, c.eps, m.h, W, ctx.stream);
-        if (e == hipSuccess) e = product(m, ctx, m.qkv[l], m.h, tokens, m.nqkv, W, m.qkv_out, nullptr);
+        e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in);
+        if (e == hipSuccess) e = product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out, nullptr);
+        const tmh::Activations a_att = tmh::carve_scratch(m.scratch[1], tokens, m.qn);
+        tmh::RopeWrite r{m.qkv_out, m.nqkv, (uint32_t)c.heads, (uint32_t)c.kv_heads, hw, m.cos, m.sin,
+                         m.slots, m.rows, m.capacity, m.q, keys, values, ctx.errors};
+        tmh::Attention a{m.q, m.qn, keys, values, m.rows, (uint32_t)c.kv_heads, m.capacity, hw,
+                         (uint32_t)c.heads, m.table, scale, m.att, m.qn, ctx.errors,
+                         quant_att ? a_att : tmh::Activations{}};
         if (e == hipSuccess) {
-            tmh::RopeWrite r{m.qkv_out, m.nqkv, (uint32_t)c.heads, (uint32_t)c.kv_heads, hw, m.cos, m.sin,
-                             m.slots, m.rows, m.capacity, m.q, keys, values, ctx.errors};
-            e = tmh::launch_rope_write(r, tokens, ctx.stream);
+            if (decode) {
+                e = tmh::launch_attention_decode(a, r, tokens, ctx.stream);
+            } else {
+                e = tmh::launch_rope_write(r, tokens, ctx.stream);
+                if (e == hipSuccess) e = tmh::launch_attention(a, tokens, ctx.stream);
+            }
         }
-        if (e == hipSuccess) {
-            tmh::Attention a{m.q, m.qn, keys, values, m.rows, (uint32_t)c.kv_heads, m.capacity, hw,
-                             (uint32_t)c.heads, m.table, scale, m.att, m.qn, ctx.errors};
-            e = tmh::launch_attention(a, tokens, ctx.stream);
-        }
-        if (e == hipSuccess) e = residual(m, ctx, m.o[l], m.att, tokens, W, m.qn);
-        if (e == hipSuccess) e = tmh::launch_rmsnorm(m.x, W, m.ffn_norm[l], tokens, W, c.eps, m.h, W, ctx.stream);
-        if (e == hipSuccess) e = product(m, ctx, m.gate_up[l], m.h, tokens, 2u * H, W, m.gu, nullptr);
-        if (e == hipSuccess) e = tmh::launch_swiglu(m.gu, m.gu + H, 2u * H, tokens, H, m.act, ctx.stream);
-        if (e == hipSuccess) e = residual(m, ctx, m.down[l], m.act, tokens, W, H);
+        if (e == hipSuccess && !quant_att) e = quantise(ctx, m.att, tokens, m.qn, a_att);
+        if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur);
+        if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in);
+        if (e == hipSuccess) e = product(m, ctx, m.gate_up[l], a_in, tokens, 2u * H, W, m.gu, nullptr);
+        const tmh::Activations a_hid = tmh::carve_scratch(m.scratch[1], tokens, H);
+        if (e == hipSuccess) e = tmh::launch_swiglu_quantise(m.gu, m.gu + H, 2u * H, tokens, H, a_hid, ctx.stream);
+        if (e == hipSuccess) e = residual(m, ctx, m.down[l], a_hid, tokens, H, cur);
     }
+    const tmh::Activations a_fin = tmh::carve_scratch(m.scratch[0], final_rows, W);
+    if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur] + (size_t)final_from * W, m.norm, final_rows, a_fin);
     if (e == hipSuccess)
-        e = tmh::launch_rmsnorm(m.x + (size_t)final_from * W, W, m.norm, final_rows, W, c.eps, m.h, W, ctx.stream);
-    if (e == hipSuccess)
-        e = product(m, ctx, m.head, m.h, final_rows, (uint32_t)c.vocab, W, m.logits + (size_t)logits_row * c.vocab,
+        e = product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, m.logits + (size_t)logits_row * c.vocab,
                     nullptr);
     return e;
+}
+
+// Chooses each row's next token from logits rows 0..rows-1, logs it and
+// moves the row on.
+hipError_t choose(const Llama& m, const DeviceContext& ctx) {
+    return tmh::launch_choose_advance(m.logits, m.rows, (uint32_t)m.c.vocab, m.best_values, m.best_index, m.ids, m.log,
+                                      m.capacity, m.steps, m.slots, m.table, m.capacity, ctx.stream);
 }
 
 // One decode step of every row from the device-held state: run each row's
 // chosen id, choose the next, log it and move the row on.
 hipError_t decode_step(const Llama& m, const DeviceContext& ctx) {
-    hipError_t e = forward_tokens(m, ctx, m.rows, 0, m.rows, 0);
-    if (e == hipSuccess) e = tmh::launch_argmax(m.logits, (uint32_t)m.c.vocab, m.rows, (uint32_t)m.c.vocab, m.ids, ctx.stream);
-    if (e == hipSuccess)
-        e = tmh::launch_advance(m.rows, m.ids, m.log, m.capacity, m.steps, m.slots, m.table, m.capacity, ctx.stream);
-    return e;
+    hipError_t e = forward_tokens(m, ctx, m.rows, 0, m.rows, 0, true);
+    return e == hipSuccess ? choose(m, ctx) : e;
 }
 
 int run_step(Llama& m, const DeviceContext& ctx, bool graph) {
@@ -297,7 +325,7 @@ int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* we
     if ((err = check_rope(c.heads, c.kv_heads, c.head_width, capacity, capacity)) != TMH_SUCCESS) return err;
     if ((err = check_attention(c.heads, c.kv_heads, c.head_width, capacity)) != TMH_SUCCESS) return err;
     if (!weights->embed || !weights->norm || !weights->attn_norm || !weights->ffn_norm || !weights->qkv ||
-        !weights->o || !weights->gate_up || !weights->down)
+        !weights->o || !weights->gate_up || !weights->down || weights->norm % 16u != 0)
         return TMH_ERROR_INVALID_VALUE;
 
     Llama* m = new Llama();
@@ -315,7 +343,8 @@ int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* we
     m->norm = (const float*)weights->norm;
     for (int32_t l = 0; l < c.layers; ++l) {
         if (!weights->attn_norm[l] || !weights->ffn_norm[l] || !weights->qkv[l] || !weights->o[l] ||
-            !weights->gate_up[l] || !weights->down[l]) {
+            !weights->gate_up[l] || !weights->down[l] || weights->attn_norm[l] % 16u != 0 ||
+            weights->ffn_norm[l] % 16u != 0) {
             delete m;
             return TMH_ERROR_INVALID_VALUE;
         }
@@ -338,7 +367,8 @@ int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* we
         void** at;
         size_t bytes;
     } parts[] = {
-        {(void**)&m->x, R * W * 4},
+        {(void**)&m->x[0], R * W * 4},
+        {(void**)&m->x[1], R * W * 4},
         {(void**)&m->h, R * W * 4},
         {(void**)&m->qkv_out, R * m->nqkv * 4},
         {(void**)&m->q, R * m->qn * 4},
@@ -354,7 +384,10 @@ int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* we
         {(void**)&m->table, R * 3 * 4},
         {(void**)&m->steps, (size_t)rows * 4},
         {(void**)&m->log, (size_t)rows * capacity * 4},
-        {(void**)&m->scratch, tmh::scratch_need((uint32_t)R, widest)},
+        {(void**)&m->scratch[0], tmh::scratch_need((uint32_t)R, widest)},
+        {(void**)&m->scratch[1], tmh::scratch_need((uint32_t)R, widest)},
+        {(void**)&m->best_values, R * tmh::argmax_chunks((uint32_t)c.vocab) * 4},
+        {(void**)&m->best_index, R * tmh::argmax_chunks((uint32_t)c.vocab) * 4},
         {(void**)&m->keys, m->layer_cache * c.layers * 4},
         {(void**)&m->values, m->layer_cache * c.layers * 4},
     };
@@ -429,7 +462,8 @@ int tmh_llama_forward(uint64_t model, uint32_t row, const int32_t* ids, uint32_t
     // A last-only forward leaves its logits in the row's logits row, where
     // generation starts from.
     const uint32_t logits_row = last_only ? row : 0u;
-    if (e == hipSuccess) e = forward_tokens(*m, ctx, count, last_only ? count - 1u : 0u, final_rows, logits_row);
+    if (e == hipSuccess)
+        e = forward_tokens(*m, ctx, count, last_only ? count - 1u : 0u, final_rows, logits_row, false);
     if (e != hipSuccess) return code(e);
     tmh::note_launch(ctx.index, 0, true);
     m->length[row] = past + (int32_t)count;
@@ -483,11 +517,7 @@ int tmh_llama_generate(uint64_t model, uint32_t steps, int32_t* tokens, uint32_t
     if (e == hipSuccess)
         e = hipMemcpyAsync(m->steps, host.data() + 4 * m->rows, (size_t)m->rows * 4, hipMemcpyHostToDevice, ctx.stream);
     // the first token of each row from its last forward's logits
-    if (e == hipSuccess)
-        e = tmh::launch_argmax(m->logits, (uint32_t)m->c.vocab, m->rows, (uint32_t)m->c.vocab, m->ids, ctx.stream);
-    if (e == hipSuccess)
-        e = tmh::launch_advance(m->rows, m->ids, m->log, m->capacity, m->steps, m->slots, m->table, m->capacity,
-                                ctx.stream);
+    if (e == hipSuccess) e = choose(*m, ctx);
     if (e != hipSuccess) return code(e);
     tmh::note_launch(ctx.index, 0, true);
     for (uint32_t i = 1; i < steps; ++i) {
