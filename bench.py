@@ -16,7 +16,12 @@ The CPU baseline times the oracle's restatement of tensomite's CPU path
 (Quant.matmul, all host cores) on the same bytes, and checks the GPU's
 output bits against it.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu]
+A second object, decode_1p7b, reports config 5: greedy decode tokens/s of a
+SmolLM2-1.7B-shaped Q4_0 Llama at batch 1 and 8 through the device-resident
+decoder (every op on the GPU with the host's bits), and the CPU oracle's
+time per token beside it.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 """
 from __future__ import annotations
 
@@ -118,6 +123,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
+    ap.add_argument("--decode-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
@@ -257,7 +264,81 @@ def main():
         result["cpu_baseline"] = cpu_baseline(weights, xs, prods, gpu_out, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
+    for buf in wbufs:
+        buf.release()
+    dev.sync()
+    if not args.no_decode:
+        log("decode at the 1.7B shape ...")
+        result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu)
     print(json.dumps(result), flush=True)
+
+
+def decode_1p7b(dev, steps, cpu_seconds, with_cpu):
+    """Config 5: greedy decode of a SmolLM2-1.7B-shaped Q4_0 Llama (random
+    block weights, tied head) through the device-resident decoder, after a
+    128-token prompt, at batch 1 and batch 8 (f32 KV capacity 2048). A step is
+    one token per row, replayed from a captured HIP graph; timed with HIP
+    events on the library's stream. The CPU figure is the oracle's forward
+    (the restatement of tensomite's host path) per decoded token after a
+    short prompt, on a bounded sample."""
+    import quant_host
+    import tensomite_hip as th
+
+    config = dict(quant_host.SMOLLM2_1P7B)
+    t0 = time.perf_counter()
+    weights = quant_host.random_block_llama(config, seed=0x5EED0005)
+    log(f"1.7B weights in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(0x5EED0005)
+    out = {"model": "SmolLM2-1.7B shape, Q4_0, tied head (random block weights)", "prompt": 128,
+           "capacity": 2048}
+    weight_bytes = sum(w.nbytes for key in ("qkv", "o", "gate_up", "down") for w in weights[key]) + \
+        weights["embed"].nbytes
+    out["weight_bytes_per_token"] = weight_bytes
+    for rows in (1, 8):
+        model = th.HIPLlama(dev, config, weights, rows=rows, capacity=2048, max_tokens=128)
+        prefill = []
+        for r in range(rows):
+            prompt = list(rng.integers(0, config["vocab"], 128))
+            t = time.perf_counter()
+            model.forward(prompt, row=r, last_only=True)
+            prefill.append(time.perf_counter() - t)
+        model.generate(4, graph=True)  # graph captured, state on the device
+        for _ in range(4):
+            model.step(graph=True)
+        dev.sync()
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        for _ in range(steps):
+            model.step(graph=True)
+        dev.record(e1)
+        ms = dev.elapsed_ms(e0, e1) / steps
+        dev.sync()
+        out[f"batch{rows}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(rows * 1e3 / ms, 1),
+                               "steps": steps, "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
+                               "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
+        model.destroy()
+        log(f"decode batch {rows}: {ms * 1e3:.0f} us/step")
+    if with_cpu:
+        from oracle import oracle
+        try:
+            cores = len(os.sched_getaffinity(0))
+        except AttributeError:
+            cores = os.cpu_count() or 1
+        cores = max(1, min(cores, 16))
+        variant = oracle.best_variant()
+        oracle.set_threads(cores, variant)
+        cpu = oracle.Llama(config, weights, variant)
+        cpu.forward(list(rng.integers(0, config["vocab"], 8)), last_only=True)
+        tokens, start = 0, time.perf_counter()
+        token = 0
+        while time.perf_counter() - start < cpu_seconds and tokens < 64:
+            token = oracle.argmax(cpu.forward([token], last_only=True)[0])
+            tokens += 1
+        elapsed = time.perf_counter() - start
+        out["cpu_baseline"] = {"ms_per_token": round(elapsed / tokens * 1e3, 1), "cores": cores, "kind": "port",
+                               "sample": f"{tokens} greedy tokens after an 8-token prompt, batch 1; the oracle's "
+                                         f"Llama forward ({variant} build, {cores} threads)"}
+    return out
 
 
 class _View:

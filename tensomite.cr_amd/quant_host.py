@@ -106,3 +106,60 @@ def synthetic_weights(kind, n: int, k: int, seed: int, std: float = 0.02, chunk_
         rows = min(chunk_rows, n - r0)
         parts.append(quantize(kind, rng.normal(0.0, std, rows * k).astype(np.float32)))
     return np.concatenate(parts)
+
+
+def random_blocks(fmt: str, n: int, k: int, rng, std: float = 0.02) -> np.ndarray:
+    """[n, k] weights as random block bytes: uniform quants with F16 scales
+    (and Q4_1 minimums) drawn so the values have about `std` spread. Valid
+    blocks of the format, made without a float pass, for model-sized tests."""
+    bb = {"Q8_0": 34, "Q4_0": 18, "Q4_1": 20}[fmt]
+    blocks = n * k // 32
+    data = np.frombuffer(rng.bytes(blocks * bb), np.uint8).copy().reshape(blocks, bb)
+    # centre the quants (no shared offset in every dot product)
+    if fmt == "Q8_0":
+        q = data[:, 2:]
+        q[q == 0x80] = 0
+    elif fmt == "Q4_0":
+        q = data[:, 2:]
+        lo, hi = q & 15, q >> 4
+        q[...] = np.where(lo == 0, 8, lo) | (np.where(hi == 0, 8, hi) << 4)
+    spread = {"Q8_0": 73.9, "Q4_0": 4.6, "Q4_1": 4.6}[fmt]
+    d = (rng.uniform(0.5, 1.5, blocks) * std / spread).astype(np.float16)
+    data[:, 0:2] = d.view(np.uint8).reshape(blocks, 2)
+    if fmt == "Q4_1":
+        m = (-7.5 * d.astype(np.float32)).astype(np.float16)
+        data[:, 2:4] = m.view(np.uint8).reshape(blocks, 2)
+    return data.reshape(-1)
+
+
+def random_block_llama(config: dict, seed: int, norm_jitter: float = 0.05, std: float = 0.05,
+                       embed_std: float = 0.02):
+    """A Llama of `config`'s shape (tied head) with random_blocks matrices and
+    jittered RMSNorm weights, as a dict of the decoder's weight layout (embed,
+    head None, norm, per-layer attn_norm, ffn_norm, merged qkv, o, merged
+    gate_up, down); quick to make at the 1.7B shape.
+    The default spreads make layers matter against the embedding, so greedy
+    tokens vary from step to step."""
+    c = config
+    fmt = c["kind"]
+    rng = np.random.default_rng(seed)
+    qn, kvn = c["heads"] * c["head_width"], c["kv_heads"] * c["head_width"]
+
+    def norm():
+        return (1.0 + rng.normal(0, norm_jitter, c["width"])).astype(np.float32)
+
+    w = dict(embed=random_blocks(fmt, c["vocab"], c["width"], rng, std=embed_std), head=None, norm=norm(),
+             attn_norm=[], ffn_norm=[], qkv=[], o=[], gate_up=[], down=[])
+    for _ in range(c["layers"]):
+        w["qkv"].append(random_blocks(fmt, qn + 2 * kvn, c["width"], rng, std))
+        w["o"].append(random_blocks(fmt, c["width"], qn, rng, std))
+        w["gate_up"].append(random_blocks(fmt, 2 * c["hidden"], c["width"], rng, std))
+        w["down"].append(random_blocks(fmt, c["width"], c["hidden"], rng, std))
+        w["attn_norm"].append(norm())
+        w["ffn_norm"].append(norm())
+    return w
+
+
+# SmolLM2-1.7B's shape (Llama, tied head), in the decoder's config keys.
+SMOLLM2_1P7B = dict(layers=24, width=2048, heads=32, kv_heads=32, head_width=64, hidden=8192, vocab=49152,
+                    context=2048, eps=1e-5, theta=10000.0, kind="Q4_0")
