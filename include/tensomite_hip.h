@@ -389,6 +389,44 @@ int tmh_llama_step(uint64_t model, uint32_t graph);
 
 int tmh_llama_destroy(uint64_t model);
 
+/* ------------------------------------------------------------ GGUF files
+ *
+ * The reference's GGUF reader (gguf.cr) for this device: the file is mapped
+ * once; a tensor's bytes reach the device through the pinned staging ring
+ * (tmh_upload_async), optionally as a list of its rows in any order, so a row
+ * reorder (Tensor#take_rows, tensor/quantised.cr:32-43, as Llama.unpermute
+ * uses it) or a join of several tensors into one buffer (Linear.merge's
+ * cat_rows, modules.cr:36-56) happens on the host before the upload, not as
+ * a download and re-upload (quantised.cr:45-55). */
+
+/* Maps and parses a GGUF file of version 2 or 3 (gguf.cr:289-329). Unknown
+ * tensor kinds are TMH_ERROR_DTYPE; a damaged file TMH_ERROR_INVALID_VALUE. */
+int tmh_gguf_open(const char* path, uint64_t* file);
+int tmh_gguf_close(uint64_t file);
+
+/* A tensor's kind (ggml numbering: F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8,
+ * BF16 30), shape outermost first (up to 4 dimensions) and byte size: the
+ * file's Entry (gguf.cr:85-98). Any output pointer may be null. */
+int tmh_gguf_tensor(uint64_t file, const char* name, uint32_t* kind, int64_t* shape, uint32_t* dims,
+                    uint64_t* bytes);
+
+/* Queues the upload of tensor `name` to device address dst, as stored (rows
+ * null) or as its rows rows[0..count) in that order (GGUF#[], gguf.cr:112-136,
+ * then take_rows). Returns once the bytes are in the staging ring. */
+int tmh_gguf_upload(uint64_t file, const char* name, const int32_t* rows, uint32_t count, uint64_t dst);
+
+/* Llama.load of a GGUF file onto the device (llama.cr:184-235): the config
+ * from its llama.* metadata (Llama.config, llama.cr:57-77), then every
+ * weight uploaded once, the q and k rows put back in Hugging Face order
+ * (Llama.unpermute) and the projections joined (qkv, gate_up) on the way;
+ * a decoder as tmh_llama_create makes, owning the weights. Every matrix and
+ * the embedding table must share one block kind (the file's token_embd);
+ * norms may be F32, F16 or BF16 (widened, as GGUF#[] widens them). A file
+ * with tensors the model lacks is refused, as the reference refuses it.
+ * `capacity` 0 means the model's context. Writes the config it read. */
+int tmh_llama_load_gguf(const char* path, uint32_t rows, uint32_t capacity, uint32_t max_tokens,
+                        tmh_llama_config* config, uint64_t* model);
+
 #ifdef __cplusplus
 }
 #endif

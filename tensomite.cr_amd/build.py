@@ -17,7 +17,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libtensomite_hip.so")
-SOURCES = [os.path.join(HERE, "csrc", name) for name in ("tmh_runtime.hip", "tmh_kernels.hip", "tmh_decode.hip", "tmh_llama.hip")]
+SOURCES = [os.path.join(HERE, "csrc", name) for name in ("tmh_runtime.hip", "tmh_kernels.hip", "tmh_decode.hip", "tmh_llama.hip", "tmh_gguf.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

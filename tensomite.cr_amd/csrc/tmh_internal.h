@@ -8,6 +8,10 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+#include <unordered_map>
+#include <vector>
+
 namespace tmh {
 
 // Bytes of one block of 32 values, by kind (dtype.cr:237-244).
@@ -155,5 +159,44 @@ hipError_t device_malloc(void** p, size_t bytes);
 // Bytes the quantise pass writes for `rows` rows of k, and its carving.
 size_t scratch_need(uint32_t rows, uint32_t k);
 Activations carve_scratch(uint8_t* base, uint32_t rows, uint32_t k);
+
+// ------------------------------------------------- GGUF files (tmh_gguf.hip)
+
+// Tensor kinds by ggml's numbering (gguf.cr:29-36).
+constexpr uint32_t GGUF_F32 = 0, GGUF_F16 = 1, GGUF_Q4_0 = 2, GGUF_Q4_1 = 3, GGUF_Q8_0 = 8, GGUF_BF16 = 30;
+
+struct GgufValue {
+    uint32_t type = 0;  // GGUF value type
+    int64_t i = 0;      // integers and bools
+    double f = 0.0;     // float32 (widened) and float64
+    std::string s;      // strings
+};
+
+struct GgufTensor {
+    std::string name;
+    uint32_t kind;
+    std::vector<int64_t> shape;  // outermost first
+    uint64_t offset, bytes;      // within the file
+};
+
+// A GGUF file, memory-mapped and parsed (metadata scalars and the tensor
+// directory); tensors are read from the mapping on demand.
+struct Gguf {
+    std::string path;
+    const uint8_t* map = nullptr;
+    size_t size = 0;
+    std::unordered_map<std::string, GgufValue> metadata;
+    std::vector<GgufTensor> tensors;
+    std::unordered_map<std::string, int> index;
+
+    ~Gguf();
+    int open(const char* file);  // a TMH_* code
+    const GgufTensor* find(const std::string& name) const;
+    const GgufValue* value(const std::string& key) const;
+};
+
+uint64_t gguf_bytes_for(uint32_t kind, int64_t count);
+// Rows rows[0..count) of t (every row, in order, when rows is null) into out.
+bool gguf_rows(const Gguf& g, const GgufTensor& t, const int32_t* rows, uint32_t count, std::vector<uint8_t>& out);
 
 }  // namespace tmh

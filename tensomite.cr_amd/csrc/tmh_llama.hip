@@ -68,6 +68,7 @@ struct Llama {
     bool generating = false;       // the device state continues a generation
 
     hipGraphExec_t graph = nullptr;
+    void* owned = nullptr;  // weights this decoder loaded itself (tmh_llama_load_gguf)
 };
 
 // dst[rows, n] = act · wᵀ (+ bias) over quantised activations.
@@ -581,7 +582,251 @@ int tmh_llama_destroy(uint64_t model) {
     if (tmh::device_context(&ctx, false) == TMH_SUCCESS) (void)hipStreamSynchronize(ctx.stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     if (m->memory) (void)hipFree(m->memory);
+    if (m->owned) (void)hipFree(m->owned);
     delete m;
+    return TMH_SUCCESS;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------- GGUF loading
+
+namespace {
+
+// Llama.unpermute's row order for block weights (llama.cr:226-235): each
+// head's rows from llama.cpp's rotary pairing (2i, 2i+1) to (i, i + half).
+std::vector<int32_t> unpermute_order(int32_t heads, int32_t head_width) {
+    const int32_t half = head_width / 2;
+    std::vector<int32_t> order;
+    order.reserve((size_t)heads * head_width);
+    for (int32_t h = 0; h < heads; ++h)
+        for (int32_t pair = 0; pair < 2; ++pair)
+            for (int32_t i = 0; i < half; ++i) order.push_back(h * 2 * half + 2 * i + pair);
+    return order;
+}
+
+bool meta_int(const tmh::Gguf& g, const std::string& key, int64_t* out) {
+    const tmh::GgufValue* v = g.value(key);
+    if (!v || !(v->type <= 5 || v->type == 10 || v->type == 11)) return false;
+    *out = v->i;
+    return true;
+}
+
+bool meta_float(const tmh::Gguf& g, const std::string& key, double* out) {
+    const tmh::GgufValue* v = g.value(key);
+    if (!v) return false;
+    if (v->type == 6 || v->type == 12) *out = v->f;
+    else if (v->type <= 5 || v->type == 10 || v->type == 11) *out = (double)v->i;
+    else return false;
+    return true;
+}
+
+// Llama.config (llama.cr:57-77) from the llama.* metadata.
+int gguf_config(const tmh::Gguf& g, tmh_llama_config* c) {
+    const tmh::GgufValue* arch = g.value("general.architecture");
+    if (!arch || arch->type != 8 || arch->s != "llama") return TMH_ERROR_INVALID_VALUE;
+    const tmh::GgufValue* scaling = g.value("llama.rope.scaling.type");
+    if (scaling && !(scaling->type == 8 && scaling->s == "none")) return TMH_ERROR_INVALID_VALUE;
+    int64_t layers, width, heads, hidden, context, kv, hw, vocab;
+    double eps, theta = 10000.0;
+    if (!meta_int(g, "llama.block_count", &layers) || !meta_int(g, "llama.embedding_length", &width) ||
+        !meta_int(g, "llama.attention.head_count", &heads) || !meta_int(g, "llama.feed_forward_length", &hidden) ||
+        !meta_int(g, "llama.context_length", &context) ||
+        !meta_float(g, "llama.attention.layer_norm_rms_epsilon", &eps))
+        return TMH_ERROR_INVALID_VALUE;
+    if (heads <= 0 || width <= 0) return TMH_ERROR_SHAPE;
+    if (!meta_int(g, "llama.attention.head_count_kv", &kv)) kv = heads;
+    if (!meta_int(g, "llama.rope.dimension_count", &hw)) hw = width / heads;
+    if (!meta_int(g, "llama.vocab_size", &vocab)) {
+        const tmh::GgufTensor* e = g.find("token_embd.weight");
+        if (!e || e->shape.size() != 2) return TMH_ERROR_INVALID_VALUE;
+        vocab = e->shape[0];
+    }
+    (void)meta_float(g, "llama.rope.freq_base", &theta);
+    const tmh::GgufTensor* e = g.find("token_embd.weight");
+    if (!e) return TMH_ERROR_INVALID_VALUE;
+    uint32_t kind;
+    switch (e->kind) {
+    case tmh::GGUF_Q8_0: kind = TMH_Q8_0; break;
+    case tmh::GGUF_Q4_0: kind = TMH_Q4_0; break;
+    case tmh::GGUF_Q4_1: kind = TMH_Q4_1; break;
+    default: return TMH_ERROR_DTYPE;
+    }
+    const int64_t limit = 1ll << 30;
+    if (layers <= 0 || layers > 4096 || heads > limit || kv <= 0 || hw <= 0 || hidden <= 0 || vocab <= 0 ||
+        context <= 0 || width > limit || hidden > limit || vocab > limit || context > limit)
+        return TMH_ERROR_SHAPE;
+    c->layers = (int32_t)layers;
+    c->width = (int32_t)width;
+    c->heads = (int32_t)heads;
+    c->kv_heads = (int32_t)kv;
+    c->head_width = (int32_t)hw;
+    c->hidden = (int32_t)hidden;
+    c->vocab = (int32_t)vocab;
+    c->context = (int32_t)context;
+    c->eps = (float)eps;
+    c->theta = theta;
+    c->kind = kind;
+    return TMH_SUCCESS;
+}
+
+// Widens an F16 or BF16 tensor to F32 on the host, as GGUF#[] does.
+bool widen(const tmh::Gguf& g, const tmh::GgufTensor& t, std::vector<float>& out) {
+    const int64_t count = (int64_t)(t.kind == tmh::GGUF_F32 ? t.bytes / 4 : t.bytes / 2);
+    out.resize((size_t)count);
+    const uint8_t* p = g.map + t.offset;
+    for (int64_t i = 0; i < count; ++i) {
+        if (t.kind == tmh::GGUF_F32) {
+            std::memcpy(&out[i], p + 4 * i, 4);
+        } else {
+            uint16_t h;
+            std::memcpy(&h, p + 2 * i, 2);
+            if (t.kind == tmh::GGUF_BF16) {
+                const uint32_t bits = (uint32_t)h << 16;
+                std::memcpy(&out[i], &bits, 4);
+            } else {
+                _Float16 f;
+                std::memcpy(&f, &h, 2);
+                out[i] = (float)f;
+            }
+        }
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmh_llama_load_gguf(const char* path, uint32_t rows, uint32_t capacity, uint32_t max_tokens,
+                        tmh_llama_config* config, uint64_t* model) {
+    if (!path || !model) return TMH_ERROR_INVALID_VALUE;
+    *model = 0;
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, true);
+    if (err) return err;
+    tmh::Gguf g;
+    if ((err = g.open(path)) != TMH_SUCCESS) return err;
+    tmh_llama_config c{};
+    if ((err = gguf_config(g, &c)) != TMH_SUCCESS) return err;
+    const uint32_t gkind = c.kind == TMH_Q8_0 ? tmh::GGUF_Q8_0 : c.kind == TMH_Q4_0 ? tmh::GGUF_Q4_0 : tmh::GGUF_Q4_1;
+    const int64_t W = c.width, H = c.hidden, qn = (int64_t)c.heads * c.head_width, kvn = (int64_t)c.kv_heads * c.head_width;
+
+    // The tensors the model has, by GGUF name, with their shapes; a block
+    // matrix or an F32-like vector each.
+    struct Want {
+        std::string name;
+        std::vector<int64_t> shape;
+        bool matrix;
+    };
+    std::vector<Want> wants = {{"token_embd.weight", {c.vocab, W}, true}, {"output_norm.weight", {W}, false}};
+    const bool tied = g.find("output.weight") == nullptr;
+    if (!tied) wants.push_back({"output.weight", {c.vocab, W}, true});
+    for (int32_t l = 0; l < c.layers; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        wants.push_back({b + "attn_norm.weight", {W}, false});
+        wants.push_back({b + "attn_q.weight", {qn, W}, true});
+        wants.push_back({b + "attn_k.weight", {kvn, W}, true});
+        wants.push_back({b + "attn_v.weight", {kvn, W}, true});
+        wants.push_back({b + "attn_output.weight", {W, qn}, true});
+        wants.push_back({b + "ffn_norm.weight", {W}, false});
+        wants.push_back({b + "ffn_gate.weight", {H, W}, true});
+        wants.push_back({b + "ffn_up.weight", {H, W}, true});
+        wants.push_back({b + "ffn_down.weight", {W, H}, true});
+    }
+    for (const Want& w : wants) {
+        const tmh::GgufTensor* t = g.find(w.name);
+        if (!t) return TMH_ERROR_INVALID_VALUE;
+        if (t->shape != w.shape) return TMH_ERROR_SHAPE;
+        if (w.matrix ? t->kind != gkind
+                     : !(t->kind == tmh::GGUF_F32 || t->kind == tmh::GGUF_F16 || t->kind == tmh::GGUF_BF16))
+            return TMH_ERROR_DTYPE;
+    }
+    if (wants.size() != g.tensors.size()) return TMH_ERROR_INVALID_VALUE;  // tensors the model lacks
+
+    // One device allocation for every weight, carved 256-byte aligned.
+    const uint64_t row = tmh::gguf_bytes_for(gkind, W);
+    const uint64_t embed_bytes = (uint64_t)c.vocab * row;
+    const uint64_t qkv_bytes = (uint64_t)(qn + 2 * kvn) * row, o_bytes = (uint64_t)W * tmh::gguf_bytes_for(gkind, qn);
+    const uint64_t gu_bytes = (uint64_t)(2 * H) * row, down_bytes = (uint64_t)W * tmh::gguf_bytes_for(gkind, H);
+    const uint64_t norm_bytes = (uint64_t)W * 4;
+    const uint64_t per_layer = align256(qkv_bytes) + align256(o_bytes) + align256(gu_bytes) + align256(down_bytes) +
+                               2 * align256(norm_bytes);
+    const uint64_t total = align256(embed_bytes) + (tied ? 0 : align256(embed_bytes)) + align256(norm_bytes) +
+                           per_layer * (uint64_t)c.layers;
+    void* mem = nullptr;
+    hipError_t e = tmh::device_malloc(&mem, total);
+    if (e != hipSuccess) return code(e);
+    uint8_t* base = (uint8_t*)mem;
+    uint64_t at = 0;
+    auto carve = [&](uint64_t bytes) {
+        uint64_t p = (uint64_t)(base + at);
+        at += align256(bytes);
+        return p;
+    };
+    auto upload = [&](const std::string& name, const int32_t* order, uint32_t count, uint64_t dst) {
+        return tmh_gguf_upload((uint64_t)&g, name.c_str(), order, count, dst);
+    };
+    auto upload_norm = [&](const std::string& name, uint64_t dst) {
+        const tmh::GgufTensor* t = g.find(name);
+        if (t->kind == tmh::GGUF_F32) return upload(name, nullptr, 0, dst);
+        std::vector<float> wide;
+        widen(g, *t, wide);
+        return tmh_upload_async(dst, wide.data(), wide.size() * 4);
+    };
+    std::vector<uint64_t> attn_norm(c.layers), ffn_norm(c.layers), qkv(c.layers), o(c.layers), gate_up(c.layers),
+        down(c.layers);
+    const std::vector<int32_t> q_order = unpermute_order(c.heads, c.head_width);
+    const std::vector<int32_t> k_order = unpermute_order(c.kv_heads, c.head_width);
+    tmh_llama_weights w{};
+    w.embed = carve(embed_bytes);
+    err = upload("token_embd.weight", nullptr, 0, w.embed);
+    if (!err && !tied) {
+        w.head = carve(embed_bytes);
+        err = upload("output.weight", nullptr, 0, w.head);
+    }
+    if (!err) {
+        w.norm = carve(norm_bytes);
+        err = upload_norm("output_norm.weight", w.norm);
+    }
+    for (int32_t l = 0; l < c.layers && !err; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        attn_norm[l] = carve(norm_bytes);
+        ffn_norm[l] = carve(norm_bytes);
+        qkv[l] = carve(qkv_bytes);
+        o[l] = carve(o_bytes);
+        gate_up[l] = carve(gu_bytes);
+        down[l] = carve(down_bytes);
+        err = upload_norm(b + "attn_norm.weight", attn_norm[l]);
+        if (!err) err = upload_norm(b + "ffn_norm.weight", ffn_norm[l]);
+        if (!err) err = upload(b + "attn_q.weight", q_order.data(), (uint32_t)q_order.size(), qkv[l]);
+        if (!err) err = upload(b + "attn_k.weight", k_order.data(), (uint32_t)k_order.size(), qkv[l] + qn * row);
+        if (!err) err = upload(b + "attn_v.weight", nullptr, 0, qkv[l] + (qn + kvn) * row);
+        if (!err) err = upload(b + "attn_output.weight", nullptr, 0, o[l]);
+        if (!err) err = upload(b + "ffn_gate.weight", nullptr, 0, gate_up[l]);
+        if (!err) err = upload(b + "ffn_up.weight", nullptr, 0, gate_up[l] + H * row);
+        if (!err) err = upload(b + "ffn_down.weight", nullptr, 0, down[l]);
+    }
+    if (!err) {
+        w.attn_norm = attn_norm.data();
+        w.ffn_norm = ffn_norm.data();
+        w.qkv = qkv.data();
+        w.o = o.data();
+        w.gate_up = gate_up.data();
+        w.down = down.data();
+        err = tmh_llama_create(&c, &w, rows, capacity ? capacity : (uint32_t)c.context, max_tokens, model);
+    }
+    if (!err) err = tmh_synchronize();  // the staged uploads have landed
+    if (err) {
+        if (*model) {
+            (void)tmh_llama_destroy(*model);
+            *model = 0;
+        }
+        (void)hipFree(mem);
+        return err;
+    }
+    ((Llama*)*model)->owned = mem;
+    if (config) *config = c;
     return TMH_SUCCESS;
 }
 

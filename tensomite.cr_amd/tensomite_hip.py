@@ -150,6 +150,12 @@ SIGNATURES = {
     "tmh_llama_reset": (INT, [U64, U32]),
     "tmh_llama_step": (INT, [U64, U32]),
     "tmh_llama_destroy": (INT, [U64]),
+    "tmh_gguf_open": (INT, [ctypes.c_char_p, ctypes.POINTER(U64)]),
+    "tmh_gguf_close": (INT, [U64]),
+    "tmh_gguf_tensor": (INT, [U64, ctypes.c_char_p, ctypes.POINTER(U32), ctypes.POINTER(I64), ctypes.POINTER(U32),
+                              ctypes.POINTER(U64)]),
+    "tmh_gguf_upload": (INT, [U64, ctypes.c_char_p, VP, U32, U64]),
+    "tmh_llama_load_gguf": (INT, [ctypes.c_char_p, U32, U32, U32, ctypes.POINTER(LlamaConfig), ctypes.POINTER(U64)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -503,6 +509,52 @@ class HIPDevice:
         return ms.value
 
 
+class GGUFFile:
+    """A GGUF file mapped by the library (tmh_gguf_*): tensor entries and
+    uploads, whole or as rows in a given order (GGUF#[] then take_rows,
+    gguf.cr:112-136, tensor/quantised.cr:32-43). Needs no GPU to open."""
+
+    KINDS = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 8: "Q8_0", 30: "BF16"}
+
+    def __init__(self, path: str):
+        self.lib = library()
+        self.path = path
+        h = U64(0)
+        check("tmh_gguf_open", self.lib.tmh_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h.value
+
+    def entry(self, name: str):
+        """(kind name, shape, bytes) of tensor `name`."""
+        kind, dims, nbytes = U32(0), U32(0), U64(0)
+        shape = (I64 * 4)()
+        check("tmh_gguf_tensor", self.lib.tmh_gguf_tensor(self.handle, name.encode(), ctypes.byref(kind), shape,
+                                                          ctypes.byref(dims), ctypes.byref(nbytes)))
+        return self.KINDS[kind.value], [shape[i] for i in range(dims.value)], nbytes.value
+
+    def upload(self, device: "HIPDevice", name: str, rows=None) -> Buffer:
+        """Tensor `name` (or its rows in the order given) in a new device buffer."""
+        _, shape, nbytes = self.entry(name)
+        order = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
+        size = nbytes if order is None else nbytes // shape[0] * order.size
+        buf = device.alloc(max(size, 4))
+        device.bind()
+        check("tmh_gguf_upload", self.lib.tmh_gguf_upload(self.handle, name.encode(),
+                                                          None if order is None else order.ctypes.data,
+                                                          0 if order is None else order.size, buf.pointer))
+        return buf
+
+    def close(self) -> None:
+        if getattr(self, "handle", 0):
+            self.lib.tmh_gguf_close(self.handle)
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 LLAMA_LAYER_KEYS = ("attn_norm", "ffn_norm", "qkv", "o", "gate_up", "down")
 
 
@@ -542,6 +594,26 @@ class HIPLlama:
         check("tmh_llama_create", device.lib.tmh_llama_create(ctypes.byref(cfg), ctypes.byref(w), rows,
                                                               self.capacity, max_tokens, ctypes.byref(handle)))
         self.handle = handle.value
+
+    @classmethod
+    def load_gguf(cls, device: HIPDevice, path: str, rows: int = 1, capacity: int = 0,
+                  max_tokens: int = 128) -> "HIPLlama":
+        """Llama.load of a GGUF file straight onto the device (tmh_llama_load_gguf):
+        the decoder owns the weights it uploads."""
+        self = cls.__new__(cls)
+        self.device = device
+        self.rows = rows
+        self.buffers = {}
+        cfg, handle = LlamaConfig(), U64(0)
+        device.bind()
+        check("tmh_llama_load_gguf", device.lib.tmh_llama_load_gguf(os.fsencode(path), rows, capacity, max_tokens,
+                                                                    ctypes.byref(cfg), ctypes.byref(handle)))
+        self.handle = handle.value
+        kinds = {Q8_0: "Q8_0", Q4_0: "Q4_0", Q4_1: "Q4_1"}
+        self.config = {name: getattr(cfg, name) for name, _ in LlamaConfig._fields_}
+        self.config["kind"] = kinds[self.config["kind"]]
+        self.capacity = capacity or self.config["context"]
+        return self
 
     def forward(self, ids, row: int = 0, last_only: bool = False) -> np.ndarray:
         """Logits [len(ids) or 1, vocab] of ids run after the row's cached positions."""

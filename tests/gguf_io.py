@@ -92,3 +92,43 @@ class GGUF:
         if kind != "F32":
             raise ValueError(f"{name} is {kind}")
         return self.raw(name).view(np.float32).reshape(shape)
+
+
+def write(path: str, metadata, tensors, alignment: int = 32) -> None:
+    """Writes a GGUF v3 file: metadata as (key, value) pairs (int -> uint32
+    or int64, float -> float32, str, bool), tensors as (name, kind name or
+    ggml code, shape outermost first, bytes) in that order, data aligned as
+    the reader expects (gguf.cr:156-191's layout)."""
+    codes = {v: k for k, v in KIND_NAMES.items()}
+    out = bytearray()
+    out += struct.pack("<IIQQ", MAGIC, 3, len(tensors), len(metadata))
+
+    def string(s):
+        b = s.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    for key, value in metadata:
+        out += string(key)
+        if isinstance(value, bool):
+            out += struct.pack("<IB", 7, value)
+        elif isinstance(value, int):
+            out += struct.pack("<II", 4, value) if 0 <= value < 2 ** 32 else struct.pack("<Iq", 11, value)
+        elif isinstance(value, float):
+            out += struct.pack("<If", 6, value)
+        else:
+            out += struct.pack("<I", 8) + string(value)
+    offset = 0
+    offsets = []
+    for name, kind, shape, data in tensors:
+        offsets.append(offset)
+        out += string(name) + struct.pack("<I", len(shape))
+        for d in reversed(shape):
+            out += struct.pack("<Q", d)
+        out += struct.pack("<IQ", codes.get(kind, kind), offset)
+        offset += (len(data) + alignment - 1) // alignment * alignment
+    out += b"\0" * ((-len(out)) % alignment)
+    for (name, kind, shape, data), off in zip(tensors, offsets):
+        out += bytes(data)
+        out += b"\0" * ((-len(out)) % alignment)
+    with open(path, "wb") as f:
+        f.write(out)

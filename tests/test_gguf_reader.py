@@ -1,0 +1,58 @@
+"""The library's GGUF reader (tmh_gguf_open/tmh_gguf_tensor) without a GPU:
+the directory of every fixture equals the test reader's (both follow
+gguf.cr:289-329), and damaged files are errors, not faults."""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import tensomite_hip as th
+from gguf_io import BLOCK_BYTES, GGUF, write
+
+
+def fixtures(golden):
+    return sorted(glob.glob(os.path.join(golden, "*", "*.gguf")))
+
+
+def test_directory_matches_the_test_reader(golden):
+    files = fixtures(golden)
+    assert len(files) >= 4
+    for path in files:
+        ref = GGUF(path)
+        lib = th.GGUFFile(path)
+        for name, (kind, shape, _) in ref.entries.items():
+            got_kind, got_shape, got_bytes = lib.entry(name)
+            count = int(np.prod(shape))
+            want_bytes = count // 32 * BLOCK_BYTES[kind] if kind in BLOCK_BYTES else count * (4 if kind == "F32" else 2)
+            assert (got_kind, got_shape, got_bytes) == (kind, shape, want_bytes), (path, name)
+        with pytest.raises(th.DeviceError):
+            lib.entry("no.such.tensor")
+        lib.close()
+
+
+def test_damaged_files_are_errors(tmp_path, golden):
+    good = open(os.path.join(golden, "tiny_llama", "model-q8_0.gguf"), "rb").read()
+    cases = {"magic": b"XXXX" + good[4:], "truncated": good[:200], "short": good[:10],
+             "version": good[:4] + (9).to_bytes(4, "little") + good[8:], "data": good[:len(good) - 100]}
+    for name, data in cases.items():
+        path = tmp_path / f"{name}.gguf"
+        path.write_bytes(data)
+        with pytest.raises(th.DeviceError):
+            th.GGUFFile(str(path))
+    with pytest.raises(th.DeviceError):
+        th.GGUFFile(str(tmp_path / "missing.gguf"))
+
+
+def test_unknown_kind_is_a_dtype_error(tmp_path):
+    path = str(tmp_path / "q4_k.gguf")
+    write(path, [("general.architecture", "llama")], [("w", 12, [4, 256], bytes(4 * 144))])  # Q4_K
+    with pytest.raises(th.DTypeError):
+        th.GGUFFile(path)
+
+
+def test_rows_not_whole_blocks_are_a_shape_error(tmp_path):
+    path = str(tmp_path / "odd.gguf")
+    write(path, [], [("w", "Q8_0", [2, 48], bytes(2 * 51))])
+    with pytest.raises(th.ShapeError):
+        th.GGUFFile(path)

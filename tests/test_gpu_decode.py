@@ -296,3 +296,70 @@ def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
     for r, p in enumerate(prompts):
         gpu.forward(p, row=r, last_only=True)
     assert np.array_equal(gpu.generate(steps, graph=False), got)
+
+
+# ------------------------------------------------------------ GGUF loading
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0"])
+def test_load_gguf_tiny_llama_bit_exact(dev, golden, fmt):
+    # Llama.load(GGUF) straight onto the device (llama.cr:184-235): the config
+    # from the metadata, q/k unpermuted and projections merged on upload; the
+    # forward has the oracle's bits on the fixture's own weights.
+    import json
+    import os
+    path = os.path.join(golden, "tiny_llama", f"model-{fmt.lower()}.gguf")
+    with open(os.path.join(golden, "tiny_llama", "logits.json")) as f:
+        prompt = json.load(f)["prompt_ids"]
+    config, weights = tiny_llama(golden, fmt)
+    gpu = th.HIPLlama.load_gguf(dev, path, max_tokens=64)
+    for key in ("layers", "width", "heads", "kv_heads", "head_width", "hidden", "vocab", "context", "kind"):
+        assert gpu.config[key] == config[key], key
+    assert np.float32(gpu.config["eps"]) == np.float32(config["eps"])
+    want = oracle.Llama(config, weights).forward(prompt)
+    assert np.array_equal(bits(gpu.forward(prompt)), bits(want))
+
+
+def test_gguf_upload_rows_in_order(dev, golden):
+    import os
+    from gguf_io import GGUF
+    from llama_fixtures import take_rows, unpermute_order
+    path = os.path.join(golden, "tiny_llama", "model-q4_0.gguf")
+    g = th.GGUFFile(path)
+    order = unpermute_order(32, 4)
+    buf = g.upload(dev, "blk.1.attn_q.weight", rows=order)
+    got = dev.to_array(buf, np.uint8, 32 * 18)
+    dev.sync()
+    assert np.array_equal(got, take_rows(GGUF(path).raw("blk.1.attn_q.weight"), 18, order))
+    whole = g.upload(dev, "token_embd.weight")
+    assert np.array_equal(dev.to_array(whole, np.uint8, 7200), GGUF(path).raw("token_embd.weight"))
+
+
+def test_load_gguf_refuses_f16_matrices(dev, golden):
+    import os
+    with pytest.raises(th.DTypeError):
+        th.HIPLlama.load_gguf(dev, os.path.join(golden, "tiny_llama", "model-f16.gguf"))
+
+
+@pytest.mark.parametrize("norm_kind", ["F16", "BF16"])
+def test_load_gguf_written_model(dev, tmp_path, norm_kind):
+    # a grouped-query model with an untied head and half-width norms, written
+    # in llama.cpp's layout; loaded, it runs as the oracle runs the same
+    # weights (norms widened as GGUF#[] widens them)
+    from llama_fixtures import write_llama_gguf
+    config = small_config("Q8_0", heads=8, kv_heads=2, head_width=32, width=256, hidden=512, vocab=300)
+    weights = random_llama(config, seed=40, norm_jitter=0.2)
+    weights["head"] = random_llama(config, seed=41)["embed"]
+    path = str(tmp_path / "model.gguf")
+    write_llama_gguf(path, config, weights, norm_kind)
+    if norm_kind == "F16":
+        widen = lambda v: np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+    else:
+        widen = lambda v: ((np.asarray(v, np.float32).view(np.uint32) >> 16) << 16).view(np.float32)
+    cpu_weights = dict(weights, norm=widen(weights["norm"]), attn_norm=[widen(v) for v in weights["attn_norm"]],
+                       ffn_norm=[widen(v) for v in weights["ffn_norm"]])
+    prompt = list(np.random.default_rng(42).integers(0, 300, 11))
+    gpu = th.HIPLlama.load_gguf(dev, path, max_tokens=16)
+    cpu = oracle.Llama(config, cpu_weights)
+    assert np.array_equal(bits(gpu.forward(prompt, last_only=True)), bits(cpu.forward(prompt, last_only=True)))
+    assert list(gpu.generate(12)[0]) == cpu.generate(prompt, 12)
