@@ -315,7 +315,8 @@ def test_errors_are_typed(dev):
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_plan_equals_products_one_by_one(dev, fmt):
     # tmh_plan_*: many one-row products in one launch give each product's bits.
-    shapes = [(960, 576), (576, 576), (3072, 576), (576, 1536), (300, 2048), (7, 64), (2304, 768), (100, 8192)]
+    shapes = [(960, 576), (576, 576), (3072, 576), (576, 1536), (300, 2048), (7, 64), (2304, 768), (100, 8192),
+              (1, 4096), (130, 128)]
     ws, xs, wants = [], [], []
     for i, (n, k) in enumerate(shapes):
         wq = weights(fmt, n, k, 500 + i)
