@@ -125,6 +125,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
     ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
@@ -269,11 +271,12 @@ def main():
     dev.sync()
     if not args.no_decode:
         log("decode at the 1.7B shape ...")
-        result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu)
+        result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
+                                            graph=not args.decode_eager)
     print(json.dumps(result), flush=True)
 
 
-def decode_1p7b(dev, steps, cpu_seconds, with_cpu):
+def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
     """Config 5: greedy decode of a SmolLM2-1.7B-shaped Q4_0 Llama (random
     block weights, tied head) through the device-resident decoder, after a
     128-token prompt, at batch 1 and batch 8 (f32 KV capacity 2048). A step is
@@ -302,18 +305,18 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu):
             t = time.perf_counter()
             model.forward(prompt, row=r, last_only=True)
             prefill.append(time.perf_counter() - t)
-        model.generate(4, graph=True)  # graph captured, state on the device
+        model.generate(4, graph=graph)  # graph captured, state on the device
         for _ in range(4):
-            model.step(graph=True)
+            model.step(graph=graph)
         dev.sync()
         e0, e1 = dev.event(), dev.event()
         dev.record(e0)
         for _ in range(steps):
-            model.step(graph=True)
+            model.step(graph=graph)
         dev.record(e1)
         ms = dev.elapsed_ms(e0, e1) / steps
         dev.sync()
-        out[f"batch{rows}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(rows * 1e3 / ms, 1),
+        out[f"batch{rows}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(rows * 1e3 / ms, 1), "graph": graph,
                                "steps": steps, "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
                                "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
         model.destroy()
