@@ -286,10 +286,17 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, A
     const uint32_t* wp = (const uint32_t*)w;
 
     if (rsub < rpi) {
-        uint32_t a[NB == 1 ? 16 : 1];
-        float sx0 = 0, sx1 = 0, mx0 = 0, mx1 = 0;
-        int e0 = 0, e1 = 0;
-        if constexpr (NB == 1) load_activations<KIND>(act, k, nb, 0, j, a, sx0, sx1, e0, e1, mx0, mx1);
+        // This thread's pair of every activation row, held in registers for
+        // all steps (j is fixed per thread).
+        uint32_t a[NB][16];
+        float sx0[NB], sx1[NB], mx0[NB], mx1[NB];
+        int e0[NB], e1[NB];
+#pragma unroll
+        for (uint32_t b = 0; b < (uint32_t)NB; ++b) {
+            mx0[b] = mx1[b] = 0.0f;
+            e0[b] = e1[b] = 0;
+            load_activations<KIND>(act, k, nb, b, j, a[b], sx0[b], sx1[b], e0[b], e1[b], mx0[b], mx1[b]);
+        }
 #pragma unroll 2
         for (uint32_t s = 0; s < steps; ++s) {
             const uint32_t r = s * rpi + rsub;
@@ -297,21 +304,11 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, A
             if (row >= n) break;
             uint32_t u[PW];
             load_pair<KIND>(wp + (size_t)row * row_words + (size_t)j * PW, u);
-            if constexpr (NB == 1) {
+#pragma unroll
+            for (uint32_t b = 0; b < (uint32_t)NB; ++b) {
                 float c0, c1;
-                Pair<KIND>::contribute(u, a, sx0, sx1, e0, e1, mx0, mx1, c0, c1);
-                *(float2*)(part + (size_t)r * stride + 2u * j) = make_float2(c0, c1);
-            } else {
-#pragma unroll 1
-                for (uint32_t b = 0; b < (uint32_t)NB; ++b) {
-                    uint32_t ab[16];
-                    float bsx0, bsx1, bmx0 = 0, bmx1 = 0;
-                    int be0 = 0, be1 = 0;
-                    load_activations<KIND>(act, k, nb, b, j, ab, bsx0, bsx1, be0, be1, bmx0, bmx1);
-                    float c0, c1;
-                    Pair<KIND>::contribute(u, ab, bsx0, bsx1, be0, be1, bmx0, bmx1, c0, c1);
-                    *(float2*)(part + (size_t)(b * tr + r) * stride + 2u * j) = make_float2(c0, c1);
-                }
+                Pair<KIND>::contribute(u, a[b], sx0[b], sx1[b], e0[b], e1[b], mx0[b], mx1[b], c0, c1);
+                *(float2*)(part + (size_t)(b * tr + r) * stride + 2u * j) = make_float2(c0, c1);
             }
         }
     }
@@ -973,7 +970,9 @@ static hipError_t launch_lanes_nb(const uint8_t* w, Activations act, float* dst,
 template <int KIND>
 static hipError_t launch_lanes(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
                                uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
-    // Activation rows in groups of 16, 8, 4, 2 and 1: each output depends on
+    // Activation rows in groups of 8, 4, 2 and 1 (a thread holds its pair
+    // of every row of a group in registers; measured, one group of 8 beats
+    // two of 4, which read the weights twice): each output depends on
     // its own row only, so the grouping changes no bits.
     const uint32_t nb = k >> 5;
     const uint32_t rpi = 256u / (nb / 2u);
@@ -989,9 +988,7 @@ static hipError_t launch_lanes(const uint8_t* w, Activations act, float* dst, co
         float* d = dst + (size_t)done * n;
         hipError_t err;
         uint32_t take;
-        if (left >= 16 && 16u * smallest <= LANES_LDS_LIMIT)
-            err = launch_lanes_nb<KIND, 16>(w, a, d, bias, n, k, compute_units, stream), take = 16;
-        else if (left >= 8 && 8u * smallest <= LANES_LDS_LIMIT)
+        if (left >= 8 && 8u * smallest <= LANES_LDS_LIMIT)
             err = launch_lanes_nb<KIND, 8>(w, a, d, bias, n, k, compute_units, stream), take = 8;
         else if (left >= 4 && 4u * smallest <= LANES_LDS_LIMIT)
             err = launch_lanes_nb<KIND, 4>(w, a, d, bias, n, k, compute_units, stream), take = 4;
