@@ -246,7 +246,7 @@ def main():
         },
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
         "roofline": {
-            "kernel": "tmh::k_matvec_rows<1, 3u> (Q4_0; one launch = the 121 products of a token)",
+            "kernel": plans[0].describe() + " (Q4_0; one launch = the 121 products of a token)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -265,6 +265,11 @@ int tmh_plan_run(uint64_t plan);
 
 int tmh_plan_destroy(uint64_t plan);
 
+/* Writes a one-line description of the plan's launch (kernel, grid, LDS)
+ * into text (at most size bytes, NUL-terminated). No counterpart in the
+ * reference: it names the kernel for profilers and benchmarks. */
+int tmh_plan_describe(uint64_t plan, char* text, uint32_t size);
+
 /* ------------------------------------------------- the rest of the decode graph
  *
  * The F32 ops a Llama decode step runs besides its products, each with the

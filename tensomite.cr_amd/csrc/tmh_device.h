@@ -38,6 +38,21 @@ __device__ __forceinline__ float round_to_half(float x) {
 
 // ------------------------------------------------------ activation quantise
 
+// A value of another lane of this lane's 8-lane group, by DPP (no LDS
+// round trip): XOR1 and XOR2 swap within quads, MIRROR takes lane 7 - i of
+// the half row. Every lane of the group must be active.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR = 0x141 };
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_int(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_float(float v) {
+    return __int_as_float(dpp_int<CTRL>(__float_as_int(v)));
+}
+
 // The quantised form of 4 of a block's 32 activations, held by one lane of
 // an 8-lane group (all 8 lanes active): the group's amax and Σq reduced over
 // the 8 lanes, then quantize_activations' arithmetic (quant.cr:428-442).
@@ -53,11 +68,14 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
     amax = fabsf(v1) > amax ? fabsf(v1) : amax;
     amax = fabsf(v2) > amax ? fabsf(v2) : amax;
     amax = fabsf(v3) > amax ? fabsf(v3) : amax;
-#pragma unroll
-    for (int width = 1; width < 8; width <<= 1) {
-        float other = __shfl_xor(amax, width, 8);
-        amax = other > amax ? other : amax;
-    }
+    // The group's largest magnitude (max is exact in any order): the quad's
+    // by two swaps, then the other quad's by the mirror.
+    float other = dpp_float<DPP_XOR1>(amax);
+    amax = other > amax ? other : amax;
+    other = dpp_float<DPP_XOR2>(amax);
+    amax = other > amax ? other : amax;
+    other = dpp_float<DPP_MIRROR>(amax);
+    amax = other > amax ? other : amax;
     const float d = amax / 127.0f;
     const float id = d == 0.0f ? 0.0f : 1.0f / d;
     const int q0 = (int8_t)(int)roundf(v0 * id);
@@ -68,8 +86,9 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
     out.packed = (uint32_t)(q0 & 0xff) | (uint32_t)(q1 & 0xff) << 8 | (uint32_t)(q2 & 0xff) << 16 |
                  (uint32_t)(q3 & 0xff) << 24;
     int total = q0 + q1 + q2 + q3;
-#pragma unroll
-    for (int width = 1; width < 8; width <<= 1) total += __shfl_xor(total, width, 8);
+    total += dpp_int<DPP_XOR1>(total);
+    total += dpp_int<DPP_XOR2>(total);
+    total += dpp_int<DPP_MIRROR>(total);
     out.total = total;
     out.scale = round_to_half(d);
     out.sum = round_to_half((float)total * d);

@@ -69,6 +69,45 @@ size_t row_part_bytes(const RowProduct& p);
 hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* owner, uint32_t tiles,
                        size_t act_bytes, size_t part_bytes, int compute_units, hipStream_t stream);
 
+// One product of the streamed one-row kernel: operands; the address of the
+// last 16-byte piece of its weight rows (direct loads never read past it);
+// its steps first ... first + steps - 1 of the launch, each `rows`
+// consecutive weight rows (the last may hold fewer), step_bytes apart;
+// pairs per row np, bytes per row, LDS floats between two rows'
+// contributions.
+struct StreamProduct {
+    const uint8_t* w;
+    const float* x;
+    float* dst;
+    const float* bias;
+    uint64_t wlast;
+    uint32_t n, k, first, steps;
+    uint32_t np, rows, row_bytes, stride;
+    uint32_t step_bytes, unused[3];
+};
+
+// The shape of a streamed launch: the product table and each workgroup's
+// first product (device memory), steps in all, workgroups, ring slots,
+// whether any product has a bias, LDS of one activation buffer and of one
+// buffer of contributions (floats), floats of one staged x, the
+// activations' LDS offset, LDS in all.
+struct StreamLaunch {
+    const StreamProduct* table;
+    const uint32_t* starts;
+    uint32_t total, grid, ring, has_bias, act_bytes, part_floats, x_floats, act_offset;
+    size_t lds;
+};
+
+// Host side: fills in each product's geometry and steps (w, x, dst, bias, n,
+// k set by the caller), the launch's shape, and each workgroup's first
+// product. False when the products do not fit the kernel (rows of an odd
+// number of blocks, or LDS).
+bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& launch,
+                 std::vector<uint32_t>& starts);
+
+// Launches the streamed one-row kernel (table and starts in device memory).
+hipError_t launch_stream(uint32_t kind, const StreamLaunch& launch, hipStream_t stream);
+
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);

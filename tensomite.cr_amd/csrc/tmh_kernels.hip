@@ -26,8 +26,8 @@ namespace tmh {
 // ------------------------------------------------------ activation quantise
 
 // One group of 8 lanes per block of 32 activations, 4 values a lane: the
-// block's largest magnitude and Σq are reduced over the 8 lanes (max and
-// integer sums are exact in any order). Then, as quantize_activations
+// block's largest magnitude and Σq are reduced over the 8 lanes by DPP (max
+// and integer sums are exact in any order). Then, as quantize_activations
 // (quant.cr:428-442): d = amax/127, id = 1/d (0 when d is 0),
 // q = round-half-away(x·id) as int8, scale F16(d), sum F16(float(Σq)·d).
 template <bool VEC>
@@ -51,11 +51,12 @@ __global__ __launch_bounds__(256) void k_quantize_rows_q8(const float* __restric
     amax = fabsf(v1) > amax ? fabsf(v1) : amax;
     amax = fabsf(v2) > amax ? fabsf(v2) : amax;
     amax = fabsf(v3) > amax ? fabsf(v3) : amax;
-#pragma unroll
-    for (int width = 1; width < 8; width <<= 1) {
-        float other = __shfl_xor(amax, width, 8);
-        amax = other > amax ? other : amax;
-    }
+    float other = dpp_float<DPP_XOR1>(amax);
+    amax = other > amax ? other : amax;
+    other = dpp_float<DPP_XOR2>(amax);
+    amax = other > amax ? other : amax;
+    other = dpp_float<DPP_MIRROR>(amax);
+    amax = other > amax ? other : amax;
     const float d = amax / 127.0f;
     const float id = d == 0.0f ? 0.0f : 1.0f / d;
     const int q0 = (int8_t)(int)roundf(v0 * id);
@@ -66,8 +67,9 @@ __global__ __launch_bounds__(256) void k_quantize_rows_q8(const float* __restric
                             (uint32_t)(q3 & 0xff) << 24;
     *(uint32_t*)(qs + (size_t)row * k + blk * 32u + sub * 4u) = packed;
     int total = q0 + q1 + q2 + q3;
-#pragma unroll
-    for (int width = 1; width < 8; width <<= 1) total += __shfl_xor(total, width, 8);
+    total += dpp_int<DPP_XOR1>(total);
+    total += dpp_int<DPP_XOR2>(total);
+    total += dpp_int<DPP_MIRROR>(total);
     if (sub == 0) {
         scales[g] = round_to_half(d);
         sums[g] = round_to_half((float)total * d);
@@ -611,6 +613,329 @@ __global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_b
     matvec_rows<KIND, D>(nullptr, nullptr, p, p.tiles, act_bytes);
 }
 
+// ------------------------------------------- one row, streamed through LDS
+
+// x · wᵀ for one activation row per product, for every product of a plan in
+// one launch. The plan's weight rows form one sequence of steps (a step is
+// the consecutive rows of one product that fit 8 KB, at most one pair of
+// blocks per thread); workgroup b takes steps [total·b/G, total·(b+1)/G),
+// an equal share whatever the products' sizes. Weights travel from HBM to
+// LDS by the direct loads of gfx950 (global_load_lds_dwordx4: 16 bytes a
+// lane, 1 KB a wave; each wave brings 2 KB of a step) into a ring of R
+// slots, R - 1 steps ahead of the step being computed: no VGPR holds weights
+// in flight, and the ring runs on across product boundaries. One workgroup
+// barrier per step; before it each wave waits for its own loads of the step
+// (a counted s_waitcnt that leaves the later steps' loads in flight). After
+// it, the step's slot is complete and is computed (thread t takes pair
+// j = t % np of row t / np, as the lanes kernels do), and the previous
+// step's contributions are complete and are folded by one thread per row in
+// block order -- the host's order. A product's activations are quantised
+// into one of two LDS buffers: the range's first two before the loop, from
+// x brought in by direct loads ahead of every weight load; a later one when
+// its turn comes. The loop keeps its scalar work small: the scalar unit is
+// shared by every wave of a compute unit.
+
+constexpr uint32_t STREAM_STEP = 8192;  // bytes of weights a step's loads bring
+
+typedef __attribute__((address_space(3))) uint8_t lds_byte;
+
+// The LDS byte address of p (a pointer into shared memory), uniform.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_byte*)p);
+}
+
+// Direct loads from global memory into LDS: each lane's 16 (or 4) bytes at
+// `from` land at LDS byte lds + 16·lane (4·lane). Written as inline asm so
+// that the compiler does not see the LDS write: it would otherwise wait for
+// every load in flight before any LDS access it cannot prove disjoint,
+// which would end the streaming; the kernels order these writes themselves
+// (counted waits and barriers). M0 carries the LDS address (an operand, so
+// the compiler writes it); s_nop covers the wait state an M0 write needs
+// before an LDS direct load.
+__device__ __forceinline__ void lds_load16(const void* from, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(from), "{m0}"(lds) : "memory");
+}
+
+// lds_load16 marked non-temporal: weights stream through the caches once,
+// so they should not displace what is read again (activations, tables).
+__device__ __forceinline__ void lds_load16_nt(const void* from, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(from), "{m0}"(lds) : "memory");
+}
+
+__device__ __forceinline__ void lds_load4(const void* from, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(from), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt: at most N vector memory operations of this wave outstanding,
+// every LDS and scalar memory operation done.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_lds() {
+    static_assert(N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (7 << 4));
+}
+
+// The per-step workgroup barrier, after this wave's operations are done as
+// wait_vm_lds<N> says. The empty asm statements keep the compiler from
+// moving memory operations across it (s_barrier alone does not order memory
+// for the compiler; __syncthreads() would wait for every load in flight).
+template <uint32_t N>
+__device__ __forceinline__ void step_barrier() {
+    asm volatile("" ::: "memory");
+    wait_vm_lds<N>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// step_barrier<A·PS> for a runtime A in [0, AMAX]: the steps issued after the
+// one about to be computed, PS operations each.
+template <uint32_t PS, uint32_t AMAX>
+__device__ __forceinline__ void step_barrier_ahead(uint32_t ahead) {
+    if constexpr (AMAX == 0) {
+        step_barrier<0>();
+    } else {
+        if (ahead >= AMAX)
+            step_barrier<AMAX * PS>();
+        else
+            step_barrier_ahead<PS, AMAX - 1>(ahead);
+    }
+}
+
+// Brings x (k floats) into LDS at `to` by direct loads, 1 KB per wave load
+// (16-byte aligned x) or 256 bytes (otherwise); lanes past the end read the
+// last piece again.
+__device__ __forceinline__ void issue_x(const float* x, uint32_t k, uint32_t to, uint32_t wave) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uintptr_t base = (uintptr_t)x;
+    if ((base & 15u) == 0) {
+        const uintptr_t last = base + (uintptr_t)k * 4u - 16u;
+        for (uint32_t q = wave; q * 1024u < k * 4u; q += 4u) {
+            uintptr_t a = base + q * 1024u + lane * 16u;
+            a = a < last ? a : last;
+            lds_load16((const void*)a, to + q * 1024u);
+        }
+    } else {
+        const uintptr_t last = base + (uintptr_t)k * 4u - 4u;
+        for (uint32_t q = wave; q * 256u < k * 4u; q += 4u) {
+            uintptr_t a = base + q * 256u + lane * 4u;
+            a = a < last ? a : last;
+            lds_load4((const void*)a, to + q * 256u);
+        }
+    }
+}
+
+// quantise_into with x read from LDS (xs, k floats).
+template <int KIND>
+__device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint32_t k) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nb = k >> 5;
+    int8_t* lqs = (int8_t*)act;
+    float* lsc = (float*)(act + k);
+    int32_t* lex = (int32_t*)(lsc + nb);
+    for (uint32_t pass = 0; pass * 32u < nb; ++pass) {
+        const uint32_t g = pass * 32u + (t >> 3), sub = t & 7u;
+        if (g < nb) {
+            const float4 v = *(const float4*)(xs + g * 32u + sub * 4u);
+            const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
+            *(uint32_t*)(lqs + g * 32u + sub * 4u) = q.packed;
+            if (sub == 0) {
+                lsc[g] = q.scale;
+                lex[g] = KIND == 1 ? -8 * q.total : __float_as_int(q.sum);
+            }
+        }
+    }
+}
+
+// The sum of a row's nb contributions c[0 ... nb-1] in block order, from 0.
+__device__ __forceinline__ float fold_row(const float* c, uint32_t nb) {
+    float sum = 0.0f;
+    uint32_t q = 0;
+    for (; q + 4 <= nb; q += 4) {
+        const float4 e = *(const float4*)(c + q);
+        sum += e.x;
+        sum += e.y;
+        sum += e.z;
+        sum += e.w;
+    }
+    for (; q < nb; ++q) sum += c[q];
+    return sum;
+}
+
+// Per-thread geometry of a product: the thread's row r of a step and pair j,
+// its LDS byte offset within a step's weights, its offset (floats) within
+// the contributions.
+struct StreamLane {
+    uint32_t r, j, wofs, pofs;
+};
+
+template <int KIND>
+__device__ __forceinline__ StreamLane stream_lane(const StreamProduct& P) {
+    StreamLane g;
+    g.r = threadIdx.x / P.np;
+    g.j = threadIdx.x - g.r * P.np;
+    g.wofs = g.r * P.row_bytes + g.j * (Fmt<KIND>::PW * 4u);
+    g.pofs = g.r * P.stride + 2u * g.j;
+    return g;
+}
+
+// LDS layout of the streamed kernel: biases (R + 1 slots of 256 floats, with
+// HB), ring slots 0 ... R-1 of STREAM_STEP bytes, contributions (two buffers
+// of part_floats), then from act_offset the activations (two buffers of
+// act_bytes). Before the loop, the x of the range's first two products
+// (x_floats apart; none when x_floats is 0) is staged from ring slot R-1
+// on, over memory first written in the loop.
+template <int KIND, uint32_t R, bool HB>
+__global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __restrict__ table,
+                                                       const uint32_t* __restrict__ starts, uint32_t total,
+                                                       uint32_t act_bytes, uint32_t part_floats, uint32_t x_floats,
+                                                       uint32_t act_offset) {
+    constexpr uint32_t PW = Fmt<KIND>::PW;
+    constexpr uint32_t PS = HB ? 3u : 2u;  // vector memory operations a wave issues per step
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t G = gridDim.x, b = blockIdx.x, t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t s_begin = (uint32_t)((uint64_t)total * b / G);
+    const uint32_t s_end = (uint32_t)((uint64_t)total * (b + 1u) / G);
+    if (s_begin >= s_end) return;
+    const uint32_t count = s_end - s_begin;
+    float* biases = (float*)smem;
+    uint8_t* ring = smem + (HB ? (R + 1u) * 1024u : 0u);
+    float* parts = (float*)(ring + R * STREAM_STEP);
+    uint8_t* acts = smem + act_offset;
+    float* xs = (float*)(ring + (R - 1u) * STREAM_STEP);
+    const uint32_t ring_lds = lds_address(ring) + wave * 2048u, bias_lds = lds_address(biases) + wave * 256u;
+
+    // The range's first two products are quantised before the loop.
+    const uint32_t first_pi = __builtin_amdgcn_readfirstlane(starts[b]);
+    const StreamProduct p0 = table[first_pi];
+    const bool two = p0.first + p0.steps < s_end;
+    const StreamProduct p1 = two ? table[first_pi + 1u] : p0;
+    const bool staged = x_floats != 0;
+    if (staged) {
+        issue_x(p0.x, p0.k, lds_address(xs), wave);
+        if (two) issue_x(p1.x, p1.k, lds_address(xs) + x_floats * 4u, wave);
+    }
+
+    // The issue cursor: the step's first weight byte, steps left in its
+    // product, slots; with HB the step's first row and the product's bias.
+    uint32_t ipi = first_pi;
+    uint64_t isrc = (uint64_t)p0.w + (uint64_t)(s_begin - p0.first) * p0.step_bytes;
+    uint64_t iwlast = p0.wlast;
+    uint32_t ileft = p0.steps - (s_begin - p0.first), istep = p0.step_bytes, irows = p0.rows;
+    uint32_t irow = (s_begin - p0.first) * p0.rows, in = p0.n;
+    const float* ibias = p0.bias ? p0.bias : p0.x;  // without a bias, x[0] (never used)
+    uint32_t ihas = p0.bias ? 1u : 0u;
+    uint32_t islot = 0, ibslot = 0, issued = 0;
+    const uint32_t lane_bytes = wave * 2048u + lane * 16u;
+    auto issue_next = [&]() {
+        const uint64_t a0 = isrc & ~(uint64_t)15;
+        uint64_t a = a0 + lane_bytes;
+        lds_load16_nt((const void*)(a < iwlast ? a : iwlast), ring_lds + islot * STREAM_STEP);
+        a += 1024u;
+        lds_load16_nt((const void*)(a < iwlast ? a : iwlast), ring_lds + islot * STREAM_STEP + 1024u);
+        if constexpr (HB) {
+            const uint32_t row = min(irow + wave * 64u + lane, in - 1u);
+            lds_load4(ibias + row * ihas, bias_lds + ibslot * 1024u);
+            ibslot = ibslot == R ? 0u : ibslot + 1u;
+            irow += irows;
+        }
+        ++issued;
+        isrc += istep;
+        islot = islot == R - 1u ? 0u : islot + 1u;
+        if (--ileft == 0 && issued < count) {
+            const StreamProduct& q = table[++ipi];
+            isrc = (uint64_t)q.w, iwlast = q.wlast, ileft = q.steps, istep = q.step_bytes, irows = q.rows;
+            irow = 0, in = q.n;
+            ibias = q.bias ? q.bias : q.x;
+            ihas = q.bias ? 1u : 0u;
+        }
+    };
+    // The prologue issues R - 1 steps into slots 0 ... R-2 (the staged x
+    // lies past them) and waits for the staged x only. Without staging (x
+    // too long for the LDS), x is loaded directly, and the wait for it
+    // waits for the prologue's weights too.
+    const uint32_t prologue = min(R - 1u, count);
+    for (uint32_t s = 0; s < prologue; ++s) issue_next();
+    if (staged) {
+        step_barrier_ahead<PS, R - 1u>(prologue);  // the staged x is complete
+        quantise_lds<KIND>(acts, xs, p0.k);
+        if (two) quantise_lds<KIND>(acts + act_bytes, xs + x_floats, p1.k);
+    } else {
+        float4 xv[XP];
+        load_x(p0.x, p0.k, xv);
+        quantise_into<KIND>(acts, p0.x, p0.k, xv);
+        if (two) {
+            load_x(p1.x, p1.k, xv);
+            quantise_into<KIND>(acts + act_bytes, p1.x, p1.k, xv);
+        }
+    }
+    step_barrier_ahead<PS, R - 1u>(prologue);  // the staged x is read; the activations are complete
+
+    // The compute cursor (product cpi, the nth of the range): the step's
+    // first weight byte (its offset past 16 bytes is where the slot's data
+    // starts), rows left in the product, slot. The fold cursor: the
+    // previous step's outputs, rows, product geometry.
+    uint32_t cpi = first_pi, nth = 0;
+    uint64_t csrc = (uint64_t)p0.w + (uint64_t)(s_begin - p0.first) * p0.step_bytes;
+    uint32_t cleft = p0.n - (s_begin - p0.first) * p0.rows, crows = p0.rows, cstep = p0.step_bytes;
+    float* cdst = p0.dst + (s_begin - p0.first) * p0.rows;
+    uint32_t cnb = 2u * p0.np, cstride = p0.stride, cslot = 0, cbslot = 0;
+    bool cbias = p0.bias != nullptr;
+    StreamLane g = stream_lane<KIND>(p0);
+    PairActs v;
+    read_acts(acts, p0.k, g.j, v);
+    float* fdst = cdst;
+    uint32_t frows = 0, fnb = cnb, fstride = cstride, fbslot = 0;
+    bool fbias = cbias;
+
+    for (uint32_t i = 0; i < count; ++i) {
+        step_barrier_ahead<PS, R - 2u>(issued - 1u - i);
+        if (issued < count) issue_next();
+        // The previous step's fold.
+        if (t < frows) {
+            float sum = fold_row(parts + ((i - 1u) & 1u) * part_floats + t * fstride, fnb);
+            if (HB && fbias) sum += biases[fbslot * 256u + t];
+            *(__attribute__((address_space(1))) float*)(fdst + t) = sum;
+        }
+        // This step's contributions.
+        const uint32_t rows = min(crows, cleft);
+        if (g.r < rows) {
+            const uint32_t* w = (const uint32_t*)(ring + cslot * STREAM_STEP + ((uint32_t)csrc & 15u) + g.wofs);
+            uint32_t u[PW];
+#pragma unroll
+            for (uint32_t e = 0; e < PW; ++e) u[e] = w[e];
+            float c0, c1;
+            Pair<KIND>::contribute(u, v.a, v.sx0, v.sx1, v.e0, v.e1, v.mx0, v.mx1, c0, c1);
+            *(float2*)(parts + (i & 1u) * part_floats + g.pofs) = make_float2(c0, c1);
+        }
+        fdst = cdst, frows = rows, fnb = cnb, fstride = cstride, fbias = cbias, fbslot = cbslot;
+        cdst += rows, cleft -= rows, csrc += cstep;
+        cslot = cslot == R - 1u ? 0u : cslot + 1u;
+        if constexpr (HB) cbslot = cbslot == R ? 0u : cbslot + 1u;
+        if (cleft == 0 && i + 1u < count) {
+            const StreamProduct& q = table[++cpi];
+            ++nth;
+            csrc = (uint64_t)q.w, cleft = q.n, crows = q.rows, cstep = q.step_bytes, cdst = q.dst;
+            cnb = 2u * q.np, cstride = q.stride, cbias = q.bias != nullptr;
+            g = stream_lane<KIND>(q);
+            if (nth >= 2) {
+                // Into the buffer of the product before last (read before the
+                // barrier that began this step).
+                float4 xv[XP];
+                load_x(q.x, q.k, xv);
+                quantise_into<KIND>(acts + (nth & 1u) * act_bytes, q.x, q.k, xv);
+                step_barrier<0>();
+            }
+            read_acts(acts + (nth & 1u) * act_bytes, q.k, g.j, v);
+        }
+    }
+    step_barrier<0>();
+    if (t < frows) {
+        float sum = fold_row(parts + ((count - 1u) & 1u) * part_floats + t * fstride, fnb);
+        if (HB && fbias) sum += biases[fbslot * 256u + t];
+        *(__attribute__((address_space(1))) float*)(fdst + t) = sum;
+    }
+}
+
 // ------------------------------------------------ matrix cores: many rows
 
 // x · wᵀ for many activation rows on the int8 matrix cores. Workgroup tile
@@ -1127,6 +1452,121 @@ hipError_t launch_row(uint32_t kind, const uint8_t* w, const float* x, float* ds
     else
         hipLaunchKernelGGL((k_matvec_row<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
     return hipGetLastError();
+}
+
+// Ring slots and workgroups per compute unit of the streamed kernel
+// (TMH_STREAM_RING, TMH_STREAM_WGS override, for tuning).
+static uint32_t env_u32(const char* name, uint32_t fallback) {
+    const char* env = getenv(name);
+    const long v = env ? atol(env) : 0;
+    return v > 0 ? (uint32_t)v : fallback;
+}
+
+static constexpr uint32_t STREAM_RING_MIN = 2, STREAM_RING_MAX = 8, STREAM_WGS = 6;
+static constexpr size_t STREAM_LDS_LIMIT = 64u * 1024u, CU_LDS = 160u * 1024u;
+
+bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& l,
+                 std::vector<uint32_t>& starts) {
+    const uint32_t bb = block_bytes(kind);
+    uint64_t total = 0;
+    uint32_t max_k = 0, part = 0;
+    bool bias = false;
+    for (StreamProduct& p : products) {
+        const uint32_t nb = p.k >> 5;
+        if (p.n == 0 || nb < 2 || nb % 2 != 0 || nb > 512 || (uintptr_t)p.w % 4u != 0) return false;
+        p.np = nb / 2u;
+        p.row_bytes = nb * bb;
+        // Rows per step: a pair per thread, within the step's 8 KB after the
+        // first row's offset past 16 bytes (at most 12).
+        p.rows = std::min(256u / p.np, (STREAM_STEP - 12u) / p.row_bytes);
+        if (p.rows == 0) return false;
+        p.step_bytes = p.rows * p.row_bytes;
+        p.stride = lanes_stride(nb);
+        p.steps = (p.n + p.rows - 1u) / p.rows;
+        p.first = (uint32_t)total;
+        p.wlast = ((uint64_t)(uintptr_t)p.w + (uint64_t)p.n * p.row_bytes - 1u) & ~(uint64_t)15;
+        total += p.steps;
+        max_k = std::max(max_k, p.k);
+        part = std::max(part, p.rows * p.stride);
+        bias = bias || p.bias != nullptr;
+    }
+    if (total == 0 || total > 0x7fffffffull) return false;
+    l.total = (uint32_t)total;
+    l.act_bytes = (uint32_t)align16((size_t)max_k + 8u * (max_k >> 5));
+    l.part_floats = (part + 3u) & ~3u;
+    l.has_bias = bias ? 1u : 0u;
+    const uint32_t x_floats = (max_k + 255u) & ~255u;  // whole 1 KB direct loads
+    l.x_floats = x_floats;
+    const size_t bias_slots = bias ? 1024u : 0u;
+    // LDS with `ring` slots: biases, ring, contributions, then the
+    // activations, no earlier than the end of the x staged from slot R-1.
+    auto lds_for = [&](uint32_t ring, size_t& act_offset) {
+        const size_t head = (ring + 1u) * bias_slots;
+        act_offset = head + (size_t)ring * STREAM_STEP + 2u * (size_t)l.part_floats * 4u;
+        act_offset = std::max(act_offset, head + (size_t)(ring - 1u) * STREAM_STEP + 2u * (size_t)l.x_floats * 4u);
+        return act_offset + 2u * (size_t)l.act_bytes;
+    };
+    // Measured on the config-2 matvec set: more workgroups per compute unit
+    // beat a deeper ring (6 with two slots: 15.9 us; 4 with three: 18.0 us;
+    // 3 with four: 21 us), so the ring gets what `wgs` workgroups leave.
+    const uint32_t wgs = env_u32("TMH_STREAM_WGS", STREAM_WGS);
+    uint32_t ring = env_u32("TMH_STREAM_RING", 0u);
+    size_t act_offset = 0;
+    if (ring == 0) {
+        const size_t budget = std::min(CU_LDS / wgs, STREAM_LDS_LIMIT);
+        ring = STREAM_RING_MIN;
+        while (ring < STREAM_RING_MAX && lds_for(ring + 1u, act_offset) <= budget) ++ring;
+    }
+    ring = std::min(std::max(ring, STREAM_RING_MIN), STREAM_RING_MAX);
+    l.ring = ring;
+    l.lds = lds_for(ring, act_offset);
+    if (l.lds > STREAM_LDS_LIMIT) {
+        l.x_floats = 0;  // no staging: x too long
+        l.lds = lds_for(ring, act_offset);
+    }
+    l.act_offset = (uint32_t)act_offset;
+    if (l.lds > STREAM_LDS_LIMIT) return false;
+    // Workgroups resident at once (LDS allocated in 1 KB pieces), so that no
+    // workgroup waits for another to finish.
+    const uint32_t fit = (uint32_t)std::max<size_t>(1u, CU_LDS / ((l.lds + 1023u) & ~(size_t)1023u));
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    l.grid = (uint32_t)std::min<uint64_t>(total, (uint64_t)cus * std::min(wgs, fit));
+    starts.assign(l.grid, 0u);
+    uint32_t pi = 0;
+    for (uint32_t b = 0; b < l.grid; ++b) {
+        const uint64_t s = total * b / l.grid;
+        while (products[pi].first + products[pi].steps <= s) ++pi;
+        starts[b] = pi;
+    }
+    return true;
+}
+
+template <int KIND, bool HB>
+static hipError_t launch_stream_kind(const StreamLaunch& l, hipStream_t stream) {
+#define TMH_STREAM(RING)                                                                                     \
+    case RING:                                                                                               \
+        hipLaunchKernelGGL((k_matvec_stream<KIND, RING, HB>), dim3(l.grid), dim3(256), l.lds, stream, l.table, \
+                           l.starts, l.total, l.act_bytes, l.part_floats, l.x_floats, l.act_offset);          \
+        break;
+    switch (l.ring) {
+        TMH_STREAM(2) TMH_STREAM(3) TMH_STREAM(4) TMH_STREAM(5) TMH_STREAM(6) TMH_STREAM(7) TMH_STREAM(8)
+    default:
+        return hipErrorInvalidValue;
+    }
+#undef TMH_STREAM
+    return hipGetLastError();
+}
+
+hipError_t launch_stream(uint32_t kind, const StreamLaunch& l, hipStream_t stream) {
+    if (l.grid == 0) return hipSuccess;
+    switch (kind * 2u + l.has_bias) {
+    case 0: return launch_stream_kind<0, false>(l, stream);
+    case 1: return launch_stream_kind<0, true>(l, stream);
+    case 2: return launch_stream_kind<1, false>(l, stream);
+    case 3: return launch_stream_kind<1, true>(l, stream);
+    case 4: return launch_stream_kind<2, false>(l, stream);
+    default: return launch_stream_kind<2, true>(l, stream);
+    }
 }
 
 template <int KIND>

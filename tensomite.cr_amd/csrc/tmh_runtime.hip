@@ -730,15 +730,60 @@ int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset,
 
 namespace {
 
+// A plan runs the streamed kernel (`stream`, device memory `mem` holding its
+// product table and workgroup starts) or, where its products do not fit
+// that kernel, the tiled one-row kernel (`table`, then each tile's product
+// index in `owner`).
 struct Plan {
     int device;
     uint32_t kind;
     uint32_t count;
     uint32_t tiles;
     size_t act_bytes, part_bytes;
-    tmh::RowProduct* table;  // device memory: the products, then each tile's product index
+    tmh::RowProduct* table;
     uint32_t* owner;
+    bool streamed;
+    tmh::StreamLaunch stream;
+    void* mem;
 };
+
+// Builds the streamed form of a plan; false (nothing allocated) when the
+// products do not fit the streamed kernel or TMH_PLAN_KERNEL=rows asks for
+// the tiled one.
+int stream_plan(Plan* p, const std::vector<tmh::RowProduct>& rows, int compute_units, bool& made) {
+    made = false;
+    const char* env = getenv("TMH_PLAN_KERNEL");
+    if (env && std::string(env) == "rows") return TMH_SUCCESS;
+    std::vector<tmh::StreamProduct> products(rows.size());
+    for (size_t i = 0; i < rows.size(); ++i) {
+        tmh::StreamProduct& q = products[i];
+        q = tmh::StreamProduct{};
+        q.w = rows[i].w, q.x = rows[i].x, q.dst = rows[i].dst, q.bias = rows[i].bias;
+        q.n = rows[i].n, q.k = rows[i].k;
+    }
+    tmh::StreamLaunch l{};
+    std::vector<uint32_t> starts;
+    if (!tmh::plan_stream(p->kind, products, compute_units, l, starts)) return TMH_SUCCESS;
+    const size_t table_bytes = align256(sizeof(tmh::StreamProduct) * products.size());
+    void* mem = nullptr;
+    hipError_t e = device_malloc(&mem, table_bytes + sizeof(uint32_t) * starts.size());
+    if (e == hipSuccess)
+        e = hipMemcpy(mem, products.data(), sizeof(tmh::StreamProduct) * products.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy((uint8_t*)mem + table_bytes, starts.data(), sizeof(uint32_t) * starts.size(),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (mem) (void)hipFree(mem);
+        return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
+    }
+    l.table = (const tmh::StreamProduct*)mem;
+    l.starts = (const uint32_t*)((uint8_t*)mem + table_bytes);
+    p->stream = l;
+    p->mem = mem;
+    p->streamed = true;
+    made = true;
+    return TMH_SUCCESS;
+}
 
 }  // namespace
 
@@ -771,8 +816,23 @@ int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, 
         act_bytes = std::max(act_bytes, tmh::row_act_bytes(r));
         part_bytes = std::max(part_bytes, tmh::row_part_bytes(r));
     }
-    if (act_bytes + part_bytes > 64u * 1024u) return TMH_ERROR_SHAPE;
-    Plan* p = new Plan{d->index, kind, count, first, act_bytes, part_bytes, nullptr, nullptr};
+    Plan* p = new Plan{d->index, kind, count, first, act_bytes, part_bytes, nullptr, nullptr, false, {}, nullptr};
+    if (count) {
+        bool made = false;
+        const int r = stream_plan(p, rows, d->compute_units, made);
+        if (r != TMH_SUCCESS) {
+            delete p;
+            return r;
+        }
+        if (made) {
+            *plan = (uint64_t)p;
+            return TMH_SUCCESS;
+        }
+    }
+    if (act_bytes + part_bytes > 64u * 1024u) {
+        delete p;
+        return TMH_ERROR_SHAPE;
+    }
     if (count) {
         // One allocation: the product table, then the tile -> product map.
         std::vector<uint32_t> owner(first);
@@ -804,10 +864,24 @@ int tmh_plan_run(uint64_t plan) {
     if (!d) return err;
     Plan* p = (Plan*)plan;
     if (p->device != d->index) return TMH_ERROR_INVALID_VALUE;
-    hipError_t e = tmh::launch_rows(p->kind, p->table, p->owner, p->tiles, p->act_bytes, p->part_bytes,
-                                    d->compute_units, d->stream);
+    hipError_t e = p->streamed ? tmh::launch_stream(p->kind, p->stream, d->stream)
+                               : tmh::launch_rows(p->kind, p->table, p->owner, p->tiles, p->act_bytes,
+                                                  p->part_bytes, d->compute_units, d->stream);
     if (e == hipSuccess) d->gpu_ops.fetch_add(p->count);
     return code(e);
+}
+
+int tmh_plan_describe(uint64_t plan, char* text, uint32_t size) {
+    if (!plan || !text || size == 0) return TMH_ERROR_INVALID_VALUE;
+    const Plan* p = (const Plan*)plan;
+    if (p->streamed)
+        snprintf(text, size, "tmh::k_matvec_stream<%u, %u, %s> grid %u, LDS %zu B, %u steps of up to %u B",
+                 p->kind, p->stream.ring, p->stream.has_bias ? "true" : "false", p->stream.grid, p->stream.lds,
+                 p->stream.total, 8192u);
+    else
+        snprintf(text, size, "tmh::k_matvec_rows<%u> %u tiles, LDS %zu B", p->kind, p->tiles,
+                 p->act_bytes + p->part_bytes);
+    return TMH_SUCCESS;
 }
 
 int tmh_plan_destroy(uint64_t plan) {
@@ -817,6 +891,7 @@ int tmh_plan_destroy(uint64_t plan) {
     Device* d = current(&err);
     if (d) (void)hipStreamSynchronize(d->stream);
     if (p->table) (void)hipFree(p->table);
+    if (p->mem) (void)hipFree(p->mem);
     delete p;
     return TMH_SUCCESS;
 }

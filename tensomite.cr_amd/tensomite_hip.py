@@ -136,6 +136,7 @@ SIGNATURES = {
     "tmh_plan_create": (INT, [U32, ctypes.POINTER(Product), U32, ctypes.POINTER(U64)]),
     "tmh_plan_run": (INT, [U64]),
     "tmh_plan_destroy": (INT, [U64]),
+    "tmh_plan_describe": (INT, [U64, ctypes.c_char_p, U32]),
     "tmh_rmsnorm": (INT, [U64, U32, U64, U32, U32, F32, U64]),
     "tmh_rope_write": (INT, [U64, U32, U32, U32, U32, U32, U64, U64, U32, U64, U32, U32, U64, U64, U64]),
     "tmh_attention": (INT, [U64, U32, U32, U32, U64, U64, U32, U32, U32, U32, U64, F32, U64, U32]),
@@ -253,6 +254,12 @@ class Plan:
 
     def run(self) -> None:
         check("tmh_plan_run", self.device.lib.tmh_plan_run(self.handle))
+
+    def describe(self) -> str:
+        """The plan's launch: kernel, grid, LDS."""
+        text = ctypes.create_string_buffer(256)
+        check("tmh_plan_describe", self.device.lib.tmh_plan_describe(self.handle, text, len(text)))
+        return text.value.decode()
 
     def destroy(self) -> None:
         if self.handle:

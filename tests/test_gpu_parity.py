@@ -312,9 +312,13 @@ def test_errors_are_typed(dev):
     dev.sync()
 
 
+@pytest.mark.parametrize("kernel", ["stream", "rows"])
 @pytest.mark.parametrize("fmt", FORMATS)
-def test_plan_equals_products_one_by_one(dev, fmt):
-    # tmh_plan_*: many one-row products in one launch give each product's bits.
+def test_plan_equals_products_one_by_one(dev, fmt, kernel, monkeypatch):
+    # tmh_plan_*: many one-row products in one launch give each product's
+    # bits, in the streamed kernel (the default; x of k = 8192 too long to
+    # stage) and in the tiled one (TMH_PLAN_KERNEL=rows).
+    monkeypatch.setenv("TMH_PLAN_KERNEL", kernel)
     shapes = [(960, 576), (576, 576), (3072, 576), (576, 1536), (300, 2048), (7, 64), (2304, 768), (100, 8192),
               (1, 4096), (130, 128)]
     ws, xs, wants = [], [], []
@@ -336,6 +340,60 @@ def test_plan_equals_products_one_by_one(dev, fmt):
         got = dev.to_array(ys[i], np.float32, n)
         want = wants[i] + (np.arange(3072, dtype=np.float32)[:n] * 0.25 if i == 2 else 0)
         assert np.array_equal(bits(got), bits(want.astype(np.float32))), shapes[i]
+    plan.destroy()
+
+
+class View:
+    """A slice of a device buffer, as the plan API takes it (pointer, bytes)."""
+
+    def __init__(self, buffer, byte_offset, bytesize):
+        self.buffer = buffer  # keeps the allocation alive
+        self.pointer = buffer.pointer + byte_offset
+        self.bytesize = bytesize
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("wgs,ring", [("1", "2"), ("1", "5"), ("6", "2")])
+def test_stream_plan_many_small_products(dev, fmt, wgs, ring, monkeypatch):
+    # The streamed kernel where one workgroup's steps span many products (a
+    # third and later product quantised in turn), rows shorter than a step,
+    # biases on some products, x only 4-byte aligned for some, ragged last
+    # steps.
+    monkeypatch.setenv("TMH_PLAN_KERNEL", "stream")
+    monkeypatch.setenv("TMH_STREAM_WGS", wgs)
+    monkeypatch.setenv("TMH_STREAM_RING", ring)
+    rng = np.random.default_rng(900)
+    ks = [64, 128, 576, 192, 1536, 64, 256]
+    shapes = [(int(rng.integers(1, 300)), ks[i % len(ks)]) for i in range(700)]
+    xs = [acts(1, k, 2000 + i) for i, (_, k) in enumerate(shapes)]
+    offsets, packed = [], []
+    at = 0
+    for i, x in enumerate(xs):
+        at += 1 if i % 3 == 0 else 4  # every third x starts one float past 16 bytes
+        offsets.append(at)
+        at += len(x)
+    host = np.zeros(at + 4, np.float32)
+    for o, x in zip(offsets, xs):
+        host[o:o + len(x)] = x
+    xbuf = dev.from_array(host)
+    items, wants, ys = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        wq = weights(fmt, n, k, 1000 + i)
+        b = rng.uniform(-1, 1, n).astype(np.float32) if i % 4 == 1 else None
+        y = dev.alloc(4 * n)
+        ys.append(y)
+        items.append((dev.from_array(wq), 0, View(xbuf, 4 * offsets[i], 4 * k), y,
+                      dev.from_array(b) if b is not None else None, n, k))
+        want = oracle.matmul(fmt, xs[i], wq, 1, n, k)[0]
+        wants.append(want if b is None else oracle.add_bias(want[None, :], b)[0])
+    say("stream plan", fmt, wgs, ring, len(shapes))
+    plan = dev.plan(fmt, items)
+    for _ in range(2):
+        plan.run()
+    dev.sync()
+    for i, (n, k) in enumerate(shapes):
+        got = dev.to_array(ys[i], np.float32, n)
+        assert np.array_equal(bits(got), bits(wants[i])), (i, shapes[i])
     plan.destroy()
 
 
