@@ -86,14 +86,28 @@ struct StreamProduct {
     uint32_t step_bytes, unused[3];
 };
 
+// What one workgroup of the streamed kernel starts from, in one record so
+// that its first loads (x, the first step's weights) need one scalar round
+// trip: its steps s_begin ... s_end - 1, its first product, the x (and K) of
+// its first two products (x1 null when it has one), and the issue cursor at
+// its first step (weight address, the product's last 16-byte piece, bias or
+// a stand-in with has 0, steps left, bytes and rows per step, first row, n).
+struct StreamStart {
+    uint64_t src, wlast;
+    const float* bias;
+    const float* x0;
+    const float* x1;
+    uint32_t k0, k1, s_begin, s_end, first_pi, left, step_bytes, rows, row, n, has, unused;
+};
+
 // The shape of a streamed launch: the product table and each workgroup's
-// first product (device memory), steps in all, workgroups, ring slots,
+// start (device memory), steps in all, workgroups, ring slots,
 // whether any product has a bias, LDS of one activation buffer and of one
 // buffer of contributions (floats), floats of one staged x, the
 // activations' LDS offset, LDS in all.
 struct StreamLaunch {
     const StreamProduct* table;
-    const uint32_t* starts;
+    const StreamStart* starts;
     uint32_t total, grid, ring, has_bias, act_bytes, part_floats, x_floats, act_offset;
     size_t lds;
 };
@@ -103,7 +117,7 @@ struct StreamLaunch {
 // product. False when the products do not fit the kernel (rows of an odd
 // number of blocks, or LDS).
 bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& launch,
-                 std::vector<uint32_t>& starts);
+                 std::vector<StreamStart>& starts);
 
 // Launches the streamed one-row kernel (table and starts in device memory).
 hipError_t launch_stream(uint32_t kind, const StreamLaunch& launch, hipStream_t stream);

@@ -618,10 +618,11 @@ __global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_b
 // x · wᵀ for one activation row per product, for every product of a plan in
 // one launch. The plan's weight rows form one sequence of steps (a step is
 // the consecutive rows of one product that fit 8 KB, at most one pair of
-// blocks per thread); workgroup b takes steps [total·b/G, total·(b+1)/G),
-// an equal share whatever the products' sizes. Weights travel from HBM to
-// LDS by the direct loads of gfx950 (global_load_lds_dwordx4: 16 bytes a
-// lane, 1 KB a wave; each wave brings 2 KB of a step) into a ring of R
+// blocks per thread); workgroup b takes the steps from bound(b) to
+// bound(b + 1), a share set by the planner whatever the products' sizes.
+// Weights travel from HBM to LDS by the direct loads of gfx950
+// (global_load_lds_dwordx4: 16 bytes a lane, 1 KB a wave; each wave brings
+// 2 KB of a step) into a ring of R
 // slots, R - 1 steps ahead of the step being computed: no VGPR holds weights
 // in flight, and the ring runs on across product boundaries. One workgroup
 // barrier per step; before it each wave waits for its own loads of the step
@@ -785,7 +786,7 @@ __device__ __forceinline__ StreamLane stream_lane(const StreamProduct& P) {
 // on, over memory first written in the loop.
 template <int KIND, uint32_t R, bool HB>
 __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __restrict__ table,
-                                                       const uint32_t* __restrict__ starts, uint32_t total,
+                                                       const StreamStart* __restrict__ starts, uint32_t total,
                                                        uint32_t act_bytes, uint32_t part_floats, uint32_t x_floats,
                                                        uint32_t act_offset) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
@@ -793,8 +794,8 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t G = gridDim.x, b = blockIdx.x, t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t s_begin = (uint32_t)((uint64_t)total * b / G);
-    const uint32_t s_end = (uint32_t)((uint64_t)total * (b + 1u) / G);
+    const StreamStart st = starts[b];
+    const uint32_t s_begin = st.s_begin, s_end = st.s_end;
     if (s_begin >= s_end) return;
     const uint32_t count = s_end - s_begin;
     float* biases = (float*)smem;
@@ -804,26 +805,25 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     float* xs = (float*)(ring + (R - 1u) * STREAM_STEP);
     const uint32_t ring_lds = lds_address(ring) + wave * 2048u, bias_lds = lds_address(biases) + wave * 256u;
 
-    // The range's first two products are quantised before the loop.
-    const uint32_t first_pi = __builtin_amdgcn_readfirstlane(starts[b]);
-    const StreamProduct p0 = table[first_pi];
-    const bool two = p0.first + p0.steps < s_end;
-    const StreamProduct p1 = two ? table[first_pi + 1u] : p0;
+    // The range's first two products are quantised before the loop; their x
+    // and the first steps' weights are requested before the product table
+    // is read.
+    const uint32_t first_pi = st.first_pi;
+    const bool two = st.x1 != nullptr;
     const bool staged = x_floats != 0;
     if (staged) {
-        issue_x(p0.x, p0.k, lds_address(xs), wave);
-        if (two) issue_x(p1.x, p1.k, lds_address(xs) + x_floats * 4u, wave);
+        issue_x(st.x0, st.k0, lds_address(xs), wave);
+        if (two) issue_x(st.x1, st.k1, lds_address(xs) + x_floats * 4u, wave);
     }
 
     // The issue cursor: the step's first weight byte, steps left in its
-    // product, slots; with HB the step's first row and the product's bias.
+    // product, slots; with HB the step's first row and the product's bias
+    // (or a stand-in, with ihas 0).
     uint32_t ipi = first_pi;
-    uint64_t isrc = (uint64_t)p0.w + (uint64_t)(s_begin - p0.first) * p0.step_bytes;
-    uint64_t iwlast = p0.wlast;
-    uint32_t ileft = p0.steps - (s_begin - p0.first), istep = p0.step_bytes, irows = p0.rows;
-    uint32_t irow = (s_begin - p0.first) * p0.rows, in = p0.n;
-    const float* ibias = p0.bias ? p0.bias : p0.x;  // without a bias, x[0] (never used)
-    uint32_t ihas = p0.bias ? 1u : 0u;
+    uint64_t isrc = st.src, iwlast = st.wlast;
+    uint32_t ileft = st.left, istep = st.step_bytes, irows = st.rows, irow = st.row, in = st.n;
+    const float* ibias = st.bias;
+    uint32_t ihas = st.has;
     uint32_t islot = 0, ibslot = 0, issued = 0;
     const uint32_t lane_bytes = wave * 2048u + lane * 16u;
     auto issue_next = [&]() {
@@ -855,6 +855,8 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     // waits for the prologue's weights too.
     const uint32_t prologue = min(R - 1u, count);
     for (uint32_t s = 0; s < prologue; ++s) issue_next();
+    const StreamProduct p0 = table[first_pi];
+    const StreamProduct p1 = two ? table[first_pi + 1u] : p0;
     if (staged) {
         step_barrier_ahead<PS, R - 1u>(prologue);  // the staged x is complete
         quantise_lds<KIND>(acts, xs, p0.k);
@@ -1462,11 +1464,11 @@ static uint32_t env_u32(const char* name, uint32_t fallback) {
     return v > 0 ? (uint32_t)v : fallback;
 }
 
-static constexpr uint32_t STREAM_RING_MIN = 2, STREAM_RING_MAX = 8, STREAM_WGS = 6;
+static constexpr uint32_t STREAM_RING_MIN = 2, STREAM_RING_MAX = 8, STREAM_WGS = 6, STREAM_RAMP_PERCENT = 20;
 static constexpr size_t STREAM_LDS_LIMIT = 64u * 1024u, CU_LDS = 160u * 1024u;
 
 bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& l,
-                 std::vector<uint32_t>& starts) {
+                 std::vector<StreamStart>& starts) {
     const uint32_t bb = block_bytes(kind);
     uint64_t total = 0;
     uint32_t max_k = 0, part = 0;
@@ -1531,12 +1533,36 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
     const uint32_t fit = (uint32_t)std::max<size_t>(1u, CU_LDS / ((l.lds + 1023u) & ~(size_t)1023u));
     const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
     l.grid = (uint32_t)std::min<uint64_t>(total, (uint64_t)cus * std::min(wgs, fit));
-    starts.assign(l.grid, 0u);
+    // Workgroup b's steps start at bound(b): shares that shrink linearly
+    // from the first workgroup to the last, by `ramp` at either end. Later
+    // workgroups are dispatched later and their first activations arrive
+    // later, behind the earlier ones' weight loads (measured: the loop
+    // starts ≈1.6 us after launch for the first workgroups, ≈4.3 us for the
+    // last, and then runs at the same rate), so equal shares end unevenly.
+
+    const char* ramp_env = getenv("TMH_STREAM_RAMP");  // percent, for tuning
+    const double ramp = ramp_env ? atof(ramp_env) : (double)STREAM_RAMP_PERCENT;
+    const double a = ramp / 100.0, G = (double)l.grid;
+    auto bound = [&](uint32_t b) -> uint64_t {
+        if (b >= l.grid) return total;
+        const double w = b * (1.0 + a * (1.0 - b / G)) / G;  // cumulative share, 0 ... 1
+        return std::min<uint64_t>(total, (uint64_t)(w * (double)total));
+    };
+    starts.assign(l.grid, StreamStart{});
     uint32_t pi = 0;
     for (uint32_t b = 0; b < l.grid; ++b) {
-        const uint64_t s = total * b / l.grid;
-        while (products[pi].first + products[pi].steps <= s) ++pi;
-        starts[b] = pi;
+        const uint64_t s = bound(b), e = bound(b + 1u);
+        while (pi + 1u < products.size() && products[pi].first + products[pi].steps <= s) ++pi;
+        StreamStart& st = starts[b];
+        const StreamProduct& p = products[pi];
+        const uint32_t sp = (uint32_t)s - p.first;
+        st.s_begin = (uint32_t)s, st.s_end = (uint32_t)e, st.first_pi = pi;
+        st.src = (uint64_t)(uintptr_t)p.w + (uint64_t)sp * p.step_bytes, st.wlast = p.wlast;
+        st.bias = p.bias ? p.bias : p.x, st.has = p.bias ? 1u : 0u;
+        st.x0 = p.x, st.k0 = p.k;
+        const bool two = e > s && (uint64_t)p.first + p.steps < e;
+        st.x1 = two ? products[pi + 1u].x : nullptr, st.k1 = two ? products[pi + 1u].k : 0u;
+        st.left = p.steps - sp, st.step_bytes = p.step_bytes, st.rows = p.rows, st.row = sp * p.rows, st.n = p.n;
     }
     return true;
 }

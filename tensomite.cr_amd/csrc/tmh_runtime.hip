@@ -762,22 +762,22 @@ int stream_plan(Plan* p, const std::vector<tmh::RowProduct>& rows, int compute_u
         q.n = rows[i].n, q.k = rows[i].k;
     }
     tmh::StreamLaunch l{};
-    std::vector<uint32_t> starts;
+    std::vector<tmh::StreamStart> starts;
     if (!tmh::plan_stream(p->kind, products, compute_units, l, starts)) return TMH_SUCCESS;
     const size_t table_bytes = align256(sizeof(tmh::StreamProduct) * products.size());
     void* mem = nullptr;
-    hipError_t e = device_malloc(&mem, table_bytes + sizeof(uint32_t) * starts.size());
+    hipError_t e = device_malloc(&mem, table_bytes + sizeof(tmh::StreamStart) * starts.size());
     if (e == hipSuccess)
         e = hipMemcpy(mem, products.data(), sizeof(tmh::StreamProduct) * products.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = hipMemcpy((uint8_t*)mem + table_bytes, starts.data(), sizeof(uint32_t) * starts.size(),
+        e = hipMemcpy((uint8_t*)mem + table_bytes, starts.data(), sizeof(tmh::StreamStart) * starts.size(),
                       hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         if (mem) (void)hipFree(mem);
         return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
     }
     l.table = (const tmh::StreamProduct*)mem;
-    l.starts = (const uint32_t*)((uint8_t*)mem + table_bytes);
+    l.starts = (const tmh::StreamStart*)((uint8_t*)mem + table_bytes);
     p->stream = l;
     p->mem = mem;
     p->streamed = true;
