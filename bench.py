@@ -124,7 +124,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
-    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-eager", action="store_true",
                     help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
     args = ap.parse_args()
