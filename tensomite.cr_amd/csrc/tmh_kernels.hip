@@ -638,43 +638,6 @@ __global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_b
 
 constexpr uint32_t STREAM_STEP = 8192;  // bytes of weights a step's loads bring
 
-typedef __attribute__((address_space(3))) uint8_t lds_byte;
-
-// The LDS byte address of p (a pointer into shared memory), uniform.
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_byte*)p);
-}
-
-// Direct loads from global memory into LDS: each lane's 16 (or 4) bytes at
-// `from` land at LDS byte lds + 16·lane (4·lane). Written as inline asm so
-// that the compiler does not see the LDS write: it would otherwise wait for
-// every load in flight before any LDS access it cannot prove disjoint,
-// which would end the streaming; the kernels order these writes themselves
-// (counted waits and barriers). M0 carries the LDS address (an operand, so
-// the compiler writes it); s_nop covers the wait state an M0 write needs
-// before an LDS direct load.
-__device__ __forceinline__ void lds_load16(const void* from, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(from), "{m0}"(lds) : "memory");
-}
-
-// lds_load16 marked non-temporal: weights stream through the caches once,
-// so they should not displace what is read again (activations, tables).
-__device__ __forceinline__ void lds_load16_nt(const void* from, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(from), "{m0}"(lds) : "memory");
-}
-
-__device__ __forceinline__ void lds_load4(const void* from, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(from), "{m0}"(lds) : "memory");
-}
-
-// s_waitcnt: at most N vector memory operations of this wave outstanding,
-// every LDS and scalar memory operation done.
-template <uint32_t N>
-__device__ __forceinline__ void wait_vm_lds() {
-    static_assert(N < 64, "vmcnt holds 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (7 << 4));
-}
-
 // The per-step workgroup barrier, after this wave's operations are done as
 // wait_vm_lds<N> says. The empty asm statements keep the compiler from
 // moving memory operations across it (s_barrier alone does not order memory
