@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tmh_internal.h"
+
 namespace tmh {
 
 // ------------------------------------------------------------------ halves
@@ -93,6 +95,145 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
     out.scale = round_to_half(d);
     out.sum = round_to_half((float)total * d);
     return out;
+}
+
+// ------------------------------------------------------------ ordered sums
+
+// Σ v[0..n) in index order from 0.0f, read from LDS by broadcast (every lane
+// computes the same sum). The adds form one dependent chain, the only
+// instructions on it; the reads of the next 32 values are issued before
+// the adds of the current 32, from two register buffers used in turn.
+__device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s += b[i].x;
+        s += b[i].y;
+        s += b[i].z;
+        s += b[i].w;
+    }
+}
+
+__device__ __forceinline__ void read32(float4 (&b)[8], const float4* v4, uint32_t j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = v4[j + i];
+}
+
+__device__ __forceinline__ float ordered_sum(const float* v, uint32_t n) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    const uint32_t n4 = n >> 2;
+    float s = 0.0f;
+    uint32_t j = 0;
+    if (n4 >= 16) {
+        float4 a[8], b[8];
+        read32(a, v4, 0);
+        for (j = 0; j + 32 <= n4; j += 16) {
+            read32(b, v4, j + 8);
+            add32(s, a);
+            read32(a, v4, j + 16);
+            add32(s, b);
+        }
+        // a holds [j, j + 8); [j + 8, n4) remain
+        if (j + 16 <= n4) {
+            read32(b, v4, j + 8);
+            add32(s, a);
+            add32(s, b);
+            j += 16;
+        } else {
+            add32(s, a);
+            j += 8;
+        }
+    }
+    for (; j < n4; ++j) {
+        const float4 c = v4[j];
+        s += c.x;
+        s += c.y;
+        s += c.z;
+        s += c.w;
+    }
+    for (uint32_t i = n4 << 2; i < n; ++i) s += v[i];
+    return s;
+}
+
+// ordered_sum by one lane (an LDS read then feeds one lane, not 256), the
+// result shared through LDS. Every thread calls it.
+__device__ __forceinline__ float shared_sum(const float* v, uint32_t n) {
+    __shared__ float result;
+    if (threadIdx.x == 0) result = ordered_sum(v, n);
+    __syncthreads();
+    return result;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+
+// Largest row the LDS kernels stage: the row and its squares, 64 KB.
+constexpr uint32_t RMSNORM_LDS_ROW = 8192;
+
+// Stages row x (n values) and its squares in LDS, then returns the root
+// sqrt(Σx²/n + eps), the squares folded in index order by every wave.
+__device__ __forceinline__ float stage_root(const float* __restrict__ xr, uint32_t n, float eps, float* row,
+                                            float* sq) {
+    // four loads in flight per thread before any store
+    for (uint32_t j0 = threadIdx.x; j0 < n; j0 += 1024u) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = j0 + 256u * u;
+            v[u] = j < n ? xr[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = j0 + 256u * u;
+            if (j < n) {
+                row[j] = v[u];
+                sq[j] = v[u] * v[u];
+            }
+        }
+    }
+    __syncthreads();
+    const float squares = shared_sum(sq, n);
+    return __builtin_sqrtf(squares / (float)n + eps);
+}
+
+// RMSNorm of row xr (n values, a multiple of 32, at most RMSNORM_LDS_ROW)
+// then the activation quantiser, by one workgroup: each 8-lane group
+// normalises 4 values a lane of a block of 32 and quantises the block
+// (quantize_activations, quant.cr:428-442, on the normalised row) into
+// `act` row r, laid out as the quantise pass lays it out. row and sq are
+// LDS of n floats each. Every thread calls it.
+__device__ __forceinline__ void rmsnorm_quantise_row(const float* __restrict__ xr, uint32_t n,
+                                                     const float* __restrict__ w, float eps, Activations act,
+                                                     uint32_t r, float* row, float* sq) {
+    const uint32_t nb = n >> 5, sub = threadIdx.x & 7u;
+    // this lane's weights, loaded before the fold (n ≤ 8192: at most 8 passes)
+    float4 wv[RMSNORM_LDS_ROW / 1024];
+#pragma unroll
+    for (uint32_t pass = 0; pass < RMSNORM_LDS_ROW / 1024; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        wv[pass] = (w && blk < nb) ? *reinterpret_cast<const float4*>(w + blk * 32u + sub * 4u)
+                                   : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    const float root = stage_root(xr, n, eps, row, sq);
+#pragma unroll
+    for (uint32_t pass = 0; pass < RMSNORM_LDS_ROW / 1024; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        if (blk >= nb) break;
+        const uint32_t j = blk * 32u + sub * 4u;
+        const float wj[4] = {wv[pass].x, wv[pass].y, wv[pass].z, wv[pass].w};
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q = row[j + i] / root;
+            v[i] = w ? q * wj[i] : q;
+        }
+        const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+        *(uint32_t*)((int8_t*)act.qs + (size_t)r * n + j) = q.packed;
+        if (sub == 0) {
+            const size_t g = (size_t)r * nb + blk;
+            ((float*)act.scales)[g] = q.scale;
+            ((float*)act.sums)[g] = q.sum;
+            ((int32_t*)act.totals)[g] = q.total;
+        }
+    }
 }
 
 // ------------------------------------------------- LDS direct loads (gfx950)

@@ -272,17 +272,16 @@ __device__ __forceinline__ void load_activations(const Activations& act, uint32_
 // the contributions of output o (and o + 256, ...) one by one in block order
 // -- the host's order -- and writes it, plus the bias.
 template <int KIND, int NB>
-__global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, Activations act,
-                                                float* __restrict__ dst, const float* __restrict__ bias, uint32_t n,
-                                                uint32_t k, uint32_t tr, uint32_t stride) {
-    extern __shared__ float part[];
+__device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst,
+                                            const float* __restrict__ bias, uint32_t n, uint32_t k, uint32_t tr,
+                                            uint32_t stride, uint32_t tile, float* part) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
     const uint32_t np = nb >> 1;
     const uint32_t rpi = 256u / np;
     const uint32_t j = t % np, rsub = t / np;
-    const uint32_t row0 = blockIdx.x * tr;
+    const uint32_t row0 = tile * tr;
     const uint32_t steps = tr / rpi;
     const size_t row_words = (size_t)np * PW;
     const uint32_t* wp = (const uint32_t*)w;
@@ -334,6 +333,15 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, A
         }
     }
 }
+
+template <int KIND, int NB>
+__global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, Activations act,
+                                                float* __restrict__ dst, const float* __restrict__ bias, uint32_t n,
+                                                uint32_t k, uint32_t tr, uint32_t stride) {
+    extern __shared__ float part[];
+    matvec_tile<KIND, NB>(w, act, dst, bias, n, k, tr, stride, blockIdx.x, part);
+}
+
 
 // ------------------------------------------- lanes, one row, fused quantise
 
