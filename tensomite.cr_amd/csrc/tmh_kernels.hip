@@ -717,18 +717,33 @@ __device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint
     }
 }
 
-// The sum of a row's nb contributions c[0 ... nb-1] in block order, from 0.
+// The sum of a row's nb contributions c[0 ... nb-1] (nb even, the same in
+// every lane) in block order, from 0. Each batch of 16 is read with all its
+// LDS reads issued before the first add, so a batch costs one LDS round
+// trip rather than one per four values (the fold is on every step's
+// critical path); the last batch reads up to 14 floats past c[nb-1], other
+// LDS data of the workgroup, and skips them.
 __device__ __forceinline__ float fold_row(const float* c, uint32_t nb) {
     float sum = 0.0f;
-    uint32_t q = 0;
-    for (; q + 4 <= nb; q += 4) {
-        const float4 e = *(const float4*)(c + q);
-        sum += e.x;
-        sum += e.y;
-        sum += e.z;
-        sum += e.w;
+    for (uint32_t q = 0; q < nb; q += 16u) {
+        float4 e[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) e[u] = *(const float4*)(c + q + 4u * u);
+        // Every read is needed here: the compiler may not sink them into the
+        // branches below (one round trip each).
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) asm volatile("" : "+v"(e[u].x), "+v"(e[u].y), "+v"(e[u].z), "+v"(e[u].w));
+        const uint32_t left = nb - q;
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) {
+            if (4u * u >= left) break;
+            sum += e[u].x;
+            sum += e[u].y;
+            if (4u * u + 2u >= left) break;
+            sum += e[u].z;
+            sum += e[u].w;
+        }
     }
-    for (; q < nb; ++q) sum += c[q];
     return sum;
 }
 
