@@ -239,16 +239,30 @@ int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset,
 
 /* ------------------------------------------------------------ plans */
 
+/* How a plan product's activation row arrives (tmh_product.x_mode). */
+enum {
+    TMH_X_F32 = 0,       /* x: f32 [k], quantised by the launch as tmh_block_matmul does */
+    TMH_X_RMSNORM = 1,   /* x: f32 [k], taken through Op::RMSNorm (host.cr:374-386) with
+                          * weights `norm` [k] and `eps` first: one launch for what
+                          * tmh_rmsnorm then the product would do, with the same bits */
+    TMH_X_QUANTISED = 2  /* x: int8 [k] values of tmh_quantize_rows_q8 (one row), with
+                          * its scales, sums and totals: as tmh_block_matmul_quantised */
+};
+
 /* One product of a plan: Op::BlockMatMul with ONE activation row,
  * dst[n] = x[k] · w[n, k]ᵀ (+ bias[n]). */
 typedef struct tmh_product {
     uint64_t w;             /* weight buffer */
     uint64_t w_byte_offset; /* byte offset of the first row (a row slice) */
-    uint64_t x;             /* f32 [k] */
+    uint64_t x;             /* the activation row, as x_mode says */
     uint64_t dst;           /* f32 [n] */
     uint64_t bias;          /* f32 [n], or 0 */
     uint32_t n;
     uint32_t k;
+    uint32_t x_mode;        /* TMH_X_F32 (0), TMH_X_RMSNORM or TMH_X_QUANTISED */
+    float eps;              /* TMH_X_RMSNORM */
+    uint64_t norm;          /* TMH_X_RMSNORM: f32 [k] */
+    uint64_t scales, sums, totals; /* TMH_X_QUANTISED: f32 [k/32], f32 [k/32], i32 [k/32] */
 } tmh_product;
 
 /* Records `count` independent products of one block kind to run as ONE
@@ -259,6 +273,8 @@ typedef struct tmh_product {
  * than at the launch rate. Rows must hold an even number of blocks and start
  * 4-byte aligned (TMH_ERROR_SHAPE otherwise). */
 int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, uint64_t* plan);
+/* Products with x_mode other than TMH_X_F32 need the streamed kernel (rows of
+ * at most 512 blocks and LDS for their staging); TMH_ERROR_SHAPE otherwise. */
 
 /* Queues the plan's launch on the device's stream. */
 int tmh_plan_run(uint64_t plan);

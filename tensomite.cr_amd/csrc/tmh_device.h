@@ -99,13 +99,15 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
 
 // ------------------------------------------------------------ ordered sums
 
-// Σ v[0..n) in index order from 0.0f, read from LDS by broadcast (every lane
-// computes the same sum). The adds form one dependent chain, the only
-// instructions on it; the reads of the next 32 values are issued before
-// the adds of the current 32, from two register buffers used in turn.
-__device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
+// Σ v[0..n) in index order from 0.0f (with SQ, Σ v[i]·v[i], each square
+// rounded before its add), read by broadcast (every lane computes the same
+// sum; from LDS, or global memory). The adds form one dependent chain, the
+// only instructions on it; the reads of the next 32 values are issued
+// before the adds of the current 32, from two register buffers used in turn.
+template <int B = 8>
+__device__ __forceinline__ void add32(float& s, const float4 (&b)[B]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < B; ++i) {
         s += b[i].x;
         s += b[i].y;
         s += b[i].z;
@@ -113,44 +115,51 @@ __device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
     }
 }
 
-__device__ __forceinline__ void read32(float4 (&b)[8], const float4* v4, uint32_t j) {
+template <bool SQ = false, int B = 8>
+__device__ __forceinline__ void read32(float4 (&b)[B], const float4* v4, uint32_t j) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = v4[j + i];
+    for (int i = 0; i < B; ++i) {
+        b[i] = v4[j + i];
+        if constexpr (SQ) b[i] = make_float4(b[i].x * b[i].x, b[i].y * b[i].y, b[i].z * b[i].z, b[i].w * b[i].w);
+    }
 }
 
+// B: float4s per register buffer (8: 32 values; 4 where registers are short).
+template <bool SQ = false, int B = 8>
 __device__ __forceinline__ float ordered_sum(const float* v, uint32_t n) {
     const float4* v4 = reinterpret_cast<const float4*>(v);
     const uint32_t n4 = n >> 2;
     float s = 0.0f;
     uint32_t j = 0;
-    if (n4 >= 16) {
-        float4 a[8], b[8];
-        read32(a, v4, 0);
-        for (j = 0; j + 32 <= n4; j += 16) {
-            read32(b, v4, j + 8);
-            add32(s, a);
-            read32(a, v4, j + 16);
-            add32(s, b);
+    if (n4 >= 2u * B) {
+        float4 a[B], b[B];
+        read32<SQ, B>(a, v4, 0);
+        for (j = 0; j + 4u * B <= n4; j += 2u * B) {
+            read32<SQ, B>(b, v4, j + B);
+            add32<B>(s, a);
+            read32<SQ, B>(a, v4, j + 2u * B);
+            add32<B>(s, b);
         }
-        // a holds [j, j + 8); [j + 8, n4) remain
-        if (j + 16 <= n4) {
-            read32(b, v4, j + 8);
-            add32(s, a);
-            add32(s, b);
-            j += 16;
+        // a holds [j, j + B); [j + B, n4) remain
+        if (j + 2u * B <= n4) {
+            read32<SQ, B>(b, v4, j + B);
+            add32<B>(s, a);
+            add32<B>(s, b);
+            j += 2u * B;
         } else {
-            add32(s, a);
-            j += 8;
+            add32<B>(s, a);
+            j += B;
         }
     }
     for (; j < n4; ++j) {
-        const float4 c = v4[j];
+        float4 c = v4[j];
+        if constexpr (SQ) c = make_float4(c.x * c.x, c.y * c.y, c.z * c.z, c.w * c.w);
         s += c.x;
         s += c.y;
         s += c.z;
         s += c.w;
     }
-    for (uint32_t i = n4 << 2; i < n; ++i) s += v[i];
+    for (uint32_t i = n4 << 2; i < n; ++i) s += SQ ? v[i] * v[i] : v[i];
     return s;
 }
 

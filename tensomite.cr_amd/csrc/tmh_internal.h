@@ -75,6 +75,13 @@ hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* o
 // consecutive weight rows (the last may hold fewer), step_bytes apart;
 // pairs per row np, bytes per row, LDS floats between two rows'
 // contributions.
+// How a streamed product's activation row arrives: f32 x, quantised by the
+// kernel; f32 x under an RMSNorm (x / sqrt(Σx²/k + eps) · norm, the host's
+// order) then quantised; or already quantised by the quantise pass (its
+// int8 values at x, scales at aux0, and at aux1 the block extras the kind
+// reads: Q4_0 totals, Q4_1 sums).
+constexpr uint32_t STREAM_X_F32 = 0, STREAM_X_RMSNORM = 1, STREAM_X_QUANTISED = 2;
+
 struct StreamProduct {
     const uint8_t* w;
     const float* x;
@@ -83,21 +90,29 @@ struct StreamProduct {
     uint64_t wlast;
     uint32_t n, k, first, steps;
     uint32_t np, rows, row_bytes, stride;
-    uint32_t step_bytes, unused[3];
+    uint32_t step_bytes, mode;
+    float eps;
+    uint32_t unused;
+    const float* aux0;  // STREAM_X_RMSNORM: the norm's weights; STREAM_X_QUANTISED: scales
+    const void* aux1;   // STREAM_X_QUANTISED: totals (Q4_0) or sums (Q4_1)
 };
 
 // What one workgroup of the streamed kernel starts from, in one record so
-// that its first loads (x, the first step's weights) need one scalar round
-// trip: its steps s_begin ... s_end - 1, its first product, the x (and K) of
-// its first two products (x1 null when it has one), and the issue cursor at
-// its first step (weight address, the product's last 16-byte piece, bias or
-// a stand-in with has 0, steps left, bytes and rows per step, first row, n).
+// that its first loads (its first product's activation row, the first
+// step's weights) need one scalar round trip: its steps s_begin ... s_end - 1,
+// its first product, that product's input mode and arrays (x0, a0, a1, K in
+// k0), the x and K of its second product when both take f32 x (x1 null
+// otherwise: a later product is prepared in the loop), and the issue cursor
+// at its first step (weight address, the product's last 16-byte piece, bias
+// or a stand-in with has 0, steps left, bytes and rows per step, first row, n).
 struct StreamStart {
     uint64_t src, wlast;
     const float* bias;
     const float* x0;
     const float* x1;
-    uint32_t k0, k1, s_begin, s_end, first_pi, left, step_bytes, rows, row, n, has, unused;
+    const float* a0;
+    const void* a1;
+    uint32_t k0, k1, s_begin, s_end, first_pi, left, step_bytes, rows, row, n, has, mode0;
 };
 
 // The shape of a streamed launch: the product table and each workgroup's

@@ -497,17 +497,25 @@ __device__ __forceinline__ void load_x(const float* __restrict__ x, uint32_t k, 
     }
 }
 
+// The RMSNorm of four values: x / root · w, the host's order.
+__device__ __forceinline__ float4 normalise4(float4 v, float root, float4 w) {
+    return make_float4(v.x / root * w.x, v.y / root * w.y, v.z / root * w.z, v.w / root * w.w);
+}
+
 // Quantises activation row x (k values) into LDS at act; the first XP
-// passes come from xv. The caller synchronises before reading it.
+// passes come from xv. With norm, the row quantised is x / root · norm
+// (an RMSNorm whose root the caller has). The caller synchronises before
+// reading it.
 template <int KIND>
 __device__ __forceinline__ void quantise_into(uint8_t* act, const float* __restrict__ x, uint32_t k,
-                                              const float4 (&xv)[XP]) {
+                                              const float4 (&xv)[XP], float root = 1.0f,
+                                              const float* __restrict__ norm = nullptr) {
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
     int8_t* lqs = (int8_t*)act;
     float* lsc = (float*)(act + k);
     int32_t* lex = (int32_t*)(lsc + nb);
-    const bool vec = ((uintptr_t)x & 15u) == 0;
+    const bool vec = ((uintptr_t)x & 15u) == 0, wvec = ((uintptr_t)norm & 15u) == 0;
     for (uint32_t pass = 0; pass * 32u < nb; ++pass) {
         const uint32_t g = pass * 32u + (t >> 3), sub = t & 7u;
         if (g < nb) {
@@ -517,6 +525,7 @@ __device__ __forceinline__ void quantise_into(uint8_t* act, const float* __restr
             } else {
                 v = load_f4(x + g * 32u + sub * 4u, vec);
             }
+            if (norm) v = normalise4(v, root, load_f4(norm + g * 32u + sub * 4u, wvec));
             const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
             *(uint32_t*)(lqs + g * 32u + sub * 4u) = q.packed;
             if (sub == 0) {
@@ -658,6 +667,10 @@ __device__ __forceinline__ void step_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// A workgroup barrier after this wave's LDS operations only; its direct
+// loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() { step_barrier<63>(); }
+
 // step_barrier<A·PS> for a runtime A in [0, AMAX]: the steps issued after the
 // one about to be computed, PS operations each.
 template <uint32_t PS, uint32_t AMAX>
@@ -695,9 +708,11 @@ __device__ __forceinline__ void issue_x(const float* x, uint32_t k, uint32_t to,
     }
 }
 
-// quantise_into with x read from LDS (xs, k floats).
+// quantise_into with x read from LDS (xs, k floats), and the norm's
+// weights too (ws, or none).
 template <int KIND>
-__device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint32_t k) {
+__device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint32_t k, float root = 1.0f,
+                                             const float* ws = nullptr) {
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
     int8_t* lqs = (int8_t*)act;
@@ -706,7 +721,8 @@ __device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint
     for (uint32_t pass = 0; pass * 32u < nb; ++pass) {
         const uint32_t g = pass * 32u + (t >> 3), sub = t & 7u;
         if (g < nb) {
-            const float4 v = *(const float4*)(xs + g * 32u + sub * 4u);
+            float4 v = *(const float4*)(xs + g * 32u + sub * 4u);
+            if (ws) v = normalise4(v, root, *(const float4*)(ws + g * 32u + sub * 4u));
             const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
             *(uint32_t*)(lqs + g * 32u + sub * 4u) = q.packed;
             if (sub == 0) {
@@ -715,6 +731,68 @@ __device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint
             }
         }
     }
+}
+
+// Bytes of a staged part of a quantised activation row: whole 1 KB direct loads.
+__host__ __device__ constexpr uint32_t stage_part(uint32_t bytes) { return (bytes + 1023u) & ~1023u; }
+
+// A product's activations quantised beforehand (int8 values, scales, block
+// extras), staged at st as three parts of stage_part() bytes, into LDS at
+// act in the layout quantise_into writes (for Q4_0, -8 · total).
+template <int KIND>
+__device__ __forceinline__ void unpack_lds(uint8_t* act, const uint8_t* st, uint32_t k) {
+    const uint32_t t = threadIdx.x, nb = k >> 5;
+    const uint32_t qb = stage_part(k), sb = stage_part(4u * nb);
+    for (uint32_t i = t; i < k / 4u; i += 256u) ((uint32_t*)act)[i] = ((const uint32_t*)st)[i];
+    float* lsc = (float*)(act + k);
+    int32_t* lex = (int32_t*)(lsc + nb);
+    const float* ssc = (const float*)(st + qb);
+    const int32_t* sex = (const int32_t*)(st + qb + sb);
+    for (uint32_t g = t; g < nb; g += 256u) {
+        lsc[g] = ssc[g];
+        lex[g] = KIND == 1 ? -8 * sex[g] : KIND == 2 ? sex[g] : 0;
+    }
+}
+
+// A product's activations into LDS at act from global memory, whatever its
+// input mode (for products not staged before the loop). free is LDS that
+// nothing else uses (one float, for the RMSNorm's root). Every thread calls
+// it; the caller synchronises before reading act.
+template <int KIND>
+__device__ __forceinline__ void prepare_global(uint8_t* act, const StreamProduct& q, float* free) {
+    const uint32_t t = threadIdx.x, k = q.k, nb = k >> 5;
+    if (q.mode == STREAM_X_QUANTISED) {
+        const uint32_t* qs = (const uint32_t*)q.x;
+        const float* sc = q.aux0;
+        const int32_t* ex = (const int32_t*)q.aux1;
+        for (uint32_t i = t; i < k / 4u; i += 256u) ((uint32_t*)act)[i] = qs[i];
+        float* lsc = (float*)(act + k);
+        int32_t* lex = (int32_t*)(lsc + nb);
+        for (uint32_t g = t; g < nb; g += 256u) {
+            lsc[g] = sc[g];
+            lex[g] = KIND == 1 ? -8 * ex[g] : KIND == 2 ? ex[g] : 0;
+        }
+        return;
+    }
+    float root = 1.0f;
+    const float* norm = nullptr;
+    if (q.mode == STREAM_X_RMSNORM) {
+        if (t == 0) {
+            float squares = 0.0f;
+            if (((uintptr_t)q.x & 15u) == 0) {
+                squares = ordered_sum<true, 4>(q.x, k);
+            } else {
+                for (uint32_t i = 0; i < k; ++i) squares += q.x[i] * q.x[i];
+            }
+            free[0] = __builtin_sqrtf(squares / (float)k + q.eps);
+        }
+        step_barrier<0>();
+        root = free[0];
+        norm = q.aux0;
+    }
+    float4 xv[XP];
+    load_x(q.x, k, xv);
+    quantise_into<KIND>(act, q.x, k, xv, root, norm);
 }
 
 // The sum of a row's nb contributions c[0 ... nb-1] (nb even, the same in
@@ -767,7 +845,7 @@ __device__ __forceinline__ StreamLane stream_lane(const StreamProduct& P) {
 // LDS layout of the streamed kernel: biases (R + 1 slots of 256 floats, with
 // HB), ring slots 0 ... R-1 of STREAM_STEP bytes, contributions (two buffers
 // of part_floats), then from act_offset the activations (two buffers of
-// act_bytes). Before the loop, the x of the range's first two products
+// act_bytes) and 16 bytes for an RMSNorm's root. Before the loop, the x of the range's first two products
 // (x_floats apart; none when x_floats is 0) is staged from ring slot R-1
 // on, over memory first written in the loop.
 template <int KIND, uint32_t R, bool HB>
@@ -788,18 +866,32 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     uint8_t* ring = smem + (HB ? (R + 1u) * 1024u : 0u);
     float* parts = (float*)(ring + R * STREAM_STEP);
     uint8_t* acts = smem + act_offset;
+    float* root_slot = (float*)(acts + 2u * act_bytes);  // an RMSNorm's root, shared
     float* xs = (float*)(ring + (R - 1u) * STREAM_STEP);
     const uint32_t ring_lds = lds_address(ring) + wave * 2048u, bias_lds = lds_address(biases) + wave * 256u;
 
-    // The range's first two products are quantised before the loop; their x
-    // and the first steps' weights are requested before the product table
-    // is read.
-    const uint32_t first_pi = st.first_pi;
+    // The range's first product (and its second, when both take f32 x) is
+    // prepared before the loop, from its activation row brought into LDS by
+    // direct loads requested, with the first steps' weights, before the
+    // product table is read: x (and the norm's weights in the second slot),
+    // or the three parts of a quantised row.
+    const uint32_t first_pi = st.first_pi, mode0 = st.mode0;
     const bool two = st.x1 != nullptr;
     const bool staged = x_floats != 0;
     if (staged) {
-        issue_x(st.x0, st.k0, lds_address(xs), wave);
-        if (two) issue_x(st.x1, st.k1, lds_address(xs) + x_floats * 4u, wave);
+        const uint32_t to = lds_address(xs);
+        if (mode0 == STREAM_X_QUANTISED) {
+            const uint32_t qb = stage_part(st.k0);
+            issue_x(st.x0, st.k0 / 4u, to, wave);
+            issue_x(st.a0, st.k0 / 32u, to + qb, wave);
+            if (st.a1) issue_x((const float*)st.a1, st.k0 / 32u, to + qb + stage_part(st.k0 / 8u), wave);
+        } else {
+            issue_x(st.x0, st.k0, to, wave);
+            if (mode0 == STREAM_X_RMSNORM)
+                issue_x(st.a0, st.k0, to + x_floats * 4u, wave);
+            else if (two)
+                issue_x(st.x1, st.k1, to + x_floats * 4u, wave);
+        }
     }
 
     // The issue cursor: the step's first weight byte, steps left in its
@@ -844,17 +936,21 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     const StreamProduct p0 = table[first_pi];
     const StreamProduct p1 = two ? table[first_pi + 1u] : p0;
     if (staged) {
-        step_barrier_ahead<PS, R - 1u>(prologue);  // the staged x is complete
-        quantise_lds<KIND>(acts, xs, p0.k);
-        if (two) quantise_lds<KIND>(acts + act_bytes, xs + x_floats, p1.k);
-    } else {
-        float4 xv[XP];
-        load_x(p0.x, p0.k, xv);
-        quantise_into<KIND>(acts, p0.x, p0.k, xv);
-        if (two) {
-            load_x(p1.x, p1.k, xv);
-            quantise_into<KIND>(acts + act_bytes, p1.x, p1.k, xv);
+        step_barrier_ahead<PS, R - 1u>(prologue);  // the staged row is complete
+        if (mode0 == STREAM_X_QUANTISED) {
+            unpack_lds<KIND>(acts, (const uint8_t*)xs, p0.k);
+        } else if (mode0 == STREAM_X_RMSNORM) {
+            // Σx² in index order by one lane, while the first weights arrive.
+            if (t == 0) root_slot[0] = __builtin_sqrtf(ordered_sum<true, 4>(xs, p0.k) / (float)p0.k + p0.eps);
+            lds_barrier();
+            quantise_lds<KIND>(acts, xs, p0.k, root_slot[0], xs + x_floats);
+        } else {
+            quantise_lds<KIND>(acts, xs, p0.k);
+            if (two) quantise_lds<KIND>(acts + act_bytes, xs + x_floats, p1.k);
         }
+    } else {
+        prepare_global<KIND>(acts, p0, root_slot);
+        if (two) prepare_global<KIND>(acts + act_bytes, p1, root_slot);
     }
     step_barrier_ahead<PS, R - 1u>(prologue);  // the staged x is read; the activations are complete
 
@@ -874,6 +970,7 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     float* fdst = cdst;
     uint32_t frows = 0, fnb = cnb, fstride = cstride, fbslot = 0;
     bool fbias = cbias;
+    const uint32_t prepared = two ? 2u : 1u;  // products prepared before the loop
 
     for (uint32_t i = 0; i < count; ++i) {
         step_barrier_ahead<PS, R - 2u>(issued - 1u - i);
@@ -905,12 +1002,10 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
             csrc = (uint64_t)q.w, cleft = q.n, crows = q.rows, cstep = q.step_bytes, cdst = q.dst;
             cnb = 2u * q.np, cstride = q.stride, cbias = q.bias != nullptr;
             g = stream_lane<KIND>(q);
-            if (nth >= 2) {
+            if (nth >= prepared) {
                 // Into the buffer of the product before last (read before the
                 // barrier that began this step).
-                float4 xv[XP];
-                load_x(q.x, q.k, xv);
-                quantise_into<KIND>(acts + (nth & 1u) * act_bytes, q.x, q.k, xv);
+                prepare_global<KIND>(acts + (nth & 1u) * act_bytes, q, root_slot);
                 step_barrier<0>();
             }
             read_acts(acts + (nth & 1u) * act_bytes, q.k, g.j, v);
@@ -1457,11 +1552,21 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
                  std::vector<StreamStart>& starts) {
     const uint32_t bb = block_bytes(kind);
     uint64_t total = 0;
-    uint32_t max_k = 0, part = 0;
+    uint32_t max_k = 0, part = 0, stage = 0;
     bool bias = false;
     for (StreamProduct& p : products) {
         const uint32_t nb = p.k >> 5;
         if (p.n == 0 || nb < 2 || nb % 2 != 0 || nb > 512 || (uintptr_t)p.w % 4u != 0) return false;
+        if (p.mode > STREAM_X_QUANTISED) return false;
+        if (p.mode == STREAM_X_RMSNORM && p.aux0 == nullptr) return false;
+        if (p.mode == STREAM_X_QUANTISED &&
+            ((uintptr_t)p.x % 4u != 0 || p.aux0 == nullptr || (kind != 0 && p.aux1 == nullptr)))
+            return false;
+        // Floats one staging slot must hold: x (the norm's weights take the
+        // second slot), or a quantised row's three parts.
+        stage = std::max(stage, p.mode == STREAM_X_QUANTISED
+                                    ? (stage_part(p.k) + 2u * stage_part(p.k / 8u)) / 4u
+                                    : p.k);
         p.np = nb / 2u;
         p.row_bytes = nb * bb;
         // Rows per step: a pair per thread, within the step's 8 KB after the
@@ -1483,7 +1588,7 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
     l.act_bytes = (uint32_t)align16((size_t)max_k + 8u * (max_k >> 5));
     l.part_floats = (part + 3u) & ~3u;
     l.has_bias = bias ? 1u : 0u;
-    const uint32_t x_floats = (max_k + 255u) & ~255u;  // whole 1 KB direct loads
+    const uint32_t x_floats = (stage + 255u) & ~255u;  // whole 1 KB direct loads
     l.x_floats = x_floats;
     const size_t bias_slots = bias ? 1024u : 0u;
     // LDS with `ring` slots: biases, ring, contributions, then the
@@ -1492,7 +1597,7 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
         const size_t head = (ring + 1u) * bias_slots;
         act_offset = head + (size_t)ring * STREAM_STEP + 2u * (size_t)l.part_floats * 4u;
         act_offset = std::max(act_offset, head + (size_t)(ring - 1u) * STREAM_STEP + 2u * (size_t)l.x_floats * 4u);
-        return act_offset + 2u * (size_t)l.act_bytes;
+        return act_offset + 2u * (size_t)l.act_bytes + 16u;  // + the root's slot
     };
     // Measured on the config-2 matvec set: more workgroups per compute unit
     // beat a deeper ring (6 with two slots: 15.9 us; 4 with three: 18.0 us;
@@ -1545,8 +1650,10 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
         st.s_begin = (uint32_t)s, st.s_end = (uint32_t)e, st.first_pi = pi;
         st.src = (uint64_t)(uintptr_t)p.w + (uint64_t)sp * p.step_bytes, st.wlast = p.wlast;
         st.bias = p.bias ? p.bias : p.x, st.has = p.bias ? 1u : 0u;
-        st.x0 = p.x, st.k0 = p.k;
-        const bool two = e > s && (uint64_t)p.first + p.steps < e;
+        st.x0 = p.x, st.k0 = p.k, st.mode0 = p.mode, st.a0 = p.aux0, st.a1 = kind != 0 ? p.aux1 : nullptr;
+        // A second product is staged with the first when both take f32 x.
+        const bool two = e > s && (uint64_t)p.first + p.steps < e && p.mode == STREAM_X_F32 &&
+                         products[pi + 1u].mode == STREAM_X_F32;
         st.x1 = two ? products[pi + 1u].x : nullptr, st.k1 = two ? products[pi + 1u].k : 0u;
         st.left = p.steps - sp, st.step_bytes = p.step_bytes, st.rows = p.rows, st.row = sp * p.rows, st.n = p.n;
     }

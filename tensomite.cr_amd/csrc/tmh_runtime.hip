@@ -750,16 +750,24 @@ struct Plan {
 // Builds the streamed form of a plan; false (nothing allocated) when the
 // products do not fit the streamed kernel or TMH_PLAN_KERNEL=rows asks for
 // the tiled one.
-int stream_plan(Plan* p, const std::vector<tmh::RowProduct>& rows, int compute_units, bool& made) {
+int stream_plan(Plan* p, const tmh_product* given, const std::vector<tmh::RowProduct>& rows, int compute_units,
+                bool& made) {
     made = false;
     const char* env = getenv("TMH_PLAN_KERNEL");
     if (env && std::string(env) == "rows") return TMH_SUCCESS;
     std::vector<tmh::StreamProduct> products(rows.size());
     for (size_t i = 0; i < rows.size(); ++i) {
         tmh::StreamProduct& q = products[i];
+        const tmh_product& g = given[i];
         q = tmh::StreamProduct{};
         q.w = rows[i].w, q.x = rows[i].x, q.dst = rows[i].dst, q.bias = rows[i].bias;
         q.n = rows[i].n, q.k = rows[i].k;
+        q.mode = g.x_mode, q.eps = g.eps;
+        if (g.x_mode == TMH_X_RMSNORM) q.aux0 = (const float*)g.norm;
+        if (g.x_mode == TMH_X_QUANTISED) {
+            q.aux0 = (const float*)g.scales;
+            q.aux1 = p->kind == 1u ? (const void*)g.totals : p->kind == 2u ? (const void*)g.sums : nullptr;
+        }
     }
     tmh::StreamLaunch l{};
     std::vector<tmh::StreamStart> starts;
@@ -796,10 +804,16 @@ int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, 
     std::vector<tmh::RowProduct> rows(count);
     uint32_t first = 0;
     size_t act_bytes = 0, part_bytes = 0;
+    bool modes = false;  // a product whose x is not plain f32: the streamed kernel only
     for (uint32_t i = 0; i < count; ++i) {
         const tmh_product& q = products[i];
         if (q.k == 0 || q.k % 32u != 0 || q.n == 0) return TMH_ERROR_SHAPE;
         if (!q.w || !q.x || !q.dst) return TMH_ERROR_INVALID_VALUE;
+        if (q.x_mode > TMH_X_QUANTISED) return TMH_ERROR_INVALID_VALUE;
+        if (q.x_mode == TMH_X_RMSNORM && !q.norm) return TMH_ERROR_INVALID_VALUE;
+        if (q.x_mode == TMH_X_QUANTISED && (!q.scales || (kind == 1u && !q.totals) || (kind == 2u && !q.sums)))
+            return TMH_ERROR_INVALID_VALUE;
+        modes = modes || q.x_mode != TMH_X_F32;
         const uint8_t* w = (const uint8_t*)(q.w + q.w_byte_offset);
         if (!tmh::row_kernel_fits(TMH_MODE_LANES, w, q.k)) return TMH_ERROR_SHAPE;
         tmh::RowProduct& r = rows[i];
@@ -819,7 +833,7 @@ int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, 
     Plan* p = new Plan{d->index, kind, count, first, act_bytes, part_bytes, nullptr, nullptr, false, {}, nullptr};
     if (count) {
         bool made = false;
-        const int r = stream_plan(p, rows, d->compute_units, made);
+        const int r = stream_plan(p, products, rows, d->compute_units, made);
         if (r != TMH_SUCCESS) {
             delete p;
             return r;
@@ -828,6 +842,10 @@ int tmh_plan_create(uint32_t kind, const tmh_product* products, uint32_t count, 
             *plan = (uint64_t)p;
             return TMH_SUCCESS;
         }
+    }
+    if (modes) {
+        delete p;
+        return TMH_ERROR_SHAPE;
     }
     if (act_bytes + part_bytes > 64u * 1024u) {
         delete p;

@@ -76,7 +76,26 @@ class DeviceInfo(ctypes.Structure):
 class Product(ctypes.Structure):
     """tmh_product: one one-row product of a plan."""
     _fields_ = [("w", ctypes.c_uint64), ("w_byte_offset", ctypes.c_uint64), ("x", ctypes.c_uint64),
-                ("dst", ctypes.c_uint64), ("bias", ctypes.c_uint64), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32)]
+                ("dst", ctypes.c_uint64), ("bias", ctypes.c_uint64), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32),
+                ("x_mode", ctypes.c_uint32), ("eps", ctypes.c_float), ("norm", ctypes.c_uint64),
+                ("scales", ctypes.c_uint64), ("sums", ctypes.c_uint64), ("totals", ctypes.c_uint64)]
+
+
+X_F32, X_RMSNORM, X_QUANTISED = 0, 1, 2
+
+
+class RMSNormInput:
+    """A plan product's x taken through Op::RMSNorm (weights `norm`, `eps`) before the product."""
+
+    def __init__(self, norm: "Buffer", eps: float):
+        self.norm, self.eps = norm, eps
+
+
+class QuantisedInput:
+    """A plan product's x already quantised by HIPDevice.quantize_rows (x is its int8 values, qs)."""
+
+    def __init__(self, scales: "Buffer", sums: "Buffer", totals: "Buffer"):
+        self.scales, self.sums, self.totals = scales, sums, totals
 
 
 class Counters(ctypes.Structure):
@@ -423,15 +442,31 @@ class HIPDevice:
 
     # -- plans: many independent one-row products in one launch
     def plan(self, kind, products) -> "Plan":
-        """products: iterable of (w Buffer, w_row, x Buffer, dst Buffer, bias Buffer|None, n, k)."""
+        """products: iterable of (w Buffer, w_row, x Buffer, dst Buffer, bias Buffer|None, n, k[, xin]);
+        xin None (x is f32), RMSNormInput or QuantisedInput (x is the int8 values)."""
         kk = kind_of(kind)
         items = list(products)
         arr = (Product * max(len(items), 1))()
-        for i, (w, w_row, x, dst, bias, n, k) in enumerate(items):
+        for i, item in enumerate(items):
+            w, w_row, x, dst, bias, n, k = item[:7]
+            xin = item[7] if len(item) > 7 else None
             rb = row_bytes(kk, k)
-            if (w_row + n) * rb > w.bytesize or k * 4 > x.bytesize or n * 4 > dst.bytesize:
+            x_bytes = k if isinstance(xin, QuantisedInput) else 4 * k
+            if (w_row + n) * rb > w.bytesize or x_bytes > x.bytesize or n * 4 > dst.bytesize:
                 raise ShapeError(f"product {i}: buffers too small for [{n}, {k}]")
             arr[i] = Product(w.pointer, w_row * rb, x.pointer, dst.pointer, bias.pointer if bias else 0, n, k)
+            if isinstance(xin, RMSNormInput):
+                if k * 4 > xin.norm.bytesize:
+                    raise ShapeError(f"product {i}: norm weights too small for {k}")
+                arr[i].x_mode, arr[i].eps, arr[i].norm = X_RMSNORM, xin.eps, xin.norm.pointer
+            elif isinstance(xin, QuantisedInput):
+                nb = k // 32
+                if min(xin.scales.bytesize, xin.sums.bytesize, xin.totals.bytesize) < 4 * nb:
+                    raise ShapeError(f"product {i}: quantised row's arrays too small for {k}")
+                arr[i].x_mode = X_QUANTISED
+                arr[i].scales, arr[i].sums, arr[i].totals = xin.scales.pointer, xin.sums.pointer, xin.totals.pointer
+            elif xin is not None:
+                raise TypeError(f"product {i}: input {xin!r} is neither RMSNormInput nor QuantisedInput")
         handle = U64(0)
         check("tmh_plan_create", self.lib.tmh_plan_create(kk, arr, len(items), ctypes.byref(handle)))
         return Plan(self, handle.value, items)

@@ -397,6 +397,101 @@ def test_stream_plan_many_small_products(dev, fmt, wgs, ring, monkeypatch):
     plan.destroy()
 
 
+def plan_input(dev, mode, x, k, seed):
+    """A plan product's activation row in input mode `mode` (0 f32, 1 RMSNorm, 2
+    quantised beforehand) and the f32 row the product should see."""
+    if mode == 0:
+        return dev.from_array(x), None, x
+    if mode == 1:
+        w = np.random.default_rng(seed).normal(1.0, 0.3, k).astype(np.float32)
+        return dev.from_array(x), th.RMSNormInput(dev.from_array(w), 1e-5), oracle.rmsnorm(x[None, :], w, 1e-5)[0]
+    scales, sums, totals, qs = dev.quantize_rows(dev.from_array(x), 1, k)
+    return qs, th.QuantisedInput(scales, sums, totals), x
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("wgs,ring,rows", [("1", "2", "short"), ("6", "2", "short"), ("2", "3", "short"),
+                                           ("6", "2", "long")])
+def test_stream_plan_input_modes(dev, fmt, wgs, ring, rows, monkeypatch):
+    # Products whose x comes in each input mode in one plan: f32, f32 under
+    # an RMSNorm (normalised by every workgroup that takes part of it), and
+    # already quantised -- staged before the loop for a workgroup's first
+    # product, prepared in the loop for the later ones ("long": an f32 row of
+    # 8192 is past the staging budget, so every product is prepared from
+    # global memory); the bits of the oracle's RMSNorm then product, or of
+    # the product of x.
+    if rows == "long" and fmt == "Q8_0":
+        pytest.skip("Q8_0 rows of 8192 values are longer than a step of the streamed kernel")
+    monkeypatch.setenv("TMH_PLAN_KERNEL", "stream")
+    monkeypatch.setenv("TMH_STREAM_WGS", wgs)
+    monkeypatch.setenv("TMH_STREAM_RING", ring)
+    rng = np.random.default_rng(950)
+    ks = [64, 576, 2048, 128, 1536, 256] if rows == "short" else [64, 576, 8192, 2048]
+    shapes = [(int(rng.integers(1, 200)) if i % 9 else 2048, ks[i % len(ks)]) for i in range(160)]
+    items, wants, ys = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        mode = i % 3
+        wq = weights(fmt, n, k, 3000 + i)
+        x = acts(1, k, 4000 + i)
+        xbuf, xin, seen = plan_input(dev, mode, x, k, 5000 + i)
+        b = rng.uniform(-1, 1, n).astype(np.float32) if i % 4 == 1 else None
+        y = dev.alloc(4 * n)
+        ys.append(y)
+        items.append((dev.from_array(wq), 0, xbuf, y, dev.from_array(b) if b is not None else None, n, k, xin))
+        want = oracle.matmul(fmt, seen, wq, 1, n, k)[0]
+        wants.append(want if b is None else oracle.add_bias(want[None, :], b)[0])
+    say("stream plan modes", fmt, wgs, ring, len(shapes))
+    plan = dev.plan(fmt, items)
+    for _ in range(2):
+        plan.run()
+    dev.sync()
+    for i, (n, k) in enumerate(shapes):
+        got = dev.to_array(ys[i], np.float32, n)
+        assert np.array_equal(bits(got), bits(wants[i])), (i, shapes[i], i % 3)
+    plan.destroy()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("mode,n,k", [(1, 6144, 2048), (1, 16384, 2048), (2, 2048, 8192), (2, 2048, 2048),
+                                      (1, 49152, 576)])
+def test_stream_plan_one_product_input_modes(dev, fmt, mode, n, k):
+    # The decode step's single-product plans: the qkv, gate_up and head
+    # products over an RMSNorm of the residual row, and the o and down
+    # products over an already quantised row with the residual as bias.
+    say("one-product plan", fmt, mode, n, k)
+    wq = weights(fmt, n, k, 6000 + n + k)
+    x = acts(1, k, 7000 + k)
+    xbuf, xin, seen = plan_input(dev, mode, x, k, 8000 + k)
+    b = acts(1, n, 9000 + n) if mode == 2 else None
+    y = dev.alloc(4 * n)
+    item = (dev.from_array(wq), 0, xbuf, y, dev.from_array(b) if b is not None else None, n, k, xin)
+    if fmt == "Q8_0" and k == 8192:
+        # a Q8_0 row of 8192 values is longer than a step of the streamed kernel
+        with pytest.raises(th.ShapeError):
+            dev.plan(fmt, [item])
+        return
+    plan = dev.plan(fmt, [item])
+    plan.run()
+    got = dev.to_array(y, np.float32, n)
+    dev.sync()
+    want = oracle.matmul(fmt, seen, wq, 1, n, k)[0]
+    if b is not None:
+        want = oracle.add_bias(want[None, :], b)[0]
+    assert np.array_equal(bits(got), bits(want))
+    plan.destroy()
+
+
+def test_plan_input_modes_need_the_streamed_kernel(dev, monkeypatch):
+    # The tiled kernel takes f32 x only: a plan with another input mode is
+    # refused when it is asked for.
+    monkeypatch.setenv("TMH_PLAN_KERNEL", "rows")
+    wq = weights("Q4_0", 64, 256, 1)
+    x = acts(1, 256, 2)
+    xbuf, xin, _ = plan_input(dev, 1, x, 256, 3)
+    with pytest.raises(th.ShapeError):
+        dev.plan("Q4_0", [(dev.from_array(wq), 0, xbuf, dev.alloc(256), None, 64, 256, xin)])
+
+
 MATRIX_SHAPES = [
     # (rows, n, k): config 4 prefill, ragged edges, short k, the 1.7B MLP
     (512, 2048, 2048), (33, 100, 576), (64, 64, 64), (100, 130, 1024), (128, 8192, 2048), (40, 2048, 8192),
