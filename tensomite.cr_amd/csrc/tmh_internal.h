@@ -131,8 +131,17 @@ struct StreamLaunch {
 // k set by the caller), the launch's shape, and each workgroup's first
 // product. False when the products do not fit the kernel (rows of an odd
 // number of blocks, or LDS).
+// wgs_per_cu: workgroups per compute unit (0: the default, 6, or TMH_STREAM_WGS);
+// the ring gets the LDS they leave.
 bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& launch,
-                 std::vector<StreamStart>& starts);
+                 std::vector<StreamStart>& starts, uint32_t wgs_per_cu = 0);
+
+// Builds a streamed launch for `products` and uploads its product table and
+// workgroup starts into one device allocation (*mem, freed by the caller).
+// hipErrorInvalidValue, nothing allocated, when the products do not fit
+// the kernel.
+hipError_t make_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& launch,
+                       void** mem, uint32_t wgs_per_cu = 0);
 
 // Launches the streamed one-row kernel (table and starts in device memory).
 hipError_t launch_stream(uint32_t kind, const StreamLaunch& launch, hipStream_t stream);

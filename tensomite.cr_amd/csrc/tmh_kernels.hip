@@ -686,12 +686,14 @@ __device__ __forceinline__ void step_barrier_ahead(uint32_t ahead) {
 }
 
 // Brings x (k floats) into LDS at `to` by direct loads, 1 KB per wave load
-// (16-byte aligned x) or 256 bytes (otherwise); lanes past the end read the
-// last piece again.
+// (x 16-byte aligned and a whole number of 16-byte pieces) or 256 bytes
+// (otherwise); lanes past the end read the last piece again and write it
+// past the end (so a piece is never partial: it would come from the wrong
+// place).
 __device__ __forceinline__ void issue_x(const float* x, uint32_t k, uint32_t to, uint32_t wave) {
     const uint32_t lane = threadIdx.x & 63u;
     const uintptr_t base = (uintptr_t)x;
-    if ((base & 15u) == 0) {
+    if ((base & 15u) == 0 && k % 4u == 0) {
         const uintptr_t last = base + (uintptr_t)k * 4u - 16u;
         for (uint32_t q = wave; q * 1024u < k * 4u; q += 4u) {
             uintptr_t a = base + q * 1024u + lane * 16u;
@@ -708,11 +710,11 @@ __device__ __forceinline__ void issue_x(const float* x, uint32_t k, uint32_t to,
     }
 }
 
-// quantise_into with x read from LDS (xs, k floats), and the norm's
-// weights too (ws, or none).
+// quantise_into with x read from LDS (xs, k floats); the norm's weights,
+// if any, from global memory.
 template <int KIND>
 __device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint32_t k, float root = 1.0f,
-                                             const float* ws = nullptr) {
+                                             const float* __restrict__ norm = nullptr) {
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
     int8_t* lqs = (int8_t*)act;
@@ -722,7 +724,7 @@ __device__ __forceinline__ void quantise_lds(uint8_t* act, const float* xs, uint
         const uint32_t g = pass * 32u + (t >> 3), sub = t & 7u;
         if (g < nb) {
             float4 v = *(const float4*)(xs + g * 32u + sub * 4u);
-            if (ws) v = normalise4(v, root, *(const float4*)(ws + g * 32u + sub * 4u));
+            if (norm) v = normalise4(v, root, load_f4(norm + g * 32u + sub * 4u, ((uintptr_t)norm & 15u) == 0));
             const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
             *(uint32_t*)(lqs + g * 32u + sub * 4u) = q.packed;
             if (sub == 0) {
@@ -842,10 +844,10 @@ __device__ __forceinline__ StreamLane stream_lane(const StreamProduct& P) {
     return g;
 }
 
-// LDS layout of the streamed kernel: biases (R + 1 slots of 256 floats, with
-// HB), ring slots 0 ... R-1 of STREAM_STEP bytes, contributions (two buffers
-// of part_floats), then from act_offset the activations (two buffers of
-// act_bytes) and 16 bytes for an RMSNorm's root. Before the loop, the x of the range's first two products
+// LDS layout of the streamed kernel: 16 bytes for an RMSNorm's root, biases
+// (R + 1 slots of 256 floats, with HB), ring slots 0 ... R-1 of STREAM_STEP
+// bytes, contributions (two buffers of part_floats), then from act_offset
+// the activations (two buffers of act_bytes; one for a one-product plan). Before the loop, the x of the range's first two products
 // (x_floats apart; none when x_floats is 0) is staged from ring slot R-1
 // on, over memory first written in the loop.
 template <int KIND, uint32_t R, bool HB>
@@ -856,17 +858,17 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     constexpr uint32_t PW = Fmt<KIND>::PW;
     constexpr uint32_t PS = HB ? 3u : 2u;  // vector memory operations a wave issues per step
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const uint32_t G = gridDim.x, b = blockIdx.x, t = threadIdx.x, lane = t & 63u;
+    const uint32_t b = blockIdx.x, t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const StreamStart st = starts[b];
     const uint32_t s_begin = st.s_begin, s_end = st.s_end;
     if (s_begin >= s_end) return;
     const uint32_t count = s_end - s_begin;
-    float* biases = (float*)smem;
-    uint8_t* ring = smem + (HB ? (R + 1u) * 1024u : 0u);
+    float* root_slot = (float*)smem;  // an RMSNorm's root, shared
+    float* biases = (float*)(smem + 16u);
+    uint8_t* ring = smem + 16u + (HB ? (R + 1u) * 1024u : 0u);
     float* parts = (float*)(ring + R * STREAM_STEP);
     uint8_t* acts = smem + act_offset;
-    float* root_slot = (float*)(acts + 2u * act_bytes);  // an RMSNorm's root, shared
     float* xs = (float*)(ring + (R - 1u) * STREAM_STEP);
     const uint32_t ring_lds = lds_address(ring) + wave * 2048u, bias_lds = lds_address(biases) + wave * 256u;
 
@@ -887,10 +889,7 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
             if (st.a1) issue_x((const float*)st.a1, st.k0 / 32u, to + qb + stage_part(st.k0 / 8u), wave);
         } else {
             issue_x(st.x0, st.k0, to, wave);
-            if (mode0 == STREAM_X_RMSNORM)
-                issue_x(st.a0, st.k0, to + x_floats * 4u, wave);
-            else if (two)
-                issue_x(st.x1, st.k1, to + x_floats * 4u, wave);
+            if (two) issue_x(st.x1, st.k1, to + x_floats * 4u, wave);
         }
     }
 
@@ -940,10 +939,18 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
         if (mode0 == STREAM_X_QUANTISED) {
             unpack_lds<KIND>(acts, (const uint8_t*)xs, p0.k);
         } else if (mode0 == STREAM_X_RMSNORM) {
-            // Σx² in index order by one lane, while the first weights arrive.
-            if (t == 0) root_slot[0] = __builtin_sqrtf(ordered_sum<true, 4>(xs, p0.k) / (float)p0.k + p0.eps);
+            // The squares in parallel (in place), then Σx² in index order by
+            // one lane -- adds only: a wave instruction a value -- while the
+            // first weights arrive. x and the norm's weights are then read
+            // from global memory, when the prologue's weight loads are in
+            // (the compiler waits for every load there).
+            for (uint32_t i = t; i < p0.k; i += 256u) xs[i] = xs[i] * xs[i];
             lds_barrier();
-            quantise_lds<KIND>(acts, xs, p0.k, root_slot[0], xs + x_floats);
+            if (t == 0) root_slot[0] = __builtin_sqrtf(ordered_sum<false, 4>(xs, p0.k) / (float)p0.k + p0.eps);
+            lds_barrier();
+            float4 xv[XP];
+            load_x(p0.x, p0.k, xv);
+            quantise_into<KIND>(acts, p0.x, p0.k, xv, root_slot[0], p0.aux0);
         } else {
             quantise_lds<KIND>(acts, xs, p0.k);
             if (two) quantise_lds<KIND>(acts + act_bytes, xs + x_floats, p1.k);
@@ -1549,7 +1556,7 @@ static constexpr uint32_t STREAM_RING_MIN = 2, STREAM_RING_MAX = 8, STREAM_WGS =
 static constexpr size_t STREAM_LDS_LIMIT = 64u * 1024u, CU_LDS = 160u * 1024u;
 
 bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& l,
-                 std::vector<StreamStart>& starts) {
+                 std::vector<StreamStart>& starts, uint32_t wgs_per_cu) {
     const uint32_t bb = block_bytes(kind);
     uint64_t total = 0;
     uint32_t max_k = 0, part = 0, stage = 0;
@@ -1591,18 +1598,22 @@ bool plan_stream(uint32_t kind, std::vector<StreamProduct>& products, int comput
     const uint32_t x_floats = (stage + 255u) & ~255u;  // whole 1 KB direct loads
     l.x_floats = x_floats;
     const size_t bias_slots = bias ? 1024u : 0u;
-    // LDS with `ring` slots: biases, ring, contributions, then the
-    // activations, no earlier than the end of the x staged from slot R-1.
+    // One product needs one staging slot and one activation buffer; more
+    // need two of each (a workgroup's first two products).
+    const size_t buffers = products.size() == 1 ? 1u : 2u;
+    // LDS with `ring` slots: the root's slot, biases, ring, contributions,
+    // then the activations, no earlier than the end of the x staged from
+    // slot R-1.
     auto lds_for = [&](uint32_t ring, size_t& act_offset) {
-        const size_t head = (ring + 1u) * bias_slots;
+        const size_t head = 16u + (ring + 1u) * bias_slots;
         act_offset = head + (size_t)ring * STREAM_STEP + 2u * (size_t)l.part_floats * 4u;
-        act_offset = std::max(act_offset, head + (size_t)(ring - 1u) * STREAM_STEP + 2u * (size_t)l.x_floats * 4u);
-        return act_offset + 2u * (size_t)l.act_bytes + 16u;  // + the root's slot
+        act_offset = std::max(act_offset, head + (size_t)(ring - 1u) * STREAM_STEP + buffers * l.x_floats * 4u);
+        return act_offset + buffers * (size_t)l.act_bytes;
     };
     // Measured on the config-2 matvec set: more workgroups per compute unit
     // beat a deeper ring (6 with two slots: 15.9 us; 4 with three: 18.0 us;
     // 3 with four: 21 us), so the ring gets what `wgs` workgroups leave.
-    const uint32_t wgs = env_u32("TMH_STREAM_WGS", STREAM_WGS);
+    const uint32_t wgs = wgs_per_cu ? wgs_per_cu : env_u32("TMH_STREAM_WGS", STREAM_WGS);
     uint32_t ring = env_u32("TMH_STREAM_RING", 0u);
     size_t act_offset = 0;
     if (ring == 0) {

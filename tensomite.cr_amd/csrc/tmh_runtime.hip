@@ -41,6 +41,28 @@ size_t scratch_need(uint32_t rows, uint32_t k) {
 }
 
 // The quantise pass's four outputs for `rows` rows of k, carved from `base`.
+hipError_t make_stream(uint32_t kind, std::vector<StreamProduct>& products, int compute_units, StreamLaunch& l,
+                       void** mem, uint32_t wgs_per_cu) {
+    *mem = nullptr;
+    std::vector<StreamStart> starts;
+    if (!plan_stream(kind, products, compute_units, l, starts, wgs_per_cu)) return hipErrorInvalidValue;
+    const size_t table_bytes = (sizeof(StreamProduct) * products.size() + 255u) & ~(size_t)255u;
+    hipError_t e = device_malloc(mem, table_bytes + sizeof(StreamStart) * starts.size());
+    if (e == hipSuccess)
+        e = hipMemcpy(*mem, products.data(), sizeof(StreamProduct) * products.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy((uint8_t*)*mem + table_bytes, starts.data(), sizeof(StreamStart) * starts.size(),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (*mem) (void)hipFree(*mem);
+        *mem = nullptr;
+        return e;
+    }
+    l.table = (const StreamProduct*)*mem;
+    l.starts = (const StreamStart*)((uint8_t*)*mem + table_bytes);
+    return hipSuccess;
+}
+
 Activations carve_scratch(uint8_t* base, uint32_t rows, uint32_t k) {
     const size_t nb = k / 32u;
     const size_t per = ((size_t)rows * nb * 4u + 255u) & ~(size_t)255u;
@@ -770,22 +792,10 @@ int stream_plan(Plan* p, const tmh_product* given, const std::vector<tmh::RowPro
         }
     }
     tmh::StreamLaunch l{};
-    std::vector<tmh::StreamStart> starts;
-    if (!tmh::plan_stream(p->kind, products, compute_units, l, starts)) return TMH_SUCCESS;
-    const size_t table_bytes = align256(sizeof(tmh::StreamProduct) * products.size());
     void* mem = nullptr;
-    hipError_t e = device_malloc(&mem, table_bytes + sizeof(tmh::StreamStart) * starts.size());
-    if (e == hipSuccess)
-        e = hipMemcpy(mem, products.data(), sizeof(tmh::StreamProduct) * products.size(), hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = hipMemcpy((uint8_t*)mem + table_bytes, starts.data(), sizeof(tmh::StreamStart) * starts.size(),
-                      hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-        if (mem) (void)hipFree(mem);
-        return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
-    }
-    l.table = (const tmh::StreamProduct*)mem;
-    l.starts = (const tmh::StreamStart*)((uint8_t*)mem + table_bytes);
+    const hipError_t e = tmh::make_stream(p->kind, products, compute_units, l, &mem);
+    if (e == hipErrorInvalidValue) return TMH_SUCCESS;  // not for the streamed kernel
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
     p->stream = l;
     p->mem = mem;
     p->streamed = true;

@@ -427,7 +427,8 @@ def test_stream_plan_input_modes(dev, fmt, wgs, ring, rows, monkeypatch):
     monkeypatch.setenv("TMH_STREAM_RING", ring)
     rng = np.random.default_rng(950)
     ks = [64, 576, 2048, 128, 1536, 256] if rows == "short" else [64, 576, 8192, 2048]
-    shapes = [(int(rng.integers(1, 200)) if i % 9 else 2048, ks[i % len(ks)]) for i in range(160)]
+    # k cycles independently of the mode (i % 3), so every mode meets every k
+    shapes = [(int(rng.integers(1, 200)) if i % 9 else 2048, ks[(i // 3) % len(ks)]) for i in range(160)]
     items, wants, ys = [], [], []
     for i, (n, k) in enumerate(shapes):
         mode = i % 3
@@ -453,7 +454,7 @@ def test_stream_plan_input_modes(dev, fmt, wgs, ring, rows, monkeypatch):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("mode,n,k", [(1, 6144, 2048), (1, 16384, 2048), (2, 2048, 8192), (2, 2048, 2048),
-                                      (1, 49152, 576)])
+                                      (1, 49152, 576), (2, 32, 64), (1, 100, 64), (2, 96, 128)])
 def test_stream_plan_one_product_input_modes(dev, fmt, mode, n, k):
     # The decode step's single-product plans: the qkv, gate_up and head
     # products over an RMSNorm of the residual row, and the o and down
