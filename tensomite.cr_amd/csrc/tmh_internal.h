@@ -146,6 +146,13 @@ hipError_t make_stream(uint32_t kind, std::vector<StreamProduct>& products, int 
 // Launches the streamed one-row kernel (table and starts in device memory).
 hipError_t launch_stream(uint32_t kind, const StreamLaunch& launch, hipStream_t stream);
 
+// dst[rows, n] = residual[rows, n] + act · wᵀ for a few activation rows
+// (fewer than the matrix cores take), the residual added in the product's
+// fold as a bias row per activation row: the host's `x + product`, one
+// rounding. hipErrorInvalidValue when the shape is not for that kernel.
+hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* residual,
+                                   uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream);
+
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);

@@ -95,8 +95,9 @@ hipError_t norm_quantise(const Llama& m, const DeviceContext& ctx, const float* 
 
 // The residual update x += act · wᵀ, as the host's `x + product` (one
 // rounding per element either way round): for one row the product adds x
-// as its bias and writes the other residual buffer; for more rows it is a
-// product and an add.
+// as its bias and writes the other residual buffer; for a few rows the
+// lanes product adds each row's x the same way; for more it is a product
+// and an add.
 hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
                     uint32_t k, int& cur) {
     const uint32_t W = (uint32_t)m.c.width;
@@ -104,6 +105,12 @@ hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, 
         hipError_t e = product(m, ctx, w, act, 1, W, k, m.x[cur ^ 1], m.x[cur]);
         cur ^= 1;
         return e;
+    }
+    hipError_t r = tmh::launch_product_residual(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], rows, W, k,
+                                                ctx.compute_units, ctx.stream);
+    if (r != hipErrorInvalidValue) {
+        cur ^= 1;
+        return r;
     }
     hipError_t e = product(m, ctx, w, act, rows, W, k, m.o_out, nullptr);
     return e == hipSuccess ? tmh::launch_add(m.x[cur], m.o_out, m.x[cur], rows * W, ctx.stream) : e;
