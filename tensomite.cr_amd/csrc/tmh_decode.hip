@@ -205,18 +205,28 @@ __device__ __forceinline__ float wave_top(float top) {
     return top;
 }
 
-// Bytes of one staged chunk of values: positions × width floats.
+// Floats of one staged chunk of values (positions × width), at most; two
+// are staged in turn, in what the LDS (160 KB a workgroup on gfx950) leaves
+// after q, the current key and value, the outputs and the scores. Small
+// chunks leave room for several workgroups a compute unit (prefill runs
+// one per query row and head).
 constexpr uint32_t ATT_CHUNK_FLOATS = 4096;
+constexpr size_t ATT_LDS_LIMIT = 160u * 1024u;
 
-__device__ __forceinline__ uint32_t chunk_positions(uint32_t width) {
-    const uint32_t ch = ATT_CHUNK_FLOATS / width;
-    return ch >= 8u ? ch & ~3u : 4u;
+__host__ __device__ inline uint32_t att_chunk_positions(uint32_t width, uint32_t capacity) {
+    const uint32_t w4 = (width + 3u) & ~3u;
+    const size_t fixed = 4u * (size_t)w4 + ((capacity + 3u) & ~3u);
+    const size_t avail = ATT_LDS_LIMIT / 4u > fixed ? ATT_LDS_LIMIT / 4u - fixed : 0u;
+    size_t ch = std::min<size_t>(ATT_CHUNK_FLOATS / width, avail / (2u * (size_t)width));
+    ch &= ~(size_t)3u;
+    return ch >= 4u ? (uint32_t)ch : 4u;
 }
 
 // LDS layout of the attention kernels, in floats: q, the current key and
 // value, the row's attended outputs, the scores, then two value chunks.
 struct AttLds {
     float *q, *kcur, *vcur, *out, *sc, *vbuf;
+    uint32_t ch;  // positions of one value chunk
 };
 
 __device__ __forceinline__ AttLds att_lds(float* base, uint32_t width, uint32_t capacity) {
@@ -228,12 +238,13 @@ __device__ __forceinline__ AttLds att_lds(float* base, uint32_t width, uint32_t 
     l.out = base + 3u * w4;
     l.sc = base + 4u * w4;
     l.vbuf = l.sc + ((capacity + 3u) & ~3u);
+    l.ch = att_chunk_positions(width, capacity);
     return l;
 }
 
 size_t attention_lds(uint32_t width, uint32_t capacity) {
     const size_t w4 = (width + 3u) & ~3u;
-    const size_t ch = ATT_CHUNK_FLOATS / width >= 8u ? (ATT_CHUNK_FLOATS / width) & ~3u : 4u;
+    const size_t ch = att_chunk_positions(width, capacity);
     return (4u * w4 + ((capacity + 3u) & ~3u) + 2u * ch * width) * sizeof(float);
 }
 
@@ -359,7 +370,7 @@ __device__ void attend(const AttLds& l, const float* __restrict__ kb, const floa
     // products are formed in parallel as the values stage through LDS in
     // chunks (the waves not folding stage the next chunk while the folding
     // waves add up this one), so the fold is a chain of adds.
-    const uint32_t ch = chunk_positions(width);
+    const uint32_t ch = l.ch;
     const uint32_t chunks = (n + ch - 1u) / ch;
     const uint32_t folding = ((width + 63u) >> 6) << 6;  // threads of the folding waves
     const bool overlap = folding < 256u;
@@ -387,16 +398,16 @@ __device__ void attend(const AttLds& l, const float* __restrict__ kb, const floa
 // the F32 values, and, when act.qs is set, their quantised blocks as
 // quantize_activations makes them for the o product's row (width a
 // multiple of 32; the row holds heads · width values).
-__device__ __forceinline__ void emit(const AttLds& l, float* out, uint32_t width, Activations act, uint32_t t,
+__device__ __forceinline__ void emit(const float* lout, float* out, uint32_t width, Activations act, uint32_t t,
                                      uint32_t h, uint32_t heads) {
     const uint32_t tid = threadIdx.x;
-    for (uint32_t c = tid; c < width; c += 256u) out[c] = l.out[c];
+    for (uint32_t c = tid; c < width; c += 256u) out[c] = lout[c];
     if (!act.qs) return;
     const uint32_t blocks = width >> 5;
     const uint32_t k = heads * width, nb = k >> 5;
     const uint32_t blk = tid >> 3, sub = tid & 7u;
     if (blk < blocks) {
-        const float4 v = *reinterpret_cast<const float4*>(l.out + blk * 32u + sub * 4u);
+        const float4 v = *reinterpret_cast<const float4*>(lout + blk * 32u + sub * 4u);
         const Q8Quad q = quantize_quad(v.x, v.y, v.z, v.w);
         const uint32_t g = h * blocks + blk;
         *(uint32_t*)((int8_t*)act.qs + (size_t)t * k + g * 32u + sub * 4u) = q.packed;
@@ -429,7 +440,7 @@ __global__ __launch_bounds__(256) void k_attention(Attention a) {
     for (uint32_t c = tid; c < a.width; c += 256u) l.q[c] = qh[c];
     __syncthreads();
     attend(l, a.keys + base, a.values + base, a.width, (uint32_t)length, last, -1, a.scale);
-    emit(l, out, a.width, a.act, t, h, a.heads);
+    emit(l.out, out, a.width, a.act, t, h, a.heads);
 }
 
 hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream) {
@@ -445,10 +456,260 @@ hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t str
 // rotates its q head and its kv head's new key, takes the new value, and --
 // the first query head of the group only -- writes both into the caches;
 // the new position is attended from LDS, earlier ones from the caches.
+// ------------------------------------------- decode attention, direct loads
+
+// The decode kernel brings everything it reads into LDS by direct loads
+// issued together at its start -- the head's q, k and v rows and RoPE
+// tables, the first chunk of keys and the first chunk of values -- so their
+// latencies overlap instead of following one another (one workgroup per
+// head has a compute unit to itself, and it is those latencies that bound
+// it). LDS, in floats: five staged rows of W64 (width rounded up to 64), q,
+// the current key and value, the outputs (w4 each), the scores (capacity),
+// a key chunk as rows, 16 bytes of pad after every 1 KB (a 16-byte direct
+// load a kilobyte: contiguous reads, few loads; the pad shifts each
+// kilobyte by four banks, so threads reading their positions' rows 16 bytes
+// at a time meet at most 1024 / (4·width)-way conflicts), and a value chunk
+// as rows.
+struct AttDecodeLds {
+    float *stage, *q, *kcur, *vcur, *out, *sc, *kt, *vrows;
+    uint32_t cp;  // positions of a chunk
+};
+
+__host__ __device__ inline uint32_t att_decode_fixed_floats(uint32_t width, uint32_t capacity) {
+    const uint32_t w64 = (width + 63u) & ~63u, w4 = (width + 3u) & ~3u;
+    return 5u * w64 + 4u * w4 + ((capacity + 3u) & ~3u);
+}
+
+__host__ __device__ inline uint32_t att_key_stride(uint32_t width);
+
+// Positions of a chunk: at most 256 (and the capacity), a key row (padded)
+// and a value row each, in what the fixed part leaves of 160 KB (less 2 KB: the value
+// chunk's last direct load and the kernel's own LDS).
+__host__ __device__ inline uint32_t att_decode_chunk(uint32_t width, uint32_t capacity) {
+    const size_t fixed = att_decode_fixed_floats(width, capacity);
+    const size_t avail = ATT_LDS_LIMIT / 4u > fixed + 512u ? ATT_LDS_LIMIT / 4u - fixed - 512u : 0u;
+    size_t cp = std::min<size_t>(std::min<size_t>(256u, (capacity + 3u) & ~3u),
+                                 avail / ((size_t)att_key_stride(width) + width));
+    cp &= ~(size_t)3u;
+    return cp >= 4u ? (uint32_t)cp : 4u;
+}
+
+// Floats a key row takes in LDS on average (width, plus its share of the
+// pad), of a key chunk (whole 1 KB direct loads, 1040 bytes apart), and of
+// a value chunk (whole 256-float direct loads).
+__host__ __device__ inline uint32_t att_key_stride(uint32_t width) { return width + (width + 63u) / 64u; }
+__host__ __device__ inline uint32_t att_kt_floats(uint32_t width, uint32_t cp) {
+    return ((cp * width + 255u) >> 8) * 260u;
+}
+// The LDS float offset of key float f (position · width + column) of a chunk.
+__device__ __forceinline__ uint32_t att_key_at(uint32_t f) { return (f >> 8) * 260u + (f & 255u); }
+__host__ __device__ inline uint32_t att_v_floats(uint32_t width, uint32_t cp) { return (cp * width + 255u) & ~255u; }
+
+__device__ __forceinline__ AttDecodeLds att_decode_lds(float* base, uint32_t width, uint32_t capacity) {
+    const uint32_t w64 = (width + 63u) & ~63u, w4 = (width + 3u) & ~3u;
+    AttDecodeLds l;
+    l.cp = att_decode_chunk(width, capacity);
+    l.stage = base;
+    l.q = base + 5u * w64;
+    l.kcur = l.q + w4;
+    l.vcur = l.kcur + w4;
+    l.out = l.vcur + w4;
+    l.sc = l.out + w4;
+    l.kt = l.sc + ((capacity + 3u) & ~3u);
+    l.vrows = l.kt + att_kt_floats(width, l.cp);
+    return l;
+}
+
+size_t attention_decode_lds(uint32_t width, uint32_t capacity) {
+    const uint32_t cp = att_decode_chunk(width, capacity);
+    return ((size_t)att_decode_fixed_floats(width, capacity) + att_kt_floats(width, cp) + att_v_floats(width, cp)) *
+           sizeof(float);
+}
+
+// Direct loads of `width` floats at src into LDS at `to` by one wave, 64 a
+// load (lanes past the row read its last value again); returns the loads.
+__device__ __forceinline__ uint32_t stage_row(const float* src, uint32_t width, uint32_t to) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t loads = 0;
+    for (uint32_t c0 = 0; c0 < width; c0 += 64u, ++loads)
+        lds_load4(src + min(c0 + lane, width - 1u), to + c0 * 4u);
+    return loads;
+}
+
+// Direct loads of the keys of positions [p0, p0 + cnt) into `to`, 1 KB a
+// load, 1040 bytes apart (att_key_at), loads wave, wave + 4, ...; returns
+// this wave's loads. Lanes past the chunk read its last piece again.
+__device__ __forceinline__ uint32_t stage_keys(const float* kb, uint32_t width, uint32_t p0, uint32_t cnt,
+                                               uint32_t to, uint32_t wave) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uintptr_t base = (uintptr_t)(kb + (size_t)p0 * width);
+    const uintptr_t last = base + (uintptr_t)cnt * width * 4u - 16u;
+    const uint32_t loads = (cnt * width + 255u) >> 8;
+    uint32_t mine = 0;
+    for (uint32_t i = wave; i < loads; i += 4u, ++mine) {
+        const uintptr_t a = base + (uintptr_t)i * 1024u + lane * 16u;
+        lds_load16((const void*)(a < last ? a : last), to + i * 1040u);
+    }
+    return mine;
+}
+
+// Direct loads of the value rows of positions [p0, p0 + cnt) into `to` (as
+// rows), loads i = wave, wave + 4, ...; returns this wave's loads. Lanes
+// past the chunk read its last piece again.
+__device__ __forceinline__ uint32_t stage_values(const float* vb, uint32_t width, uint32_t p0, uint32_t cnt,
+                                                 uint32_t to, uint32_t wave) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uintptr_t base = (uintptr_t)(vb + (size_t)p0 * width);
+    const uintptr_t last = base + (uintptr_t)cnt * width * 4u - 16u;
+    const uint32_t loads = (cnt * width + 255u) >> 8;
+    uint32_t mine = 0;
+    for (uint32_t i = wave; i < loads; i += 4u, ++mine) {
+        const uintptr_t a = base + (uintptr_t)i * 1024u + lane * 16u;
+        lds_load16((const void*)(a < last ? a : last), to + i * 1024u);
+    }
+    return mine;
+}
+
+// attend() of one decode row from the staged chunks: the scores of chunk
+// after chunk (the first staged already), the softmax, then the weighted
+// values chunk after chunk, each product rounded before it is added, in
+// position order. `vloads`: this wave's loads of the first value chunk,
+// issued after its first key chunk. Barriers leave direct loads in flight
+// until they are waited for.
+__device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ kb, const float* __restrict__ vb,
+                              uint32_t width, uint32_t n, int32_t last, int32_t cur, float scale, uint32_t vloads) {
+    __shared__ float tops[4];
+    __shared__ float total_slot;
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t cols = width >> 2, cp = l.cp;
+    const float4* q4 = reinterpret_cast<const float4*>(l.q);
+    const float4* kc4 = reinterpret_cast<const float4*>(l.kcur);
+
+
+    float top = -__builtin_inff();
+    for (uint32_t p0 = 0; p0 < n; p0 += cp) {
+        const uint32_t cnt = min(cp, n - p0);
+        if (p0 == 0) {
+            wait_vm_lds_upto(vloads);  // the first key chunk (the value chunk after it may fly)
+        } else {
+            lds_sync();  // the last chunk's keys are read
+            stage_keys(kb, width, p0, cnt, lds_address(l.kt), wave);
+            wait_vm_lds<0>();
+        }
+        lds_sync();
+        for (uint32_t pl = tid; pl < cnt; pl += 256u) {
+            const uint32_t p = p0 + pl;
+            const bool now = (int32_t)p == cur;
+            float dot = 0.0f;
+            for (uint32_t c4 = 0; c4 < cols; ++c4) {
+                const float4 q = q4[c4];
+                const float4 k = now ? kc4[c4] : *reinterpret_cast<const float4*>(l.kt + att_key_at(pl * width + 4u * c4));
+                dot += q.x * k.x;
+                dot += q.y * k.y;
+                dot += q.z * k.z;
+                dot += q.w * k.w;
+            }
+            float x = dot * scale;
+            // The causal mask adds -inf past the last position seen; its 0
+            // elsewhere only turns a -0 score into +0, which changes no later bit.
+            if ((int32_t)p > last) x = x + -__builtin_inff();
+            l.sc[p] = x;
+            top = x > top ? x : top;
+        }
+    }
+    top = wave_top(top);
+    if ((tid & 63u) == 0) tops[tid >> 6] = top;
+    lds_sync();
+    top = tops[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) top = tops[i] > top ? tops[i] : top;
+    if (l.sc[0] != l.sc[0]) top = l.sc[0];  // the host's top is a NaN at position 0
+    for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = maths_exp(l.sc[p] - top);
+    lds_sync();
+    if (tid == 0) total_slot = ordered_sum(l.sc, n);
+    lds_sync();
+    const float total = total_slot;
+    for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = l.sc[p] / total;
+
+    // Σ_p weight_p · v_p[c] in position order, one lane per column.
+    float acc = 0.0f;
+    const float vnow = tid < width ? l.vcur[tid] : 0.0f;
+    for (uint32_t p0 = 0; p0 < n; p0 += cp) {
+        const uint32_t cnt = min(cp, n - p0);
+        if (p0 > 0) {
+            lds_sync();  // the last chunk's values are read
+            stage_values(vb, width, p0, cnt, lds_address(l.vrows), wave);
+        }
+        wait_vm_lds<0>();
+        lds_sync();  // the chunk's values and the weights are in
+        if (tid < width) {
+            const float* vr = l.vrows + tid;
+            const float* wr = l.sc + p0;
+            // 16 positions a batch: a batch's values and weights are read
+            // into registers before the previous batch is folded (two sets
+            // of registers in turn); the fold makes each product, the
+            // current position's value coming from vnow, and adds it. The
+            // asm statements keep the compiler from sinking a read behind
+            // the current position's test.
+            auto read = [&](uint32_t pl, float (&v)[16], float4 (&w)[4]) {
+                const float* vp = vr + (size_t)pl * width;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = vp[(size_t)i * width];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) w[q] = *reinterpret_cast<const float4*>(wr + pl + 4u * q);
+            };
+            auto fold = [&](uint32_t pl, float (&v)[16], const float4 (&w)[4]) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(v[i]));
+                const int32_t at = cur - (int32_t)(p0 + pl);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float w4[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * q + e;
+                        const float prod = w4[e] * (i == at ? vnow : v[i]);
+                        acc += prod;
+                    }
+                }
+            };
+            uint32_t pl = 0;
+            if (cnt >= 32u) {
+                float va[16], vb2[16];
+                float4 wa[4], wb[4];
+                read(0, va, wa);
+                for (; pl + 48u <= cnt; pl += 32u) {
+                    read(pl + 16u, vb2, wb);
+                    fold(pl, va, wa);
+                    read(pl + 32u, va, wa);
+                    fold(pl + 16u, vb2, wb);
+                }
+                // va holds [pl, pl + 16)
+                if (pl + 32u <= cnt) {
+                    read(pl + 16u, vb2, wb);
+                    fold(pl, va, wa);
+                    fold(pl + 16u, vb2, wb);
+                    pl += 32u;
+                } else {
+                    fold(pl, va, wa);
+                    pl += 16u;
+                }
+            }
+            for (; pl < cnt; ++pl) {
+                const float vv = (int32_t)(p0 + pl) == cur ? vnow : vr[(size_t)pl * width];
+                const float prod = l.sc[p0 + pl] * vv;
+                acc += prod;
+            }
+        }
+    }
+    if (tid < width) l.out[tid] = acc;
+    lds_sync();
+}
+
 __global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite r) {
     extern __shared__ float4 lds4[];
-    const AttLds l = att_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
-    const uint32_t tid = threadIdx.x;
+    const AttDecodeLds l = att_decode_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t t = blockIdx.x / a.heads;
     const uint32_t h = blockIdx.x - t * a.heads;
     const uint32_t width = a.width;
@@ -463,14 +724,36 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite
         return;
     }
     const uint32_t group = a.heads / a.kv_heads, kv = h / group;
-    const uint32_t pos = (uint32_t)last, half = width >> 1;
+    const uint32_t pos = (uint32_t)last, half = width >> 1, w64 = (width + 63u) & ~63u;
     const float* src = r.x + (size_t)t * r.ldx;
-    const float* cs = r.cos + (size_t)pos * width;
-    const float* sn = r.sin + (size_t)pos * width;
-    const float* qs = src + (size_t)h * width;
-    const float* ks = src + (size_t)(a.heads + kv) * width;
-    const float* vs = src + (size_t)(a.heads + a.kv_heads + kv) * width;
     const size_t base = ((size_t)row * a.kv_heads + kv) * a.capacity * width;
+    const float* kb = a.keys + base;
+    const float* vb = a.values + base;
+    const uint32_t n = (uint32_t)length, cp = l.cp;
+
+    // Every load at once: wave 0 the head's rows and tables, then every
+    // wave its share of the first key chunk, then of the first value chunk.
+    const uint32_t stage = lds_address(l.stage);
+    if (wave == 0) {
+        stage_row(src + (size_t)h * width, width, stage);
+        stage_row(src + (size_t)(a.heads + kv) * width, width, stage + w64 * 4u);
+        stage_row(src + (size_t)(a.heads + a.kv_heads + kv) * width, width, stage + 2u * w64 * 4u);
+        stage_row(r.cos + (size_t)pos * width, width, stage + 3u * w64 * 4u);
+        stage_row(r.sin + (size_t)pos * width, width, stage + 4u * w64 * 4u);
+    }
+    const uint32_t kloads = stage_keys(kb, width, 0, min(cp, n), lds_address(l.kt), wave);
+    const uint32_t vloads = stage_values(vb, width, 0, min(cp, n), lds_address(l.vrows), wave);
+    wait_vm_lds_upto(kloads + vloads);  // wave 0: its staged rows
+    lds_sync();
+
+    // RoPE of q and k from the staged rows, the cache write of k and v by
+    // the first head of the group (host order: x·cos + (partner·-1 or
+    // partner)·sin).
+    const float* qs = l.stage;
+    const float* ks = l.stage + w64;
+    const float* vs = l.stage + 2u * w64;
+    const float* cs = l.stage + 3u * w64;
+    const float* sn = l.stage + 4u * w64;
     for (uint32_t c = tid; c < width; c += 256u) {
         const uint32_t o = c < half ? c + half : c - half;
         const float qp = qs[o], kp = ks[o];
@@ -487,14 +770,14 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite
             r.values[base + (size_t)pos * width + c] = v;
         }
     }
-    __syncthreads();
-    attend(l, a.keys + base, a.values + base, width, (uint32_t)length, last, last, a.scale);
-    emit(l, out, width, a.act, t, h, a.heads);
+    lds_sync();
+    attend_staged(l, kb, vb, width, n, last, last, a.scale, vloads);
+    emit(l.out, out, width, a.act, t, h, a.heads);
 }
 
 hipError_t launch_attention_decode(const Attention& a, const RopeWrite& r, uint32_t tokens, hipStream_t stream) {
     if (tokens == 0 || a.heads == 0) return hipSuccess;
-    const size_t lds = attention_lds(a.width, a.capacity);
+    const size_t lds = attention_decode_lds(a.width, a.capacity);
     hipLaunchKernelGGL(k_attention_decode, dim3(tokens * a.heads), dim3(256), lds, stream, a, r);
     return hipGetLastError();
 }

@@ -284,4 +284,28 @@ __device__ __forceinline__ void wait_vm_lds() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (7 << 4));
 }
 
+// wait_vm_lds<n> for a runtime n (at most 63; n past it waits for 63).
+template <uint32_t N = 63>
+__device__ __forceinline__ void wait_vm_lds_upto(uint32_t n) {
+    if constexpr (N == 0) {
+        wait_vm_lds<0>();
+    } else {
+        if (n >= N)
+            wait_vm_lds<N>();
+        else
+            wait_vm_lds_upto<N - 1>(n);
+    }
+}
+
+// A workgroup barrier after this wave's LDS (and scalar memory) operations,
+// leaving its direct loads in flight: __syncthreads() would wait for them.
+// The empty asm statements keep the compiler from moving memory operations
+// across it.
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("" ::: "memory");
+    wait_vm_lds<63>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 }  // namespace tmh

@@ -198,6 +198,7 @@ struct Attention {
     Activations act;  // with qs set, the outputs are also quantised here (width a multiple of 32)
 };
 size_t attention_lds(uint32_t width, uint32_t capacity);
+size_t attention_decode_lds(uint32_t width, uint32_t capacity);  // of launch_attention_decode
 hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream);
 // A decode step's attention with the RoPE and cache write of `r` fused: each
 // token is its cache row's one new position.
