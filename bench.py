@@ -182,9 +182,18 @@ def main():
         plans.append(dev.plan("Q4_0", plan_items))
     dev.sync()
 
-    # Warm-up, then the timed region: K launches back to back.
-    for s in range(args.warmup):
-        plans[s % copies].run()
+    # Warm-up, then the timed region: K launches back to back. The warm-up is
+    # W launches, continued until they have kept the GPU busy for at least
+    # 50 ms: the set takes ~16 us, and after the host-side set-up the GPU's
+    # clocks need that long to settle (20 launches leave the mean ~1 us high).
+    warm = 0
+    t_warm = time.perf_counter()
+    while warm < args.warmup or time.perf_counter() - t_warm < 0.05:
+        for _ in range(100 if warm >= args.warmup else 1):
+            plans[warm % copies].run()
+            warm += 1
+        if warm >= args.warmup:
+            dev.sync()
     dev.sync()
     # HIP events on the library's stream bracket the K launches (one launch
     # per step, back to back): their mean is the kernel's launch duration.
@@ -254,6 +263,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles(),
             "launch_us_mean": round(launch_ms * 1e3, 2),
+            "warmup_launches": warm,
         },
         "per_product_launches": {
             "ms_per_token": round(per_product_ms, 4),

@@ -101,6 +101,73 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantise(const float* __restric
     rmsnorm_quantise_row(x + (size_t)blockIdx.x * ldx, n, w, eps, act, blockIdx.x, row, row + n);
 }
 
+// k_rmsnorm_quantise for a row whose squares (each x·x rounded, as the
+// product that wrote x writes them) are in memory beside it: wave 0 folds
+// them in index order from scalar registers (ordered_sum_scalar) while every
+// thread loads its own values and weights, then each 8-lane group
+// normalises and quantises its blocks of 32 as rmsnorm_quantise_row does.
+__global__ __launch_bounds__(256) void k_rmsnorm_quantise_squares(const float* __restrict__ x, uint32_t ldx,
+                                                                  const float* __restrict__ squares,
+                                                                  const float* __restrict__ w, uint32_t n, float eps,
+                                                                  Activations act) {
+    __shared__ float root_slot;
+    constexpr uint32_t PASSES = RMSNORM_LDS_ROW / 1024u;
+    const uint32_t r = blockIdx.x, nb = n >> 5, sub = threadIdx.x & 7u;
+    const float* xr = x + (size_t)r * ldx;
+    float4 xv[PASSES], wv[PASSES];
+#pragma unroll
+    for (uint32_t pass = 0; pass < PASSES; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        const uint32_t j = blk * 32u + sub * 4u;
+        xv[pass] = blk < nb ? *reinterpret_cast<const float4*>(xr + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        wv[pass] = (w && blk < nb) ? *reinterpret_cast<const float4*>(w + j) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    const float* sr = squares + (size_t)r * ldx;
+    if (threadIdx.x < 64u) {
+        const float total = ordered_sum_scalar(sr, n);
+        if (threadIdx.x == 0) root_slot = __builtin_sqrtf(total / (float)n + eps);
+    } else {
+        // The squares were written from every XCD: waves 1-3 read them once
+        // with vector loads (all in flight together), which brings them into
+        // this XCD's L2 ahead of wave 0's scalar loads -- each of those would
+        // otherwise wait a memory round trip per batch.
+        constexpr uint32_t LOADS = (RMSNORM_LDS_ROW / 4u + 191u) / 192u;
+        const float4* s4 = reinterpret_cast<const float4*>(sr);
+        float v[LOADS];
+#pragma unroll
+        for (uint32_t i = 0; i < LOADS; ++i) {
+            const uint32_t j = threadIdx.x - 64u + 192u * i;
+            v[i] = j < (n >> 2) ? s4[j].x : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < LOADS; ++i) asm volatile("" ::"v"(v[i]));
+    }
+    __syncthreads();
+    const float root = root_slot;
+#pragma unroll
+    for (uint32_t pass = 0; pass < PASSES; ++pass) {
+        const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;
+        if (blk >= nb) break;
+        const uint32_t j = blk * 32u + sub * 4u;
+        const float xj[4] = {xv[pass].x, xv[pass].y, xv[pass].z, xv[pass].w};
+        const float wj[4] = {wv[pass].x, wv[pass].y, wv[pass].z, wv[pass].w};
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q = xj[i] / root;
+            v[i] = w ? q * wj[i] : q;
+        }
+        const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+        *(uint32_t*)((int8_t*)act.qs + (size_t)r * n + j) = q.packed;
+        if (sub == 0) {
+            const size_t g = (size_t)r * nb + blk;
+            ((float*)act.scales)[g] = q.scale;
+            ((float*)act.sums)[g] = q.sum;
+            ((int32_t*)act.totals)[g] = q.total;
+        }
+    }
+}
+
 // Rows too wide for LDS: the fold reads the row from memory (one cache line
 // feeds 32 steps of every lane).
 __global__ __launch_bounds__(256) void k_rmsnorm_wide(const float* __restrict__ x, uint32_t ldx,
@@ -132,9 +199,14 @@ hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t
 bool rmsnorm_quantise_fits(uint32_t n) { return n > 0 && n % 32u == 0 && n <= RMSNORM_LDS_ROW; }
 
 hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
-                                   Activations act, hipStream_t stream) {
+                                   Activations act, hipStream_t stream, const float* squares) {
     if (rows == 0) return hipSuccess;
     if (!rmsnorm_quantise_fits(n)) return hipErrorInvalidValue;
+    if (squares) {
+        hipLaunchKernelGGL(k_rmsnorm_quantise_squares, dim3(rows), dim3(256), 0, stream, x, ldx, squares, w, n, eps,
+                           act);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_rmsnorm_quantise, dim3(rows), dim3(256), 2u * (size_t)n * sizeof(float), stream, x, ldx, w,
                        n, eps, act);
     return hipGetLastError();
