@@ -31,38 +31,6 @@
 
 namespace tmh {
 
-// ---------------------------------------------------------------- Maths.exp
-
-// Maths.exp (maths.cr:36-54): x = n·ln2 + r with n = round(x·log2 e) by the
-// 1.5·2^23 rounder, r in two steps (ln2 split into a high and a low part),
-// a degree-6 polynomial in r, then 2^n as two exponent halves; inf above
-// 88.72, 0 below -87.34, NaN kept.
-__device__ __forceinline__ float maths_exp(float x) {
-    const float LOG2E = 1.44269504088896341f, LN2_HI = 0.693359375f, LN2_LO = -2.12194440e-4f;
-    const float EXP_HI = 88.72283905f, EXP_LO = -87.3365447f, ROUNDER = 12582912.0f;
-    const float clamped = (x > EXP_HI || x < EXP_LO) ? 0.0f : x;
-    float n = clamped * LOG2E;
-    n = n + ROUNDER;
-    n = n - ROUNDER;
-    float r = clamped - n * LN2_HI;
-    r = r - n * LN2_LO;
-    const float z = r * r;
-    float p = 1.9875691500e-4f;
-    p = p * r + 1.3981999507e-3f;
-    p = p * r + 8.3334519073e-3f;
-    p = p * r + 4.1665795894e-2f;
-    p = p * r + 1.6666665459e-1f;
-    p = p * r + 5.0000001201e-1f;
-    p = p * z + r;
-    p = p + 1.0f;
-    const int32_t whole = (int32_t)n;
-    const int32_t half = whole >> 1;
-    float result = p * __uint_as_float((uint32_t)(half + 127) << 23);
-    result = result * __uint_as_float((uint32_t)(whole - half + 127) << 23);
-    result = x > EXP_HI ? __builtin_inff() : result;
-    result = x < EXP_LO ? 0.0f : result;
-    return x != x ? x : result;
-}
 
 __device__ __forceinline__ void report(int32_t* errors, int32_t value, int32_t limit) {
     if (atomicAdd(&errors[0], 1) == 0) {
@@ -862,11 +830,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ gate, 
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= total) return;
     const uint32_t r = i / n, j = i - r * n;
-    const float g = gate[(size_t)r * ld + j];
-    const float e = maths_exp(-g);
-    const float d = e + 1.0f;
-    const float q = g / d;
-    dst[i] = q * value[(size_t)r * ld + j];
+    dst[i] = swiglu_value(gate[(size_t)r * ld + j], value[(size_t)r * ld + j]);
 }
 
 // SwiGLU then the activation quantiser: each 8-lane group takes a block of
@@ -883,13 +847,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quantise(const float* __restrict
     const uint32_t j = blk * 32u + sub * 4u;
     float v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float gt = gate[(size_t)r * ld + j + i];
-        const float e = maths_exp(-gt);
-        const float d = e + 1.0f;
-        const float q = gt / d;
-        v[i] = q * value[(size_t)r * ld + j + i];
-    }
+    for (int i = 0; i < 4; ++i) v[i] = swiglu_value(gate[(size_t)r * ld + j + i], value[(size_t)r * ld + j + i]);
     const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
     *(uint32_t*)((int8_t*)act.qs + (size_t)r * n + j) = q.packed;
     if (sub == 0) {

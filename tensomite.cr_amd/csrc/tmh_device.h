@@ -97,6 +97,47 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
     return out;
 }
 
+// ---------------------------------------------------------------- Maths.exp
+
+// Maths.exp (maths.cr:36-54): x = n·ln2 + r with n = round(x·log2 e) by the
+// 1.5·2^23 rounder, r in two steps (ln2 split into a high and a low part),
+// a degree-6 polynomial in r, then 2^n as two exponent halves; inf above
+// 88.72, 0 below -87.34, NaN kept.
+__device__ __forceinline__ float maths_exp(float x) {
+    const float LOG2E = 1.44269504088896341f, LN2_HI = 0.693359375f, LN2_LO = -2.12194440e-4f;
+    const float EXP_HI = 88.72283905f, EXP_LO = -87.3365447f, ROUNDER = 12582912.0f;
+    const float clamped = (x > EXP_HI || x < EXP_LO) ? 0.0f : x;
+    float n = clamped * LOG2E;
+    n = n + ROUNDER;
+    n = n - ROUNDER;
+    float r = clamped - n * LN2_HI;
+    r = r - n * LN2_LO;
+    const float z = r * r;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * z + r;
+    p = p + 1.0f;
+    const int32_t whole = (int32_t)n;
+    const int32_t half = whole >> 1;
+    float result = p * __uint_as_float((uint32_t)(half + 127) << 23);
+    result = result * __uint_as_float((uint32_t)(whole - half + 127) << 23);
+    result = x > EXP_HI ? __builtin_inff() : result;
+    result = x < EXP_LO ? 0.0f : result;
+    return x != x ? x : result;
+}
+
+// SwiGLU of one element (kernels.cr:18): gate / (Maths.exp(-gate) + 1) · value.
+__device__ __forceinline__ float swiglu_value(float gate, float value) {
+    const float e = maths_exp(-gate);
+    const float d = e + 1.0f;
+    const float q = gate / d;
+    return q * value;
+}
+
 // ------------------------------------------------------------ ordered sums
 
 // Σ v[0..n) in index order from 0.0f (with SQ, Σ v[i]·v[i], each square

@@ -156,6 +156,15 @@ hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations 
                                    uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream,
                                    float* squares = nullptr);
 
+// SwiGLU(act · gateᵀ, act · upᵀ) quantised into `glu` ([rows, H] as the
+// quantise pass lays it out), one launch per group of rows: w is the merged
+// [gate | up] matrix of 2·H rows, the lanes product folds each output in
+// block order and its epilogue applies SwiGLU and the quantiser, with the
+// bits of a product, k_swiglu_quantise's arithmetic and a quantise pass.
+// hipErrorInvalidValue when the shape is not for that kernel.
+hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations act, uint32_t rows, uint32_t H,
+                                 uint32_t k, Activations glu, hipStream_t stream);
+
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);

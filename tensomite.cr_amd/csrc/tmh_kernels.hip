@@ -273,11 +273,19 @@ __device__ __forceinline__ void load_activations(const Activations& act, uint32_
 // -- the host's order -- and writes it, plus the bias; with sq, also the
 // output's square (each rounded, as a later Σx² would square it) at the
 // same index of sq.
-template <int KIND, int NB>
+//
+// GLU: w is a merged [gate | up] matrix of n = 2·H rows, and the tile's tr
+// rows are gate rows tile·tr/2 .. + tr/2 then the up rows of the same
+// indices (tr/2 a multiple of 32). The folded outputs stay in LDS; then
+// each 8-lane group takes a block of 32 of them, SwiGLU
+// (gate / (Maths.exp(-gate) + 1) · up) 4 a lane, and quantises the block
+// into `glu` as the quantise pass lays out an [NB, H] activation.
+template <int KIND, int NB, bool GLU = false>
 __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst,
                                             const float* __restrict__ bias, uint32_t bias_ld,
                                             float* __restrict__ sq, uint32_t n, uint32_t k,
-                                            uint32_t tr, uint32_t stride, uint32_t tile, float* part) {
+                                            uint32_t tr, uint32_t stride, uint32_t tile, float* part,
+                                            Activations glu = Activations{}) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
@@ -288,6 +296,9 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
     const uint32_t steps = tr / rpi;
     const size_t row_words = (size_t)np * PW;
     const uint32_t* wp = (const uint32_t*)w;
+    // GLU: output r of the tile is gate row g0 + r, or up row H + g0 + r - h
+    const uint32_t h = tr >> 1, H = n >> 1, g0 = tile * h;
+    auto row_of = [&](uint32_t r) -> uint32_t { return GLU ? (r < h ? g0 + r : H + g0 + (r - h)) : row0 + r; };
 
     if (rsub < rpi) {
         // This thread's pair of every activation row, held in registers for
@@ -304,8 +315,8 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
 #pragma unroll 2
         for (uint32_t s = 0; s < steps; ++s) {
             const uint32_t r = s * rpi + rsub;
-            const uint32_t row = row0 + r;
-            if (row >= n) break;
+            const uint32_t row = row_of(r);
+            if (!GLU && row >= n) break;
             uint32_t u[PW];
             load_pair<KIND>(wp + (size_t)row * row_words + (size_t)j * PW, u);
 #pragma unroll
@@ -317,10 +328,11 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
         }
     }
     __syncthreads();
+    float* outs = part + (size_t)NB * tr * stride;  // GLU: the tile's outputs, [NB][tr]
     for (uint32_t o = t; o < (uint32_t)NB * tr; o += 256u) {
         const uint32_t b = o / tr, r = o - b * tr;
-        const uint32_t row = row0 + r;
-        if (row < n) {
+        const uint32_t row = row_of(r);
+        if (GLU || row < n) {
             const float* c = part + (size_t)o * stride;
             float sum = 0.0f;
             uint32_t i = 0;
@@ -332,9 +344,35 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
                 sum += v.w;
             }
             for (; i < nb; ++i) sum += c[i];
-            const float v = bias ? sum + bias[(size_t)b * bias_ld + row] : sum;
-            dst[(size_t)b * n + row] = v;
-            if (sq) sq[(size_t)b * n + row] = v * v;
+            if constexpr (GLU) {
+                outs[o] = sum;
+            } else {
+                const float v = bias ? sum + bias[(size_t)b * bias_ld + row] : sum;
+                dst[(size_t)b * n + row] = v;
+                if (sq) sq[(size_t)b * n + row] = v * v;
+            }
+        }
+    }
+    if constexpr (GLU) {
+        __syncthreads();
+        // blocks of 32 outputs: NB rows x h / 32; every lane of a group takes
+        // the same trip count (quantize_quad reduces across the 8 lanes)
+        const uint32_t hb = h >> 5, sub = t & 7u, Hb = H >> 5;
+        for (uint32_t g = t >> 3; g < (uint32_t)NB * hb; g += 32u) {
+            const uint32_t b = g / hb, blk = g - b * hb;
+            const float* gate = outs + (size_t)b * tr + blk * 32u + sub * 4u;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = swiglu_value(gate[i], gate[h + i]);
+            const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+            const uint32_t col = g0 + blk * 32u + sub * 4u;
+            *(uint32_t*)((int8_t*)glu.qs + (size_t)b * H + col) = q.packed;
+            if (sub == 0) {
+                const size_t at = (size_t)b * Hb + (g0 >> 5) + blk;
+                ((float*)glu.scales)[at] = q.scale;
+                ((float*)glu.sums)[at] = q.sum;
+                ((int32_t*)glu.totals)[at] = q.total;
+            }
         }
     }
 }
@@ -349,6 +387,16 @@ __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, A
                                                 uint32_t tr, uint32_t stride) {
     extern __shared__ float part[];
     matvec_tile<KIND, NB>(w, act, dst, bias, bias_ld, sq, n, k, tr, stride, blockIdx.x, part);
+}
+
+// The lanes product over a merged [gate | up] matrix with SwiGLU and the
+// activation quantiser in its epilogue (matvec_tile's GLU form): `glu`
+// receives quantised SwiGLU(gate, up) rows of n / 2.
+template <int KIND, int NB>
+__global__ __launch_bounds__(256) void k_matvec_glu(const uint8_t* __restrict__ w, Activations act, uint32_t n,
+                                                    uint32_t k, uint32_t tr, uint32_t stride, Activations glu) {
+    extern __shared__ float part[];
+    matvec_tile<KIND, NB, true>(w, act, nullptr, nullptr, 0, nullptr, n, k, tr, stride, blockIdx.x, part, glu);
 }
 
 
@@ -1759,6 +1807,66 @@ hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations 
     case 0: return launch_lanes<0>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
     case 1: return launch_lanes<1>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
     default: return launch_lanes<2>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
+    }
+}
+
+// The GLU tile: h gate rows and the h up rows of the same indices, h a
+// multiple of 32 (whole quantisation blocks) and 2h a multiple of the rows
+// one step of the lanes kernel covers (256 / pairs per row, a power of two).
+static uint32_t glu_half(uint32_t nb) { return std::max(32u, (256u / (nb / 2u)) / 2u); }
+
+static size_t glu_lds(uint32_t nbatch, uint32_t nb) {
+    const size_t tr = 2u * glu_half(nb);
+    return ((size_t)nbatch * tr * lanes_stride(nb) + (size_t)nbatch * tr) * sizeof(float);
+}
+
+template <int KIND, int NB>
+static hipError_t launch_glu_nb(const uint8_t* w, Activations act, uint32_t H, uint32_t k, Activations glu,
+                                hipStream_t stream) {
+    const uint32_t nb = k >> 5, h = glu_half(nb);
+    hipLaunchKernelGGL((k_matvec_glu<KIND, NB>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H, k,
+                       2u * h, lanes_stride(nb), glu);
+    return hipGetLastError();
+}
+
+template <int KIND>
+static hipError_t launch_glu(const uint8_t* w, Activations act, uint32_t rows, uint32_t H, uint32_t k,
+                             Activations glu, hipStream_t stream) {
+    const uint32_t nb = k >> 5, hb = H >> 5;
+    uint32_t done = 0;
+    while (done < rows) {
+        const uint32_t left = rows - done;
+        Activations a = act, g = glu;
+        a.scales += (size_t)done * nb;
+        a.sums += (size_t)done * nb;
+        a.totals += (size_t)done * nb;
+        a.qs += (size_t)done * k;
+        g.scales += (size_t)done * hb;
+        g.sums += (size_t)done * hb;
+        g.totals += (size_t)done * hb;
+        g.qs += (size_t)done * H;
+        hipError_t err;
+        uint32_t take;
+        if (left >= 8 && glu_lds(8, nb) <= CU_LDS) err = launch_glu_nb<KIND, 8>(w, a, H, k, g, stream), take = 8;
+        else if (left >= 4 && glu_lds(4, nb) <= CU_LDS) err = launch_glu_nb<KIND, 4>(w, a, H, k, g, stream), take = 4;
+        else if (left >= 2 && glu_lds(2, nb) <= CU_LDS) err = launch_glu_nb<KIND, 2>(w, a, H, k, g, stream), take = 2;
+        else err = launch_glu_nb<KIND, 1>(w, a, H, k, g, stream), take = 1;
+        if (err != hipSuccess) return err;
+        done += take;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations act, uint32_t rows, uint32_t H,
+                                 uint32_t k, Activations glu, hipStream_t stream) {
+    if (rows == 0 || H == 0) return hipSuccess;
+    if (!lanes_fit(w, k) || rows >= MATRIX_ROWS) return hipErrorInvalidValue;
+    const uint32_t nb = k >> 5, np = nb / 2u;
+    if ((np & (np - 1u)) != 0 || H % glu_half(nb) != 0 || glu_lds(1, nb) > CU_LDS) return hipErrorInvalidValue;
+    switch (kind) {
+    case 0: return launch_glu<0>(w, act, rows, H, k, glu, stream);
+    case 1: return launch_glu<1>(w, act, rows, H, k, glu, stream);
+    default: return launch_glu<2>(w, act, rows, H, k, glu, stream);
     }
 }
 

@@ -162,9 +162,19 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
         if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur, squared);
         if (e == hipSuccess)
             e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in, squared ? m.squares : nullptr);
-        if (e == hipSuccess) e = product(m, ctx, m.gate_up[l], a_in, tokens, 2u * H, W, m.gu, nullptr);
         const tmh::Activations a_hid = tmh::carve_scratch(m.scratch[1], tokens, H);
-        if (e == hipSuccess) e = tmh::launch_swiglu_quantise(m.gu, m.gu + H, 2u * H, tokens, H, a_hid, ctx.stream);
+        if (e == hipSuccess) {
+            // gate_up with SwiGLU and the quantiser in its epilogue where the
+            // shape allows, else the product then SwiGLU+quantise
+            hipError_t g = tmh::launch_gate_up_swiglu(c.kind, m.gate_up[l], a_in, tokens, H, W, a_hid, ctx.stream);
+            if (g == hipErrorInvalidValue) {
+                e = product(m, ctx, m.gate_up[l], a_in, tokens, 2u * H, W, m.gu, nullptr);
+                if (e == hipSuccess)
+                    e = tmh::launch_swiglu_quantise(m.gu, m.gu + H, 2u * H, tokens, H, a_hid, ctx.stream);
+            } else {
+                e = g;
+            }
+        }
         if (e == hipSuccess) e = residual(m, ctx, m.down[l], a_hid, tokens, H, cur, squared);
     }
     const tmh::Activations a_fin = tmh::carve_scratch(m.scratch[0], final_rows, W);
