@@ -39,15 +39,14 @@ __device__ __forceinline__ void report(int32_t* errors, int32_t value, int32_t l
     }
 }
 
-// One workgroup per row: the squares in parallel, their ordered sum, then
-// x / root · w in parallel.
+// One workgroup per row: the row staged in LDS, the ordered sum of its
+// squares by wave 0, then x / root · w in parallel.
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, uint32_t ldx,
                                                  const float* __restrict__ w, uint32_t n, float eps,
                                                  float* __restrict__ dst, uint32_t ld_dst) {
     extern __shared__ float4 lds4[];
     float* row = reinterpret_cast<float*>(lds4);
-    float* sq = row + ((n + 3u) & ~3u);
-    const float root = stage_root(x + (size_t)blockIdx.x * ldx, n, eps, row, sq);
+    const float root = stage_root(x + (size_t)blockIdx.x * ldx, n, eps, row);
     float* out = dst + (size_t)blockIdx.x * ld_dst;
     if (w) {
         for (uint32_t j = threadIdx.x; j < n; j += 256u) {
@@ -66,18 +65,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantise(const float* __restric
                                                           Activations act) {
     extern __shared__ float4 lds4[];
     float* row = reinterpret_cast<float*>(lds4);
-    rmsnorm_quantise_row(x + (size_t)blockIdx.x * ldx, n, w, eps, act, blockIdx.x, row, row + n);
+    rmsnorm_quantise_row(x + (size_t)blockIdx.x * ldx, n, w, eps, act, blockIdx.x, row);
 }
 
-// k_rmsnorm_quantise for a row whose squares (each x·x rounded, as the
-// product that wrote x writes them) are in memory beside it: wave 0 folds
-// them in index order from scalar registers (ordered_sum_scalar) while every
-// thread loads its own values and weights, then each 8-lane group
-// normalises and quantises its blocks of 32 as rmsnorm_quantise_row does.
-__global__ __launch_bounds__(256) void k_rmsnorm_quantise_squares(const float* __restrict__ x, uint32_t ldx,
-                                                                  const float* __restrict__ squares,
-                                                                  const float* __restrict__ w, uint32_t n, float eps,
-                                                                  Activations act) {
+// RMSNorm then the activation quantiser, one workgroup per row, with Σx²
+// folded by speculation (ordered_sum_wave): wave 0's lane c loads and
+// squares values [c·M, c·M + M) of the row while every thread loads its own
+// values and weights; then each 8-lane group normalises and quantises its
+// blocks of 32 as rmsnorm_quantise_row does (the same bits: the squares
+// each rounded, their sum in index order from 0, sqrtf(Σ/n + ε)).
+template <int M>
+__global__ __launch_bounds__(256) void k_rmsnorm_quantise_wave(const float* __restrict__ x, uint32_t ldx,
+                                                               const float* __restrict__ w, uint32_t n, float eps,
+                                                               Activations act) {
     __shared__ float root_slot;
     constexpr uint32_t PASSES = RMSNORM_LDS_ROW / 1024u;
     const uint32_t r = blockIdx.x, nb = n >> 5, sub = threadIdx.x & 7u;
@@ -90,25 +90,20 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantise_squares(const float* _
         xv[pass] = blk < nb ? *reinterpret_cast<const float4*>(xr + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         wv[pass] = (w && blk < nb) ? *reinterpret_cast<const float4*>(w + j) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    const float* sr = squares + (size_t)r * ldx;
     if (threadIdx.x < 64u) {
-        const float total = ordered_sum_scalar(sr, n);
-        if (threadIdx.x == 0) root_slot = __builtin_sqrtf(total / (float)n + eps);
-    } else {
-        // The squares were written from every XCD: waves 1-3 read them once
-        // with vector loads (all in flight together), which brings them into
-        // this XCD's L2 ahead of wave 0's scalar loads -- each of those would
-        // otherwise wait a memory round trip per batch.
-        constexpr uint32_t LOADS = (RMSNORM_LDS_ROW / 4u + 191u) / 192u;
-        const float4* s4 = reinterpret_cast<const float4*>(sr);
-        float v[LOADS];
+        float v[M];
+        const uint32_t c0 = threadIdx.x * (uint32_t)M;
 #pragma unroll
-        for (uint32_t i = 0; i < LOADS; ++i) {
-            const uint32_t j = threadIdx.x - 64u + 192u * i;
-            v[i] = j < (n >> 2) ? s4[j].x : 0.0f;
+        for (int i = 0; i < M; i += 4) {
+            const float4 q = c0 + i < n ? *reinterpret_cast<const float4*>(xr + c0 + i)
+                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            v[i] = q.x * q.x;
+            v[i + 1] = q.y * q.y;
+            v[i + 2] = q.z * q.z;
+            v[i + 3] = q.w * q.w;
         }
-#pragma unroll
-        for (uint32_t i = 0; i < LOADS; ++i) asm volatile("" ::"v"(v[i]));
+        const float total = ordered_sum_wave<M>(v);
+        if (threadIdx.x == 0) root_slot = __builtin_sqrtf(total / (float)n + eps);
     }
     __syncthreads();
     const float root = root_slot;
@@ -156,7 +151,7 @@ hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t
                           float* dst, uint32_t ld_dst, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (n <= RMSNORM_LDS_ROW) {
-        const size_t lds = 2u * (((size_t)n + 3u) & ~(size_t)3u) * sizeof(float);
+        const size_t lds = (((size_t)n + 3u) & ~(size_t)3u) * sizeof(float);
         hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), lds, stream, x, ldx, w, n, eps, dst, ld_dst);
     } else {
         hipLaunchKernelGGL(k_rmsnorm_wide, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, dst, ld_dst);
@@ -167,15 +162,19 @@ hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t
 bool rmsnorm_quantise_fits(uint32_t n) { return n > 0 && n % 32u == 0 && n <= RMSNORM_LDS_ROW; }
 
 hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
-                                   Activations act, hipStream_t stream, const float* squares) {
+                                   Activations act, hipStream_t stream) {
     if (rows == 0) return hipSuccess;
     if (!rmsnorm_quantise_fits(n)) return hipErrorInvalidValue;
-    if (squares) {
-        hipLaunchKernelGGL(k_rmsnorm_quantise_squares, dim3(rows), dim3(256), 0, stream, x, ldx, squares, w, n, eps,
-                           act);
+    if (ldx % 4u == 0 && ((uintptr_t)x & 15u) == 0 && (!w || ((uintptr_t)w & 15u) == 0)) {
+        if (n <= 64u * 8u)
+            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<8>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
+        else if (n <= 64u * 32u)
+            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<32>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
+        else
+            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<128>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_rmsnorm_quantise, dim3(rows), dim3(256), 2u * (size_t)n * sizeof(float), stream, x, ldx, w,
+    hipLaunchKernelGGL(k_rmsnorm_quantise, dim3(rows), dim3(256), (size_t)n * sizeof(float), stream, x, ldx, w,
                        n, eps, act);
     return hipGetLastError();
 }
@@ -666,7 +665,10 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     if (l.sc[0] != l.sc[0]) top = l.sc[0];  // the host's top is a NaN at position 0
     for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = maths_exp(l.sc[p] - top);
     lds_sync();
-    if (tid == 0) total_slot = ordered_sum(l.sc, n);
+    if (tid < 64u) {
+        const float sum = n <= WAVE_SUM_MAX ? ordered_sum_by_wave(l.sc, n) : ordered_sum(l.sc, n);
+        if (tid == 0) total_slot = sum;
+    }
     lds_sync();
     const float total = total_slot;
     for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = l.sc[p] / total;

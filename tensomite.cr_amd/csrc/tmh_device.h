@@ -204,81 +204,117 @@ __device__ __forceinline__ float ordered_sum(const float* v, uint32_t n) {
     return s;
 }
 
-// ordered_sum of memory that the kernel never writes, at a wave-uniform
-// address: the compiler then reads it with scalar loads (16 values an
-// instruction) and each add takes its value straight from a scalar
-// register, so the dependent chain is nearly all the wave issues (≈6
-// cycles an add, against ≈8.5 when each value comes through LDS). Scalar
-// loads may complete out of order, so the only wait is for all of them:
-// the wait for one batch of B values comes before the next batch's loads
-// are issued, and those arrive while the B adds run.
-template <int B>
-__device__ __forceinline__ void scalar_batch(float (&a)[B], const float* __restrict__ v) {
+// ------------------------------------------- ordered sums by speculation
+
+// DPP moves across a wave64 (gfx9 controls): lane l receives lane l-1's value
+// (wave_shr:1; lane 0 receives 0), and an inclusive prefix sum (row_shr 1, 2,
+// 4, 8 within rows of 16, then row_bcast:15 and row_bcast:31 across rows).
+__device__ __forceinline__ float wave_shift_up(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x138, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xF, 0xF, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xF, 0xF, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xF, 0xF, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xF, 0xF, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xC, 0xF, false));
+    return x;
+}
+
+// Σ of 64·M values in index order from +0.0f -- the sequential fold's own
+// bits -- by one whole wave, lane c holding values [c·M, c·M + M) in v.
+// Each pass, every lane folds its M values in order from a start S_c (lane
+// 0 from +0.0f) to an end E_c. If every S_c equals E_{c-1} bit for bit, the
+// starts are the sequential fold's values at the chunk boundaries (by
+// induction from lane 0), so E_63 is the sum. Otherwise each start is
+// re-guessed as E_{c-1} plus the sum of the mismatches E_{j-1} - S_j of
+// the lanes before it (within one binade of the running sum a start that
+// is off by some ulps moves the end by the same amount), and the pass
+// repeats. The first mismatching lane always receives its predecessor's
+// exact end unchanged, so every pass fixes at least one more lane and 64
+// passes bound the loop; typically 2-8 are needed (more when the running
+// sum crosses many binades, or at exact ties).
+template <int M>
+__device__ __forceinline__ float ordered_sum_wave(const float (&v)[M]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    float start = 0.0f, end = 0.0f;
+    bool verified = false;
+    for (int pass = 0; pass <= 64; ++pass) {
+        end = start;
 #pragma unroll
-    for (int i = 0; i < B; ++i) a[i] = v[i];
-}
-
-template <int B>
-__device__ __forceinline__ void scalar_adds(float& s, const float (&a)[B]) {
-#pragma unroll
-    for (int i = 0; i < B; ++i) s += a[i];
-}
-
-__device__ __forceinline__ void wait_scalar_loads() {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int B = 32>
-__device__ __forceinline__ float ordered_sum_scalar(const float* __restrict__ v, uint32_t n) {
-    float s = 0.0f;
-    uint32_t j = 0;
-    if (n >= 2u * B) {
-        float a[B], b[B];
-        scalar_batch<B>(a, v);
-        for (; j + 3u * B <= n; j += 2u * B) {
-            wait_scalar_loads();
-            scalar_batch<B>(b, v + j + B);
-            __builtin_amdgcn_sched_barrier(0);
-            scalar_adds<B>(s, a);
-            wait_scalar_loads();
-            scalar_batch<B>(a, v + j + 2u * B);
-            __builtin_amdgcn_sched_barrier(0);
-            scalar_adds<B>(s, b);
+        for (int i = 0; i < M; ++i) end += v[i];
+        const float prev = wave_shift_up(end);
+        const bool ok = lane == 0 || __float_as_uint(prev) == __float_as_uint(start);
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+            verified = true;
+            break;
         }
-        // a holds [j, j + B)
-        wait_scalar_loads();
-        scalar_adds<B>(s, a);
-        j += B;
+        const float miss = ok ? 0.0f : prev - start;
+        const float before = wave_shift_up(wave_prefix_sum(miss));
+        start = lane == 0 ? 0.0f : (before == 0.0f ? prev : prev + before);
     }
-    for (; j + B <= n; j += B) {
-        float a[B];
-        scalar_batch<B>(a, v + j);
-        scalar_adds<B>(s, a);
+    if (!verified) {
+        // not reached (the bound above suffices); the plain fold, lane by lane
+        float sum = 0.0f;
+        for (uint32_t c = 0; c < 64u; ++c)
+            for (int i = 0; i < M; ++i) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), c));
+        return sum;
     }
-    for (; j < n; ++j) s += v[j];
-    return s;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(end), 63));
 }
 
-// ordered_sum by one lane (an LDS read then feeds one lane, not 256), the
-// result shared through LDS. Every thread calls it.
+// ordered_sum_wave over v[0..n) (SQ: the squares v[i]·v[i], each rounded),
+// lane c loading values [c·M, c·M + M); positions past n hold +0.0f, whose
+// adds leave a running sum from +0.0f unchanged.
+template <bool SQ, int M>
+__device__ __forceinline__ float ordered_sum_wave_m(const float* v, uint32_t n) {
+    float a[M];
+    const uint32_t c0 = (threadIdx.x & 63u) * (uint32_t)M;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const uint32_t j = c0 + (uint32_t)i;
+        const float x = j < n ? v[j] : 0.0f;
+        a[i] = SQ ? x * x : x;
+    }
+    return ordered_sum_wave<M>(a);
+}
+
+// Largest n the wave fold takes (64 lanes x 128 values).
+constexpr uint32_t WAVE_SUM_MAX = 8192;
+
+// Σ v[0..n) in index order from +0.0f (SQ: Σ v[i]·v[i]) by one whole wave:
+// every lane of the wave calls it with the same v and n (n <= WAVE_SUM_MAX)
+// and receives the sum.
+template <bool SQ = false>
+__device__ __forceinline__ float ordered_sum_by_wave(const float* v, uint32_t n) {
+    if (n <= 64u * 8u) return ordered_sum_wave_m<SQ, 8>(v, n);
+    if (n <= 64u * 32u) return ordered_sum_wave_m<SQ, 32>(v, n);
+    return ordered_sum_wave_m<SQ, 128>(v, n);
+}
+
+// The ordered sum of v[0..n) by wave 0 (ordered_sum_by_wave; beyond its
+// limit, ordered_sum), shared through LDS. Every thread calls it.
 __device__ __forceinline__ float shared_sum(const float* v, uint32_t n) {
     __shared__ float result;
-    if (threadIdx.x == 0) result = ordered_sum(v, n);
+    if (threadIdx.x < 64u) {
+        const float sum = n <= WAVE_SUM_MAX ? ordered_sum_by_wave(v, n) : ordered_sum(v, n);
+        if (threadIdx.x == 0) result = sum;
+    }
     __syncthreads();
     return result;
 }
 
 // ------------------------------------------------------------------ RMSNorm
 
-// Largest row the LDS kernels stage: the row and its squares, 64 KB.
+// Largest row the LDS kernels stage: 32 KB.
 constexpr uint32_t RMSNORM_LDS_ROW = 8192;
 
-// Stages row x (n values) and its squares in LDS, then returns the root
-// sqrt(Σx²/n + eps), the squares folded in index order by every wave.
-__device__ __forceinline__ float stage_root(const float* __restrict__ xr, uint32_t n, float eps, float* row,
-                                            float* sq) {
+// Stages row x (n values, at most RMSNORM_LDS_ROW) in LDS, then returns the
+// root sqrt(Σx²/n + eps), the squares folded in index order by wave 0
+// (ordered_sum_by_wave) and shared through LDS. Every thread calls it.
+__device__ __forceinline__ float stage_root(const float* __restrict__ xr, uint32_t n, float eps, float* row) {
     // four loads in flight per thread before any store
     for (uint32_t j0 = threadIdx.x; j0 < n; j0 += 1024u) {
         float v[4];
@@ -290,26 +326,28 @@ __device__ __forceinline__ float stage_root(const float* __restrict__ xr, uint32
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t j = j0 + 256u * u;
-            if (j < n) {
-                row[j] = v[u];
-                sq[j] = v[u] * v[u];
-            }
+            if (j < n) row[j] = v[u];
         }
     }
+    __shared__ float root;
     __syncthreads();
-    const float squares = shared_sum(sq, n);
-    return __builtin_sqrtf(squares / (float)n + eps);
+    if (threadIdx.x < 64u) {
+        const float squares = ordered_sum_by_wave<true>(row, n);
+        if (threadIdx.x == 0) root = __builtin_sqrtf(squares / (float)n + eps);
+    }
+    __syncthreads();
+    return root;
 }
 
 // RMSNorm of row xr (n values, a multiple of 32, at most RMSNORM_LDS_ROW)
 // then the activation quantiser, by one workgroup: each 8-lane group
 // normalises 4 values a lane of a block of 32 and quantises the block
 // (quantize_activations, quant.cr:428-442, on the normalised row) into
-// `act` row r, laid out as the quantise pass lays it out. row and sq are
-// LDS of n floats each. Every thread calls it.
+// `act` row r, laid out as the quantise pass lays it out. row is LDS of n
+// floats. Every thread calls it.
 __device__ __forceinline__ void rmsnorm_quantise_row(const float* __restrict__ xr, uint32_t n,
                                                      const float* __restrict__ w, float eps, Activations act,
-                                                     uint32_t r, float* row, float* sq) {
+                                                     uint32_t r, float* row) {
     const uint32_t nb = n >> 5, sub = threadIdx.x & 7u;
     // this lane's weights, loaded before the fold (n ≤ 8192: at most 8 passes)
     float4 wv[RMSNORM_LDS_ROW / 1024];
@@ -319,7 +357,7 @@ __device__ __forceinline__ void rmsnorm_quantise_row(const float* __restrict__ x
         wv[pass] = (w && blk < nb) ? *reinterpret_cast<const float4*>(w + blk * 32u + sub * 4u)
                                    : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    const float root = stage_root(xr, n, eps, row, sq);
+    const float root = stage_root(xr, n, eps, row);
 #pragma unroll
     for (uint32_t pass = 0; pass < RMSNORM_LDS_ROW / 1024; ++pass) {
         const uint32_t blk = (threadIdx.x >> 3) + 32u * pass;

@@ -149,12 +149,9 @@ hipError_t launch_stream(uint32_t kind, const StreamLaunch& launch, hipStream_t 
 // dst[rows, n] = residual[rows, n] + act · wᵀ for a few activation rows
 // (fewer than the matrix cores take), the residual added in the product's
 // fold as a bias row per activation row: the host's `x + product`, one
-// rounding. With `squares`, each output's square (rounded) goes to the same
-// index there, for an RMSNorm that follows. hipErrorInvalidValue when the
-// shape is not for that kernel.
+// rounding. hipErrorInvalidValue when the shape is not for that kernel.
 hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* residual,
-                                   uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream,
-                                   float* squares = nullptr);
+                                   uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream);
 
 // SwiGLU(act · gateᵀ, act · upᵀ) quantised into `glu` ([rows, H] as the
 // quantise pass lays it out), one launch per group of rows: w is the merged
@@ -217,11 +214,10 @@ hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t str
 hipError_t launch_attention_decode(const Attention& a, const RopeWrite& r, uint32_t tokens, hipStream_t stream);
 
 // RMSNorm then quantisation into `act`, one launch; for n a multiple of 32
-// up to the LDS limit. `squares`: null, or x's squares (x·x rounded, same
-// layout), which the launch then folds instead of squaring x itself.
+// up to the LDS limit.
 bool rmsnorm_quantise_fits(uint32_t n);
 hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w, uint32_t rows, uint32_t n, float eps,
-                                   Activations act, hipStream_t stream, const float* squares = nullptr);
+                                   Activations act, hipStream_t stream);
 hipError_t launch_swiglu_quantise(const float* gate, const float* value, uint32_t ld, uint32_t rows, uint32_t n,
                                   Activations act, hipStream_t stream);
 

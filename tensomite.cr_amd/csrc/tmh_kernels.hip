@@ -270,9 +270,7 @@ __device__ __forceinline__ void load_activations(const Activations& act, uint32_
 // A thread computes its pair's two contributions to each output it touches
 // and writes them to LDS, part[output][block]. Then thread o < NB·tr adds
 // the contributions of output o (and o + 256, ...) one by one in block order
-// -- the host's order -- and writes it, plus the bias; with sq, also the
-// output's square (each rounded, as a later Σx² would square it) at the
-// same index of sq.
+// -- the host's order -- and writes it, plus the bias.
 //
 // GLU: w is a merged [gate | up] matrix of n = 2·H rows, and the tile's tr
 // rows are gate rows tile·tr/2 .. + tr/2 then the up rows of the same
@@ -282,9 +280,8 @@ __device__ __forceinline__ void load_activations(const Activations& act, uint32_
 // into `glu` as the quantise pass lays out an [NB, H] activation.
 template <int KIND, int NB, bool GLU = false>
 __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst,
-                                            const float* __restrict__ bias, uint32_t bias_ld,
-                                            float* __restrict__ sq, uint32_t n, uint32_t k,
-                                            uint32_t tr, uint32_t stride, uint32_t tile, float* part,
+                                            const float* __restrict__ bias, uint32_t bias_ld, uint32_t n,
+                                            uint32_t k, uint32_t tr, uint32_t stride, uint32_t tile, float* part,
                                             Activations glu = Activations{}) {
     constexpr uint32_t PW = Fmt<KIND>::PW;
     const uint32_t t = threadIdx.x;
@@ -347,9 +344,7 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
             if constexpr (GLU) {
                 outs[o] = sum;
             } else {
-                const float v = bias ? sum + bias[(size_t)b * bias_ld + row] : sum;
-                dst[(size_t)b * n + row] = v;
-                if (sq) sq[(size_t)b * n + row] = v * v;
+                dst[(size_t)b * n + row] = bias ? sum + bias[(size_t)b * bias_ld + row] : sum;
             }
         }
     }
@@ -378,15 +373,14 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
 }
 
 // bias_ld: the bias's elements per activation row (0: one bias row for
-// every activation row; n: a row each, e.g. a residual). sq: null, or where
-// the outputs' squares go.
+// every activation row; n: a row each, e.g. a residual).
 template <int KIND, int NB>
 __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, Activations act,
                                                 float* __restrict__ dst, const float* __restrict__ bias,
-                                                uint32_t bias_ld, float* __restrict__ sq, uint32_t n, uint32_t k,
-                                                uint32_t tr, uint32_t stride) {
+                                                uint32_t bias_ld, uint32_t n, uint32_t k, uint32_t tr,
+                                                uint32_t stride) {
     extern __shared__ float part[];
-    matvec_tile<KIND, NB>(w, act, dst, bias, bias_ld, sq, n, k, tr, stride, blockIdx.x, part);
+    matvec_tile<KIND, NB>(w, act, dst, bias, bias_ld, n, k, tr, stride, blockIdx.x, part);
 }
 
 // The lanes product over a merged [gate | up] matrix with SwiGLU and the
@@ -396,7 +390,7 @@ template <int KIND, int NB>
 __global__ __launch_bounds__(256) void k_matvec_glu(const uint8_t* __restrict__ w, Activations act, uint32_t n,
                                                     uint32_t k, uint32_t tr, uint32_t stride, Activations glu) {
     extern __shared__ float part[];
-    matvec_tile<KIND, NB, true>(w, act, nullptr, nullptr, 0, nullptr, n, k, tr, stride, blockIdx.x, part, glu);
+    matvec_tile<KIND, NB, true>(w, act, nullptr, nullptr, 0, n, k, tr, stride, blockIdx.x, part, glu);
 }
 
 
@@ -1429,21 +1423,20 @@ static uint32_t lanes_tile(uint32_t nb, uint32_t nbatch, uint32_t n, int compute
 
 template <int KIND, int NB>
 static hipError_t launch_lanes_nb(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t bias_ld,
-                                  float* sq, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+                                  uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
     const uint32_t nb = k >> 5;
     const uint32_t tr = lanes_tile(nb, NB, n, compute_units);
     const uint32_t stride = lanes_stride(nb);
     const size_t lds = (size_t)NB * tr * stride * sizeof(float);
     const uint32_t grid = (n + tr - 1u) / tr;
-    hipLaunchKernelGGL((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, sq, n, k,
-                       tr, stride);
+    hipLaunchKernelGGL((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k, tr,
+                       stride);
     return hipGetLastError();
 }
 
 template <int KIND>
 static hipError_t launch_lanes(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
-                               uint32_t n, uint32_t k, int compute_units, hipStream_t stream, uint32_t bias_ld = 0,
-                               float* sq = nullptr) {
+                               uint32_t n, uint32_t k, int compute_units, hipStream_t stream, uint32_t bias_ld = 0) {
     // Activation rows in groups of 8, 4, 2 and 1 (a thread holds its pair
     // of every row of a group in registers; measured, one group of 8 beats
     // two of 4, which read the weights twice): each output depends on
@@ -1461,16 +1454,15 @@ static hipError_t launch_lanes(const uint8_t* w, Activations act, float* dst, co
         a.qs += (size_t)done * k;
         float* d = dst + (size_t)done * n;
         const float* bi = bias ? bias + (size_t)done * bias_ld : nullptr;
-        float* sqd = sq ? sq + (size_t)done * n : nullptr;
         hipError_t err;
         uint32_t take;
         if (left >= 8 && 8u * smallest <= LANES_LDS_LIMIT)
-            err = launch_lanes_nb<KIND, 8>(w, a, d, bi, bias_ld, sqd, n, k, compute_units, stream), take = 8;
+            err = launch_lanes_nb<KIND, 8>(w, a, d, bi, bias_ld, n, k, compute_units, stream), take = 8;
         else if (left >= 4 && 4u * smallest <= LANES_LDS_LIMIT)
-            err = launch_lanes_nb<KIND, 4>(w, a, d, bi, bias_ld, sqd, n, k, compute_units, stream), take = 4;
+            err = launch_lanes_nb<KIND, 4>(w, a, d, bi, bias_ld, n, k, compute_units, stream), take = 4;
         else if (left >= 2 && 2u * smallest <= LANES_LDS_LIMIT)
-            err = launch_lanes_nb<KIND, 2>(w, a, d, bi, bias_ld, sqd, n, k, compute_units, stream), take = 2;
-        else err = launch_lanes_nb<KIND, 1>(w, a, d, bi, bias_ld, sqd, n, k, compute_units, stream), take = 1;
+            err = launch_lanes_nb<KIND, 2>(w, a, d, bi, bias_ld, n, k, compute_units, stream), take = 2;
+        else err = launch_lanes_nb<KIND, 1>(w, a, d, bi, bias_ld, n, k, compute_units, stream), take = 1;
         if (err != hipSuccess) return err;
         done += take;
     }
@@ -1799,14 +1791,13 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
 }
 
 hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* residual,
-                                  uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream,
-                                  float* squares) {
+                                  uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (!lanes_fit(w, k) || rows >= MATRIX_ROWS) return hipErrorInvalidValue;
     switch (kind) {
-    case 0: return launch_lanes<0>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
-    case 1: return launch_lanes<1>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
-    default: return launch_lanes<2>(w, act, dst, residual, rows, n, k, compute_units, stream, n, squares);
+    case 0: return launch_lanes<0>(w, act, dst, residual, rows, n, k, compute_units, stream, n);
+    case 1: return launch_lanes<1>(w, act, dst, residual, rows, n, k, compute_units, stream, n);
+    default: return launch_lanes<2>(w, act, dst, residual, rows, n, k, compute_units, stream, n);
     }
 }
 

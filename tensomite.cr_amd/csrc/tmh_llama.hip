@@ -57,7 +57,6 @@ struct Llama {
     float* x[2] = {nullptr, nullptr};  // the residual stream, ping-ponged by one-row residual products
     float *h = nullptr, *qkv_out = nullptr, *q = nullptr, *att = nullptr, *o_out = nullptr;
     float *gu = nullptr, *act = nullptr, *logits = nullptr;
-    float* squares = nullptr;  // x's squares, written beside x by the residual product for the next RMSNorm
     float *cos = nullptr, *sin = nullptr;
     float *keys = nullptr, *values = nullptr;  // [layers][rows][kv_heads][capacity][head_width]
     int32_t *ids = nullptr, *slots = nullptr, *table = nullptr, *steps = nullptr, *log = nullptr;
@@ -88,31 +87,26 @@ hipError_t quantise(const DeviceContext& ctx, const float* x, uint32_t rows, uin
 }
 
 // RMSNorm of x's rows, quantised into act: one launch where the row fits.
-// squares: null, or x's squares as the residual product wrote them.
 hipError_t norm_quantise(const Llama& m, const DeviceContext& ctx, const float* x, const float* w, uint32_t rows,
-                         tmh::Activations act, const float* squares = nullptr) {
+                         tmh::Activations act) {
     const uint32_t W = (uint32_t)m.c.width;
-    if (tmh::rmsnorm_quantise_fits(W))
-        return tmh::launch_rmsnorm_quantise(x, W, w, rows, W, m.c.eps, act, ctx.stream, squares);
+    if (tmh::rmsnorm_quantise_fits(W)) return tmh::launch_rmsnorm_quantise(x, W, w, rows, W, m.c.eps, act, ctx.stream);
     hipError_t e = tmh::launch_rmsnorm(x, W, w, rows, W, m.c.eps, m.h, W, ctx.stream);
     return e == hipSuccess ? quantise(ctx, m.h, rows, W, act) : e;
 }
 
 // The residual update x += act · wᵀ, as the host's `x + product` (one
 // rounding per element either way round): for fewer rows than the matrix
-// cores take, the lanes product adds each row's x as its bias, writes the
-// other residual buffer and the new rows' squares (`squared` tells the
-// caller so); else one row is a product with x as bias, and more rows a
-// product and an add.
+// cores take, the lanes product adds each row's x as its bias and writes
+// the other residual buffer; else one row is a product with x as bias, and
+// more rows a product and an add.
 hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
-                    uint32_t k, int& cur, bool& squared) {
+                    uint32_t k, int& cur) {
     const uint32_t W = (uint32_t)m.c.width;
-    squared = false;
     hipError_t r = tmh::launch_product_residual(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], rows, W, k,
-                                                ctx.compute_units, ctx.stream, m.squares);
+                                                ctx.compute_units, ctx.stream);
     if (r != hipErrorInvalidValue) {
         cur ^= 1;
-        squared = r == hipSuccess;
         return r;
     }
     if (rows == 1) {
@@ -136,13 +130,12 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
     const float scale = (float)(1.0 / std::sqrt((double)hw));
     const bool quant_att = hw % 32u == 0;
     int cur = 0;
-    bool squared = false;  // m.squares holds m.x[cur]'s squares
     hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x[cur], ctx.errors, ctx.stream);
     const tmh::Activations a_in = tmh::carve_scratch(m.scratch[0], tokens, W);
     for (int32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
         float* keys = m.keys + (size_t)l * m.layer_cache;
         float* values = m.values + (size_t)l * m.layer_cache;
-        e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in, squared ? m.squares : nullptr);
+        e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in);
         if (e == hipSuccess) e = product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out, nullptr);
         const tmh::Activations a_att = tmh::carve_scratch(m.scratch[1], tokens, m.qn);
         tmh::RopeWrite r{m.qkv_out, m.nqkv, (uint32_t)c.heads, (uint32_t)c.kv_heads, hw, m.cos, m.sin,
@@ -159,9 +152,8 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
             }
         }
         if (e == hipSuccess && !quant_att) e = quantise(ctx, m.att, tokens, m.qn, a_att);
-        if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur, squared);
-        if (e == hipSuccess)
-            e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in, squared ? m.squares : nullptr);
+        if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur);
+        if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in);
         const tmh::Activations a_hid = tmh::carve_scratch(m.scratch[1], tokens, H);
         if (e == hipSuccess) {
             // gate_up with SwiGLU and the quantiser in its epilogue where the
@@ -175,12 +167,10 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
                 e = g;
             }
         }
-        if (e == hipSuccess) e = residual(m, ctx, m.down[l], a_hid, tokens, H, cur, squared);
+        if (e == hipSuccess) e = residual(m, ctx, m.down[l], a_hid, tokens, H, cur);
     }
     const tmh::Activations a_fin = tmh::carve_scratch(m.scratch[0], final_rows, W);
-    if (e == hipSuccess)
-        e = norm_quantise(m, ctx, m.x[cur] + (size_t)final_from * W, m.norm, final_rows, a_fin,
-                          squared ? m.squares + (size_t)final_from * W : nullptr);
+    if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur] + (size_t)final_from * W, m.norm, final_rows, a_fin);
     if (e == hipSuccess)
         e = product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, m.logits + (size_t)logits_row * c.vocab,
                     nullptr);
@@ -404,7 +394,6 @@ int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* we
         {(void**)&m->q, R * m->qn * 4},
         {(void**)&m->att, R * m->qn * 4},
         {(void**)&m->o_out, R * W * 4},
-        {(void**)&m->squares, R * W * 4},
         {(void**)&m->gu, R * 2 * H * 4},
         {(void**)&m->act, R * H * 4},
         {(void**)&m->logits, R * (size_t)c.vocab * 4},

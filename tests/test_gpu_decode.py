@@ -57,6 +57,51 @@ def test_rmsnorm_bit_exact(dev, n):
         assert np.array_equal(bits(got), bits(want))
 
 
+def adversarial_rows(rng, rows, n):
+    """Rows whose ordered Σx² is hard to fold out of order: exact ties
+    (small integers), magnitudes over 2^±40, sums that double many times
+    (ascending, geometric), sums that barely grow (descending), constant
+    rows, and rows with a NaN or an inf."""
+    x = np.empty((rows, n), np.float32)
+    for r in range(rows):
+        kind = r % 8
+        if kind == 0:
+            v = rng.integers(-6, 7, n).astype(np.float64)
+        elif kind == 1:
+            v = rng.choice([-1.0, 1.0], n) * 2.0 ** rng.uniform(-40, 40, n)
+        elif kind == 2:
+            v = np.sort(np.abs(rng.normal(0, 1, n)) * 2.0 ** rng.uniform(-8, 8, n))
+        elif kind == 3:
+            v = 2.0 ** (np.arange(n) * (60.0 / max(n, 1)) - 30.0)
+        elif kind == 4:
+            v = np.sort(np.abs(rng.normal(0, 1, n)))[::-1]
+        elif kind == 5:
+            v = np.full(n, rng.normal())
+        elif kind == 6:
+            v = rng.normal(0, 1, n)
+            v[rng.integers(0, n)] = np.nan
+        else:
+            v = rng.normal(0, 1, n)
+            v[rng.integers(0, n)] = np.inf
+        x[r] = v.astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("n", [100, 576, 1000, 2048, 4097, 8192])
+def test_rmsnorm_ordered_sum_adversarial(dev, n):
+    # The squares' sum is folded by speculation across a wave (every lane
+    # folds its chunk from a guessed start until each start equals the
+    # previous chunk's end); its bits must be the sequential fold's on rows
+    # built to break the guesses.
+    say("rmsnorm adversarial n", n)
+    rng = np.random.default_rng(1000 + n)
+    rows = 64
+    x = adversarial_rows(rng, rows, n)
+    got = f32(dev, dev.rmsnorm(dev.from_array(x), None, rows, n, 1e-5), rows * n).reshape(rows, n)
+    want = oracle.rmsnorm(x, None, 1e-5)
+    assert np.array_equal(bits(got), bits(want))
+
+
 def test_rmsnorm_square_root_rounding(dev):
     # Rows of one value a: root = sqrt(a·a/1 + eps), out = a / root; over a
     # million magnitudes every rounding of the square root and the division
