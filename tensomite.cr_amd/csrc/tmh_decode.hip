@@ -254,7 +254,8 @@ constexpr size_t ATT_LDS_LIMIT = 160u * 1024u;
 
 __host__ __device__ inline uint32_t att_chunk_positions(uint32_t width, uint32_t capacity) {
     const uint32_t w4 = (width + 3u) & ~3u;
-    const size_t fixed = 4u * (size_t)w4 + ((capacity + 3u) & ~3u);
+    // 64 floats left for the kernel's own LDS (its tops and total)
+    const size_t fixed = 4u * (size_t)w4 + ((capacity + 3u) & ~3u) + 64u;
     const size_t avail = ATT_LDS_LIMIT / 4u > fixed ? ATT_LDS_LIMIT / 4u - fixed : 0u;
     size_t ch = std::min<size_t>(ATT_CHUNK_FLOATS / width, avail / (2u * (size_t)width));
     ch &= ~(size_t)3u;

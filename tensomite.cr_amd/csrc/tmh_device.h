@@ -272,11 +272,24 @@ template <bool SQ, int M>
 __device__ __forceinline__ float ordered_sum_wave_m(const float* v, uint32_t n) {
     float a[M];
     const uint32_t c0 = (threadIdx.x & 63u) * (uint32_t)M;
+    if ((M % 4 == 0) && n % 4u == 0 && ((uintptr_t)v & 15u) == 0) {
+        // 16-byte reads (a lane's chunk starts 16-byte aligned)
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const uint32_t j = c0 + (uint32_t)i;
-        const float x = j < n ? v[j] : 0.0f;
-        a[i] = SQ ? x * x : x;
+        for (int i = 0; i < M; i += 4) {
+            const uint32_t j = c0 + (uint32_t)i;
+            const float4 x = j < n ? *reinterpret_cast<const float4*>(v + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            a[i] = SQ ? x.x * x.x : x.x;
+            a[i + 1] = SQ ? x.y * x.y : x.y;
+            a[i + 2] = SQ ? x.z * x.z : x.z;
+            a[i + 3] = SQ ? x.w * x.w : x.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const uint32_t j = c0 + (uint32_t)i;
+            const float x = j < n ? v[j] : 0.0f;
+            a[i] = SQ ? x * x : x;
+        }
     }
     return ordered_sum_wave<M>(a);
 }
@@ -285,13 +298,17 @@ __device__ __forceinline__ float ordered_sum_wave_m(const float* v, uint32_t n) 
 constexpr uint32_t WAVE_SUM_MAX = 8192;
 
 // Σ v[0..n) in index order from +0.0f (SQ: Σ v[i]·v[i]) by one whole wave:
-// every lane of the wave calls it with the same v and n (n <= WAVE_SUM_MAX)
-// and receives the sum.
-template <bool SQ = false>
+// every lane of the wave calls it with the same v and n (n <= 64·MAXM, at
+// most WAVE_SUM_MAX) and receives the sum. MAXM bounds the values a lane
+// holds, and so the registers the caller's kernel is compiled for.
+template <bool SQ = false, int MAXM = 128>
 __device__ __forceinline__ float ordered_sum_by_wave(const float* v, uint32_t n) {
     if (n <= 64u * 8u) return ordered_sum_wave_m<SQ, 8>(v, n);
-    if (n <= 64u * 32u) return ordered_sum_wave_m<SQ, 32>(v, n);
-    return ordered_sum_wave_m<SQ, 128>(v, n);
+    if constexpr (MAXM >= 32) {
+        if (n <= 64u * 32u) return ordered_sum_wave_m<SQ, 32>(v, n);
+    }
+    if constexpr (MAXM >= 128) return ordered_sum_wave_m<SQ, 128>(v, n);
+    return 0.0f;
 }
 
 // The ordered sum of v[0..n) by wave 0 (ordered_sum_by_wave; beyond its

@@ -30,8 +30,10 @@ int check_rope(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t table
 
 int check_attention(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t capacity) {
     if (width == 0 || width % 4u != 0 || heads == 0 || kv_heads == 0 || heads % kv_heads != 0) return TMH_ERROR_SHAPE;
-    if (capacity == 0 || tmh::attention_lds(width, capacity) > 160u * 1024u ||
-        tmh::attention_decode_lds(width, capacity) > 160u * 1024u)
+    // the attention kernels' dynamic LDS plus their own (256 bytes; decode:
+    // 2 KB, also covering its last direct load) within a CU's 160 KB
+    if (capacity == 0 || tmh::attention_lds(width, capacity) + 256u > 160u * 1024u ||
+        tmh::attention_decode_lds(width, capacity) + 2048u > 160u * 1024u)
         return TMH_ERROR_SHAPE;
     return TMH_SUCCESS;
 }
