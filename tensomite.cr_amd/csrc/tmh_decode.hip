@@ -623,7 +623,6 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t cols = width >> 2, cp = l.cp;
     const float4* q4 = reinterpret_cast<const float4*>(l.q);
-    const float4* kc4 = reinterpret_cast<const float4*>(l.kcur);
 
 
     float top = -__builtin_inff();
@@ -637,13 +636,18 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
             wait_vm_lds<0>();
         }
         lds_sync();
+        // the current position's key (rotated here, not yet in what was
+        // staged) into its row of the chunk: the host reads it from its cache
+        if (cur >= (int32_t)p0 && cur < (int32_t)(p0 + cnt)) {
+            for (uint32_t c = tid; c < width; c += 256u) l.kt[att_key_at((uint32_t)(cur - (int32_t)p0) * width + c)] = l.kcur[c];
+            lds_sync();
+        }
         for (uint32_t pl = tid; pl < cnt; pl += 256u) {
             const uint32_t p = p0 + pl;
-            const bool now = (int32_t)p == cur;
             float dot = 0.0f;
             for (uint32_t c4 = 0; c4 < cols; ++c4) {
                 const float4 q = q4[c4];
-                const float4 k = now ? kc4[c4] : *reinterpret_cast<const float4*>(l.kt + att_key_at(pl * width + 4u * c4));
+                const float4 k = *reinterpret_cast<const float4*>(l.kt + att_key_at(pl * width + 4u * c4));
                 dot += q.x * k.x;
                 dot += q.y * k.y;
                 dot += q.z * k.z;
@@ -676,7 +680,6 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
 
     // Σ_p weight_p · v_p[c] in position order, one lane per column.
     float acc = 0.0f;
-    const float vnow = tid < width ? l.vcur[tid] : 0.0f;
     for (uint32_t p0 = 0; p0 < n; p0 += cp) {
         const uint32_t cnt = min(cp, n - p0);
         if (p0 > 0) {
@@ -685,15 +688,18 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
         }
         wait_vm_lds<0>();
         lds_sync();  // the chunk's values and the weights are in
+        if (cur >= (int32_t)p0 && cur < (int32_t)(p0 + cnt)) {
+            // the current position's value row, as for its key
+            for (uint32_t c = tid; c < width; c += 256u) l.vrows[(size_t)(cur - (int32_t)p0) * width + c] = l.vcur[c];
+            lds_sync();
+        }
         if (tid < width) {
             const float* vr = l.vrows + tid;
             const float* wr = l.sc + p0;
             // 16 positions a batch: a batch's values and weights are read
             // into registers before the previous batch is folded (two sets
-            // of registers in turn); the fold makes each product, the
-            // current position's value coming from vnow, and adds it. The
-            // asm statements keep the compiler from sinking a read behind
-            // the current position's test.
+            // of registers in turn); the fold makes each product and adds
+            // it.
             auto read = [&](uint32_t pl, float (&v)[16], float4 (&w)[4]) {
                 const float* vp = vr + (size_t)pl * width;
 #pragma unroll
@@ -701,17 +707,13 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
 #pragma unroll
                 for (int q = 0; q < 4; ++q) w[q] = *reinterpret_cast<const float4*>(wr + pl + 4u * q);
             };
-            auto fold = [&](uint32_t pl, float (&v)[16], const float4 (&w)[4]) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(v[i]));
-                const int32_t at = cur - (int32_t)(p0 + pl);
+            auto fold = [&](uint32_t, float (&v)[16], const float4 (&w)[4]) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float w4[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const int i = 4 * q + e;
-                        const float prod = w4[e] * (i == at ? vnow : v[i]);
+                        const float prod = w4[e] * v[4 * q + e];
                         acc += prod;
                     }
                 }
@@ -739,8 +741,7 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
                 }
             }
             for (; pl < cnt; ++pl) {
-                const float vv = (int32_t)(p0 + pl) == cur ? vnow : vr[(size_t)pl * width];
-                const float prod = l.sc[p0 + pl] * vv;
+                const float prod = l.sc[p0 + pl] * vr[(size_t)pl * width];
                 acc += prod;
             }
         }
