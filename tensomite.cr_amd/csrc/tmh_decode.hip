@@ -610,6 +610,62 @@ __device__ __forceinline__ uint32_t stage_values(const float* vb, uint32_t width
     return mine;
 }
 
+// acc += Σ_p w[p] · v[p · stride] over p in [0, cnt), each product rounded
+// before its add, in position order (one column of a value chunk; one lane
+// each). 16 positions a batch: a batch's values and weights are read into
+// registers before the previous batch is folded (two sets of registers in
+// turn). S: the row stride when fixed at compile time (reads then take
+// immediate offsets), else 0 and `stride` holds it.
+template <uint32_t S>
+__device__ __forceinline__ void fold_values(const float* vr, const float* wr, uint32_t cnt, uint32_t stride,
+                                            float& acc) {
+    const uint32_t width = S ? S : stride;
+    auto read = [&](uint32_t pl, float (&v)[16], float4 (&w)[4]) {
+        const float* vp = vr + (size_t)pl * width;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = vp[(size_t)i * width];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = *reinterpret_cast<const float4*>(wr + pl + 4u * q);
+    };
+    auto fold = [&](float (&v)[16], const float4 (&w)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float w4[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float prod = w4[e] * v[4 * q + e];
+                acc += prod;
+            }
+        }
+    };
+    uint32_t pl = 0;
+    if (cnt >= 32u) {
+        float va[16], vb[16];
+        float4 wa[4], wb[4];
+        read(0, va, wa);
+        for (; pl + 48u <= cnt; pl += 32u) {
+            read(pl + 16u, vb, wb);
+            fold(va, wa);
+            read(pl + 32u, va, wa);
+            fold(vb, wb);
+        }
+        // va holds [pl, pl + 16)
+        if (pl + 32u <= cnt) {
+            read(pl + 16u, vb, wb);
+            fold(va, wa);
+            fold(vb, wb);
+            pl += 32u;
+        } else {
+            fold(va, wa);
+            pl += 16u;
+        }
+    }
+    for (; pl < cnt; ++pl) {
+        const float prod = wr[pl] * vr[(size_t)pl * width];
+        acc += prod;
+    }
+}
+
 // attend() of one decode row from the staged chunks: the scores of chunk
 // after chunk (the first staged already), the softmax, then the weighted
 // values chunk after chunk, each product rounded before it is added, in
@@ -694,56 +750,10 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
             lds_sync();
         }
         if (tid < width) {
-            const float* vr = l.vrows + tid;
-            const float* wr = l.sc + p0;
-            // 16 positions a batch: a batch's values and weights are read
-            // into registers before the previous batch is folded (two sets
-            // of registers in turn); the fold makes each product and adds
-            // it.
-            auto read = [&](uint32_t pl, float (&v)[16], float4 (&w)[4]) {
-                const float* vp = vr + (size_t)pl * width;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) v[i] = vp[(size_t)i * width];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) w[q] = *reinterpret_cast<const float4*>(wr + pl + 4u * q);
-            };
-            auto fold = [&](uint32_t, float (&v)[16], const float4 (&w)[4]) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float w4[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float prod = w4[e] * v[4 * q + e];
-                        acc += prod;
-                    }
-                }
-            };
-            uint32_t pl = 0;
-            if (cnt >= 32u) {
-                float va[16], vb2[16];
-                float4 wa[4], wb[4];
-                read(0, va, wa);
-                for (; pl + 48u <= cnt; pl += 32u) {
-                    read(pl + 16u, vb2, wb);
-                    fold(pl, va, wa);
-                    read(pl + 32u, va, wa);
-                    fold(pl + 16u, vb2, wb);
-                }
-                // va holds [pl, pl + 16)
-                if (pl + 32u <= cnt) {
-                    read(pl + 16u, vb2, wb);
-                    fold(pl, va, wa);
-                    fold(pl + 16u, vb2, wb);
-                    pl += 32u;
-                } else {
-                    fold(pl, va, wa);
-                    pl += 16u;
-                }
-            }
-            for (; pl < cnt; ++pl) {
-                const float prod = l.sc[p0 + pl] * vr[(size_t)pl * width];
-                acc += prod;
-            }
+            if (width == 64u)
+                fold_values<64>(l.vrows + tid, l.sc + p0, cnt, width, acc);
+            else
+                fold_values<0>(l.vrows + tid, l.sc + p0, cnt, width, acc);
         }
     }
     if (tid < width) l.out[tid] = acc;
