@@ -681,6 +681,12 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     const float4* q4 = reinterpret_cast<const float4*>(l.q);
 
 
+    // width 64: q held in registers for every score
+    float4 qr[16];
+    if (width == 64u) {
+#pragma unroll
+        for (uint32_t c4 = 0; c4 < 16u; ++c4) qr[c4] = q4[c4];
+    }
     float top = -__builtin_inff();
     for (uint32_t p0 = 0; p0 < n; p0 += cp) {
         const uint32_t cnt = min(cp, n - p0);
@@ -701,13 +707,28 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
         for (uint32_t pl = tid; pl < cnt; pl += 256u) {
             const uint32_t p = p0 + pl;
             float dot = 0.0f;
-            for (uint32_t c4 = 0; c4 < cols; ++c4) {
-                const float4 q = q4[c4];
-                const float4 k = *reinterpret_cast<const float4*>(l.kt + att_key_at(pl * width + 4u * c4));
-                dot += q.x * k.x;
-                dot += q.y * k.y;
-                dot += q.z * k.z;
-                dot += q.w * k.w;
+            if (width == 64u) {
+                // q in registers; a position's 64 keys lie in one 1 KB piece
+                // (four rows a piece), read at immediate offsets
+                const float4* k4 = reinterpret_cast<const float4*>(l.kt + (pl >> 2) * 260u + (pl & 3u) * 64u);
+#pragma unroll
+                for (uint32_t c4 = 0; c4 < 16u; ++c4) {
+                    const float4 q = qr[c4];
+                    const float4 k = k4[c4];
+                    dot += q.x * k.x;
+                    dot += q.y * k.y;
+                    dot += q.z * k.z;
+                    dot += q.w * k.w;
+                }
+            } else {
+                for (uint32_t c4 = 0; c4 < cols; ++c4) {
+                    const float4 q = q4[c4];
+                    const float4 k = *reinterpret_cast<const float4*>(l.kt + att_key_at(pl * width + 4u * c4));
+                    dot += q.x * k.x;
+                    dot += q.y * k.y;
+                    dot += q.z * k.z;
+                    dot += q.w * k.w;
+                }
             }
             float x = dot * scale;
             // The causal mask adds -inf past the last position seen; its 0
