@@ -1013,16 +1013,26 @@ __global__ __launch_bounds__(256) void k_argmax_chunks(const float* __restrict__
 // position on. A row whose cache is full gets a slot of -1 and an entry one
 // past its capacity, so a step that would run it anyway is reported by the
 // RoPE and attention kernels instead of writing into the next row.
-__global__ void k_advance(uint32_t rows, const float* __restrict__ logits, uint32_t vocab, uint32_t chunks,
-                          const float* __restrict__ values, const int32_t* __restrict__ index,
-                          int32_t* __restrict__ ids, int32_t* __restrict__ log, uint32_t log_stride,
-                          int32_t* __restrict__ steps, int32_t* __restrict__ slots, int32_t* __restrict__ table,
-                          uint32_t capacity) {
-    const uint32_t r = blockIdx.x * 64u + threadIdx.x;
-    if (r >= rows) return;
+// One wave per row: the lanes load the chunks' bests together and reduce
+// them by `better` (highest value, then lowest index: a maximum under a
+// total order, so any reduction order gives the chunk-order result).
+__global__ __launch_bounds__(64) void k_advance(uint32_t rows, const float* __restrict__ logits, uint32_t vocab,
+                                                uint32_t chunks, const float* __restrict__ values,
+                                                const int32_t* __restrict__ index, int32_t* __restrict__ ids,
+                                                int32_t* __restrict__ log, uint32_t log_stride,
+                                                int32_t* __restrict__ steps, int32_t* __restrict__ slots,
+                                                int32_t* __restrict__ table, uint32_t capacity) {
+    const uint32_t r = blockIdx.x;
     float v = 0.0f;
     int32_t i = -1;
-    for (uint32_t c = 0; c < chunks; ++c) better(v, i, values[r * chunks + c], index[r * chunks + c]);
+    for (uint32_t c = threadIdx.x; c < chunks; c += 64u) better(v, i, values[r * chunks + c], index[r * chunks + c]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        const float ov = __shfl_xor(v, s, 64);
+        const int32_t oi = __shfl_xor(i, s, 64);
+        better(v, i, ov, oi);
+    }
+    if (threadIdx.x != 0) return;
     const float first = logits[(size_t)r * vocab];
     const int32_t chosen = (first != first || i < 0) ? 0 : i;
     ids[r] = chosen;
@@ -1043,7 +1053,7 @@ hipError_t launch_choose_advance(const float* logits, uint32_t rows, uint32_t vo
     const uint32_t chunks = argmax_chunks(vocab);
     hipLaunchKernelGGL(k_argmax_chunks, dim3(rows * chunks), dim3(256), 0, stream, logits, vocab, vocab, chunks, values,
                        index);
-    hipLaunchKernelGGL(k_advance, dim3((rows + 63u) / 64u), dim3(64), 0, stream, rows, logits, vocab, chunks, values,
+    hipLaunchKernelGGL(k_advance, dim3(rows), dim3(64), 0, stream, rows, logits, vocab, chunks, values,
                        index, ids, log, log_stride, steps, slots, table, capacity);
     return hipGetLastError();
 }
