@@ -125,6 +125,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--gemm", action="store_true",
+                    help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
     ap.add_argument("--decode-eager", action="store_true",
                     help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
     args = ap.parse_args()
@@ -138,6 +140,9 @@ def main():
 
     dev = th.HIPDevice(0)
     log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
+    if args.gemm:
+        print(json.dumps(gemm_config4(dev, args.steps, args.warmup)), flush=True)
+        return
     prods = products_135m()
     weight_bytes = sum(q4_0_bytes(n, k) for _, n, k in prods)
     algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
@@ -351,6 +356,41 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
         out["cpu_baseline"] = {"ms_per_token": round(elapsed / tokens * 1e3, 1), "cores": cores, "kind": "port",
                                "sample": f"{tokens} greedy tokens after an 8-token prompt, batch 1; the oracle's "
                                          f"Llama forward ({variant} build, {cores} threads)"}
+    return out
+
+
+def gemm_config4(dev, steps, warmup):
+    """Config 4: the Q8_0 prefill GEMM at the Llama-1.7B shape, 512 tokens x
+    K = 2048 against N = 2048 (attention projections) and N = 8192 (MLP
+    up/gate). One call is tmh_block_matmul over f32 x (the activation
+    quantiser, then the matrix-core kernel, k_matmul_mfma); timed with HIP
+    events over `steps` calls. int8 work: 2 · 512 · 2048 · N ops a call."""
+    import quant_host
+    rows, k = 512, 2048
+    rng = np.random.default_rng(0x5EED0004)
+    x = dev.from_array(rng.normal(0.0, 1.0, (rows, k)).astype(np.float32))
+    out = {"metric": "Q8_0 prefill GEMM int8 TOP/s (config 4, 512 tokens x K=2048)", "unit": "TOP/s",
+           "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
+           "data": "synthetic: W ~ N(0,0.02) quantised to Q8_0, x ~ N(0,1)", "shapes": {}}
+    for n in (2048, 8192):
+        w = dev.from_array(quant_host.synthetic_weights("Q8_0", n, k, seed=0x5EED0004 + n))
+        dst = dev.alloc(4 * rows * n)
+        for _ in range(warmup):
+            dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst)
+        dev.sync()
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        for _ in range(steps):
+            dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst)
+        dev.record(e1)
+        dev.sync()
+        ms = dev.elapsed_ms(e0, e1) / steps
+        ops = 2.0 * rows * k * n
+        out["shapes"][f"N={n}"] = {"ms_per_call": round(ms, 4), "TOP_per_s": round(ops / (ms * 1e-3) / 1e12, 1),
+                                   "int8_mfma_peak_frac": round(ops / (ms * 1e-3) / 5.0e15, 4)}
+        w.release()
+        dst.release()
+    out["value"] = out["shapes"]["N=8192"]["TOP_per_s"]
     return out
 
 
