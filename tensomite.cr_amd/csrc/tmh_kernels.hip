@@ -1212,18 +1212,30 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const uint8_t* __restrict__
     MmLoad<KIND> L;
     stage_load<KIND>(w, act, n, m, nb, n0, m0, 0, L);
     stage_store<KIND>(stage[0], L);
+    // This wave's activation operands of a pair of blocks ([block][a]), one
+    // pair ahead of the MFMAs that take them (the last pair loads itself
+    // again), so their latency hides behind a pair's work.
+    long avc[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int a = 0; a < 2; ++a) avc[h][a] = *(const __attribute__((address_space(1))) long*)(arow[a] + h * 32u);
     __syncthreads();
 
     for (uint32_t pair = 0; pair < pairs; ++pair) {
         const MmStage& S = stage[pair & 1u];
         const bool more = pair + 1u < pairs;
         if (more) stage_load<KIND>(w, act, n, m, nb, n0, m0, pair + 1u, L);
+        long avn[2][2];
+        const uint32_t next = min(pair + 1u, pairs - 1u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+                avn[h][a] = *(const __attribute__((address_space(1))) long*)(arow[a] + (2u * next + h) * 32u);
 #pragma unroll
         for (uint32_t h = 0; h < 2; ++h) {
-            const uint32_t blk = 2u * pair + h;
-            long av[2];
-#pragma unroll
-            for (int a = 0; a < 2; ++a) av[a] = *(const __attribute__((address_space(1))) long*)(arow[a] + blk * 32u);
+            const long* av = avc[h];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const uint32_t col = wn0 + 16u * b + lr;
@@ -1263,6 +1275,10 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const uint8_t* __restrict__
         }
         if (more) stage_store<KIND>(stage[(pair + 1u) & 1u], L);
         __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int a = 0; a < 2; ++a) avc[h][a] = avn[h][a];
     }
 
 #pragma unroll
