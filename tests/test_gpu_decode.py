@@ -346,6 +346,29 @@ def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
 # ------------------------------------------------------------ GGUF loading
 
 
+
+@pytest.mark.parametrize("kind,rows", [("Q8_0", 1), ("Q8_0", 3), ("Q4_1", 1), ("Q4_1", 3)])
+def test_1p7b_shape_other_formats(dev, kind, rows):
+    # The 1.7B shape in Q8_0 (17-dword pairs) and Q4_1 (sums): the last
+    # prefill logits bit for bit, then greedy tokens from a graph, against
+    # the CPU -- the residual lanes product, gate_up with SwiGLU in its
+    # epilogue and the head at k = 2048 in both formats, and at 3 rows the
+    # row groups of the 16-token prefills.
+    say("1.7B shape", kind, rows, "rows")
+    config = dict(SMOLLM2_1P7B, layers=2, context=128, kind=kind)
+    weights = random_block_llama(config, seed=40 + rows)
+    rng = np.random.default_rng(41)
+    prompts = [list(rng.integers(0, config["vocab"], 16 - r)) for r in range(rows)]
+    gpu = th.HIPLlama(dev, config, weights, rows=rows, capacity=64, max_tokens=16)
+    cpu = oracle.Llama(config, weights)
+    for r, p in enumerate(prompts):
+        got = gpu.forward(p, row=r, last_only=True)
+        if r == 0:
+            assert np.array_equal(bits(got), bits(cpu.forward(p, last_only=True)))
+    tokens = gpu.generate(6, graph=True)
+    for r, p in enumerate(prompts[:2]):
+        assert list(tokens[r]) == oracle.Llama(config, weights).generate(p, 6), r
+
 @pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0"])
 def test_load_gguf_tiny_llama_bit_exact(dev, golden, fmt):
     # Llama.load(GGUF) straight onto the device (llama.cr:184-235): the config
