@@ -132,7 +132,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
-              "how it would shard is described in DESIGN.md", file=sys.stderr)
+              "a product shards by output rows across GPUs, each GPU running this kernel on its share",
+              file=sys.stderr)
         sys.exit(1)
 
     import quant_host

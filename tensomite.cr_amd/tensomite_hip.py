@@ -2,9 +2,9 @@
 device API (src/tensomite/device.cr:6-68) for the quantised-product path.
 
 The reference's host language is Crystal, whose toolchain is absent here; this
-module is the same binding a Crystal `lib LibTensomiteHIP` would be (the
-Crystal stub is in INTEGRATION.md), written with ctypes so tests and bench.py
-drive the C ABI directly. It loads only the in-tree library and raises when
+module is the same binding a Crystal `lib LibTensomiteHIP` would be (the same
+functions and argument types as include/tensomite_hip.h), written with ctypes
+so tests and bench.py drive the C ABI directly. It loads only the in-tree library and raises when
 it is missing: there is no CPU fallback.
 
     dev = HIPDevice()
