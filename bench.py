@@ -125,6 +125,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--batched", action="store_true",
+                    help="config 3 instead (Q4_1 batched-decode products, B = 1..16); its own JSON line")
     ap.add_argument("--gemm", action="store_true",
                     help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
     ap.add_argument("--decode-eager", action="store_true",
@@ -143,6 +145,9 @@ def main():
     log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
     if args.gemm:
         print(json.dumps(gemm_config4(dev, args.steps, args.warmup)), flush=True)
+        return
+    if args.batched:
+        print(json.dumps(batched_config3(dev, args.steps, args.warmup)), flush=True)
         return
     prods = products_135m()
     weight_bytes = sum(q4_0_bytes(n, k) for _, n, k in prods)
@@ -357,6 +362,50 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
         out["cpu_baseline"] = {"ms_per_token": round(elapsed / tokens * 1e3, 1), "cores": cores, "kind": "port",
                                "sample": f"{tokens} greedy tokens after an 8-token prompt, batch 1; the oracle's "
                                          f"Llama forward ({variant} build, {cores} threads)"}
+    return out
+
+
+def batched_config3(dev, steps, warmup):
+    """Config 3: Q4_1 batched-decode products, W [8192, 2048] and [2048, 8192]
+    against B = 1, 2, 4, 8, 16 activation rows. One call is tmh_block_matmul
+    over f32 x (the activation quantiser, then the lanes product); calls
+    rotate through enough weight copies (>= 512 MB) that the 256 MB Infinity
+    Cache cannot serve them; HIP events over `steps` calls. Bytes a call:
+    weights + 4·B·K of x + 4·B·N of y."""
+    import quant_host
+    out = {"metric": "Q4_1 batched-decode product GB/s (config 3)", "unit": "GB/s", "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
+           "data": "synthetic: W ~ N(0,0.02) quantised to Q4_1, x ~ N(0,1)", "shapes": {}}
+    rng = np.random.default_rng(0x5EED0003)
+    for n, k in ((8192, 2048), (2048, 8192)):
+        host = quant_host.synthetic_weights("Q4_1", n, k, seed=0x5EED0003 + n)
+        copies = max(2, math.ceil(2 * MALL_BYTES / host.nbytes))
+        first = dev.from_array(host)
+        ws = [first] + [dev.alloc(host.nbytes) for _ in range(copies - 1)]
+        for w in ws[1:]:
+            dev.copy(w, first, host.nbytes)
+        for b in (1, 2, 4, 8, 16):
+            x = dev.from_array(rng.normal(0.0, 1.0, (b, k)).astype(np.float32))
+            dst = dev.alloc(4 * b * n)
+            for i in range(warmup):
+                dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
+            dev.sync()
+            e0, e1 = dev.event(), dev.event()
+            dev.record(e0)
+            for i in range(steps):
+                dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
+            dev.record(e1)
+            dev.sync()
+            ms = dev.elapsed_ms(e0, e1) / steps
+            nbytes = host.nbytes + 4 * b * k + 4 * b * n
+            out["shapes"][f"{n}x{k} B={b}"] = {"us_per_call": round(ms * 1e3, 2),
+                                               "GB_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                               "hbm_peak_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            x.release()
+            dst.release()
+        for w in ws:
+            w.release()
+    out["value"] = out["shapes"]["8192x2048 B=1"]["GB_per_s"]
     return out
 
 

@@ -696,7 +696,13 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     if (rows == 0 || n == 0) return TMH_SUCCESS;
     if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
     const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
-    if (rows == 1 && tmh::row_kernel_fits(mode, wrow, k)) {
+    // One row of a product of at most 4 MB of weights: the one-row kernel,
+    // which quantises x itself (one launch). Larger ones stream better as
+    // the quantise pass and the lanes product (measured: Q4_1 8192x2048 one
+    // row 11.7 us against about 7; 2048x8192 21 against about 10).
+    constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
+    if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
+        tmh::row_kernel_fits(mode, wrow, k)) {
         hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
                                        d->compute_units, d->stream);
         if (e == hipSuccess) d->gpu_ops.fetch_add(1);
