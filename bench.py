@@ -10,18 +10,27 @@ resident in HBM before timing. One step = one token's 121 products as ONE
 launch (tmh_plan_run). Steps rotate through enough distinct copies of the
 weights (>= 512 MB) that the 256 MB Infinity Cache cannot serve them.
 
-value = algorithmic bytes per step (weights + f32 x + f32 y) / time per
-step, in GB/s; the roofline object prices the launch against 8 TB/s.
-The CPU baseline times the oracle's restatement of tensomite's CPU path
-(Quant.matmul, all host cores) on the same bytes, and checks the GPU's
-output bits against it.
+value = algorithmic bytes per step (weights + f32 x + f32 y) / wall time
+per step, in GB/s. The roofline object prices the launch against 8 TB/s
+from the median of at least 100 per-launch HIP event times (an event after
+every launch on the library's stream). The CPU baseline times the oracle's
+restatement of tensomite's CPU path (Quant.matmul on every host core, in its
+portable and native builds) on the same bytes, and checks the GPU's output
+bits against it.
 
-A second object, decode_1p7b, reports config 5: greedy decode tokens/s of a
-SmolLM2-1.7B-shaped Q4_0 Llama at batch 1 and 8 through the device-resident
-decoder (every op on the GPU with the host's bits), and the CPU oracle's
-time per token beside it.
+Beside it, in the same line:
+  config1      BASELINE configs[0], the Q8_0 GPT-2 c_attn matvec (2304 x 768):
+               one product a launch, and 128 products (distinct weight
+               copies) a launch; >= 1024 copies rotated; its CPU baseline.
+  decode_1p7b  config 5: greedy decode of a SmolLM2-1.7B-shaped Llama with
+               W ~ N(0, 0.02) quantised to Q4_0, after a 128-token prompt, at
+               batch 1 and 8 through the device-resident decoder (every op on
+               the GPU with the host's bits); the CPU oracle's time per token
+               after the same prompt, and its tokens against the GPU's.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+    python bench.py --batched     # config 3, its own line
+    python bench.py --gemm        # config 4, its own line
 """
 from __future__ import annotations
 
@@ -29,6 +38,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -40,12 +50,17 @@ for _p in (ROOT, os.path.join(ROOT, "tensomite.cr_amd")):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
+ROOFLINE_LAUNCHES = 100
 
 # config 2: (name, n, k) per layer, then the head
 LAYER = [("qkv", 960, 576), ("o", 576, 576), ("gate_up", 3072, 576), ("down", 576, 1536)]
 LAYERS = 30
 HEAD = ("head", 49152, 576)
+
+# config 1: GPT-2-small c_attn
+C_ATTN = (2304, 768)
 
 
 def products_135m():
@@ -61,14 +76,41 @@ def q4_0_bytes(n, k):
     return n * (k // 32) * 18
 
 
+def q8_0_bytes(n, k):
+    return n * (k // 32) * 34
+
+
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles():
+def host_cpu() -> dict:
+    """The host's core count (the threads the CPU baselines use), model and
+    NUMA nodes."""
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    model = "?"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        numa = len([d for d in os.listdir("/sys/devices/system/node") if d.startswith("node")])
+    except OSError:
+        numa = None
+    return {"cores": cores, "nproc": os.cpu_count(), "model": model, "numa_nodes": numa}
+
+
+def traffic_from_profiles(name):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     scaled by a copy kernel's reading), if the committed summary has them."""
-    path = os.path.join(ROOT, "profiles", "traffic_q4_0_set_135m.json")
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             return json.load(f).get("hbm_bytes_per_launch")
@@ -76,95 +118,123 @@ def traffic_from_profiles():
         return None
 
 
-def cpu_baseline(weights, xs, prods, gpu_out, seconds):
-    """The oracle's Quant.matmul restatement on the host's cores, timed over
-    whole tokens for about `seconds`; also checks the GPU's bits."""
+def time_launches(dev, launch, count):
+    """Runs launch(i) for i < count, back to back on the library's stream,
+    with a HIP event after each: the per-launch times in ms and the wall time
+    of the whole (host clock, from the first enqueue to the end of the GPU's
+    work)."""
+    events = [dev.event() for _ in range(count + 1)]
+    t0 = time.perf_counter()
+    dev.record(events[0])
+    for i in range(count):
+        launch(i)
+        dev.record(events[i + 1])
+    dev.sync()
+    wall = time.perf_counter() - t0
+    per = [dev.elapsed_ms(events[i], events[i + 1]) for i in range(count)]
+    for ev in events:
+        dev.destroy_event(ev)
+    return per, wall
+
+
+def warm_up(dev, launch, count, seconds=0.05):
+    """`count` launches, continued until the GPU has been kept busy for
+    `seconds`: after the host-side set-up the GPU's clocks need that long to
+    settle (20 launches of config 2 left the mean ~1 us high)."""
+    done = 0
+    t0 = time.perf_counter()
+    while done < count or time.perf_counter() - t0 < seconds:
+        for _ in range(100 if done >= count else 1):
+            launch(done)
+            done += 1
+        if done >= count:
+            dev.sync()
+    dev.sync()
+    return done
+
+
+def launch_stats(per_ms, algorithmic_bytes):
+    med = statistics.median(per_ms)
+    mean = sum(per_ms) / len(per_ms)
+    return {"launches": len(per_ms), "median_us": round(med * 1e3, 3), "mean_us": round(mean * 1e3, 3),
+            "min_us": round(min(per_ms) * 1e3, 3), "max_us": round(max(per_ms) * 1e3, 3),
+            "GB_per_s_median": round(algorithmic_bytes / (med * 1e-3) / 1e9, 1)}
+
+
+# ---------------------------------------------------------------- CPU baselines
+
+def cpu_products(kind, weights, xs, shapes, gpu_out, seconds, variant, cores):
+    """The oracle's Quant.matmul restatement over a set of one-row products
+    (`variant` build, `cores` threads), timed over whole sets for about
+    `seconds`; with gpu_out, also counts the products whose GPU bits differ."""
     from oracle import oracle
 
-    variant = oracle.best_variant()
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
     oracle.set_threads(cores, variant)
-    # parity: every product's output bits
-    mismatched = 0
-    for i, (name, n, k) in enumerate(prods):
-        want = oracle.matmul("Q4_0", xs[i], weights[i], 1, n, k, variant)[0]
-        if not np.array_equal(want.view(np.uint32), gpu_out[i].view(np.uint32)):
-            mismatched += 1
-    tokens = 0
-    start = time.perf_counter()
+    mismatched = None
+    if gpu_out is not None:
+        mismatched = 0
+        for i, (n, k) in enumerate(shapes):
+            want = oracle.matmul(kind, xs[i], weights[i], 1, n, k, variant)[0]
+            if not np.array_equal(want.view(np.uint32), gpu_out[i].view(np.uint32)):
+                mismatched += 1
+    sets, start = 0, time.perf_counter()
     while True:
-        for i, (name, n, k) in enumerate(prods):
-            oracle.matmul("Q4_0", xs[i], weights[i], 1, n, k, variant)
-        tokens += 1
+        for i, (n, k) in enumerate(shapes):
+            oracle.matmul(kind, xs[i], weights[i], 1, n, k, variant)
+        sets += 1
         elapsed = time.perf_counter() - start
         if elapsed >= seconds:
             break
+    return sets, elapsed, mismatched
+
+
+def cpu_baseline_config2(weights, xs, prods, gpu_out, seconds):
+    """Config 2 on the host: the portable build and the widest native build
+    the CPU runs (the reference's --mcpu=native analogue), every core each;
+    `value` is the faster."""
+    from oracle import oracle
+
+    host = host_cpu()
     algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
+    shapes = [(n, k) for _, n, k in prods]
+    builds = {}
+    for variant in dict.fromkeys(["portable", oracle.best_variant()]):
+        sets, elapsed, mismatched = cpu_products("Q4_0", weights, xs, shapes, gpu_out, seconds, variant,
+                                                 host["cores"])
+        builds[variant] = {"GB_per_s": round(algorithmic * sets / elapsed / 1e9, 2),
+                           "ms_per_token": round(elapsed / sets * 1e3, 3), "tokens": sets,
+                           "seconds": round(elapsed, 2), "parity_mismatched_products": mismatched}
+    best = max(builds, key=lambda v: builds[v]["GB_per_s"])
     return {
-        "value": algorithmic * tokens / elapsed / 1e9,
+        "value": builds[best]["GB_per_s"],
         "unit": "GB/s",
-        "cores": cores,
+        "cores": host["cores"],
         "kind": "port",
-        "sample": f"{tokens} tokens of the config-2 set (121 products each) in {elapsed:.1f} s; "
-                  f"oracle Quant.matmul restatement, {variant} build, spin pool of {cores} threads",
-        "ms_per_token": elapsed / tokens * 1e3,
-        "parity_mismatched_products": mismatched,
+        "sample": f"whole tokens of the config-2 set (121 one-row products each) for ~{seconds:.0f} s per build; "
+                  f"the oracle's Quant.matmul restatement with the reference's span rule and spin pool, "
+                  f"{host['cores']} threads; value from the {best} build",
+        "ms_per_token": builds[best]["ms_per_token"],
+        "builds": builds,
+        "host": host,
+        "parity_mismatched_products": builds[best]["parity_mismatched_products"],
     }
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
-    ap.add_argument("--decode-steps", type=int, default=256)
-    ap.add_argument("--batched", action="store_true",
-                    help="config 3 instead (Q4_1 batched-decode products, B = 1..16); its own JSON line")
-    ap.add_argument("--gemm", action="store_true",
-                    help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
-    ap.add_argument("--decode-eager", action="store_true",
-                    help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
-              "a product shards by output rows across GPUs, each GPU running this kernel on its share",
-              file=sys.stderr)
-        sys.exit(1)
+# ---------------------------------------------------------------- config 2
 
+def build_config2(dev, copies):
+    """Config 2's inputs on the device: the 121 products' Q4_0 weights (W ~
+    N(0, 0.02) quantised, seed 0x5EED0002 + i) packed into one buffer per
+    copy at 256-byte offsets, x ~ N(0, 1) per product, outputs, and one plan
+    per copy (the launch bench.py times)."""
     import quant_host
-    import tensomite_hip as th
 
-    dev = th.HIPDevice(0)
-    log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
-    if args.gemm:
-        print(json.dumps(gemm_config4(dev, args.steps, args.warmup)), flush=True)
-        return
-    if args.batched:
-        print(json.dumps(batched_config3(dev, args.steps, args.warmup)), flush=True)
-        return
     prods = products_135m()
-    weight_bytes = sum(q4_0_bytes(n, k) for _, n, k in prods)
-    algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
-    copies = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
-
-    # Host weights (one copy), quantised by the package's host quantiser.
-    t0 = time.perf_counter()
     rng = np.random.default_rng(0x5EED0002)
     weights, xs = [], []
     for i, (name, n, k) in enumerate(prods):
         weights.append(quant_host.synthetic_weights("Q4_0", n, k, seed=0x5EED0002 + i))
-        xs.append(rng.normal(0.0, 1.0, k).astype(np.float32))
-    log(f"weights quantised in {time.perf_counter() - t0:.1f} s; {weight_bytes / 1e6:.1f} MB per token, "
-        f"{copies} copies = {copies * weight_bytes / 1e6:.0f} MB")
-
-    # Device: one packed weight buffer per copy, activations, outputs.
+        xs.append(rng.standard_normal(k, dtype=np.float32))
     offsets, off = [], 0
     for w in weights:
         offsets.append(off)
@@ -183,63 +253,55 @@ def main():
     ybufs = [dev.alloc(4 * n) for _, n, _ in prods]
     plans = []
     for c in range(copies):
-        items = []
-        for i, (name, n, k) in enumerate(prods):
-            items.append((wbufs[c], 0, xbufs[i], ybufs[i], None, n, k))
-        # w_row is in rows; the packed offset is in bytes: pass it through a view
-        plan_items = []
-        for i, (w, _, x, y, b, n, k) in enumerate(items):
-            plan_items.append((_View(w, offsets[i]), 0, x, y, b, n, k))
-        plans.append(dev.plan("Q4_0", plan_items))
+        items = [(_View(wbufs[c], offsets[i]), 0, xbufs[i], ybufs[i], None, n, k)
+                 for i, (name, n, k) in enumerate(prods)]
+        plans.append(dev.plan("Q4_0", items))
     dev.sync()
+    return {"prods": prods, "weights": weights, "xs": xs, "offsets": offsets, "wbufs": wbufs, "xbufs": xbufs,
+            "ybufs": ybufs, "plans": plans, "packed_bytes": int(packed.nbytes)}
 
-    # Warm-up, then the timed region: K launches back to back. The warm-up is
-    # W launches, continued until they have kept the GPU busy for at least
-    # 50 ms: the set takes ~16 us, and after the host-side set-up the GPU's
-    # clocks need that long to settle (20 launches leave the mean ~1 us high).
-    warm = 0
-    t_warm = time.perf_counter()
-    while warm < args.warmup or time.perf_counter() - t_warm < 0.05:
-        for _ in range(100 if warm >= args.warmup else 1):
-            plans[warm % copies].run()
-            warm += 1
-        if warm >= args.warmup:
-            dev.sync()
-    dev.sync()
-    # HIP events on the library's stream bracket the K launches (one launch
-    # per step, back to back): their mean is the kernel's launch duration.
-    ev0, ev1 = dev.event(), dev.event()
-    t_start = time.perf_counter()
-    dev.record(ev0)
-    for s in range(args.steps):
-        plans[s % copies].run()
-    dev.record(ev1)
-    dev.sync()
-    t_end = time.perf_counter()
-    ms_per_step = (t_end - t_start) * 1e3 / args.steps
-    launch_ms = dev.elapsed_ms(ev0, ev1) / args.steps
+
+def config2(dev, args):
+    import tensomite_hip as th
+
+    prods = products_135m()
+    weight_bytes = sum(q4_0_bytes(n, k) for _, n, k in prods)
+    algorithmic = sum(q4_0_bytes(n, k) + 4 * k + 4 * n for _, n, k in prods)
+    copies = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
+    t0 = time.perf_counter()
+    c2 = build_config2(dev, copies)
+    plans, wbufs, xbufs, ybufs, offsets = (c2[key] for key in ("plans", "wbufs", "xbufs", "ybufs", "offsets"))
+    log(f"config 2 built in {time.perf_counter() - t0:.1f} s; {weight_bytes / 1e6:.1f} MB per token, "
+        f"{copies} copies = {copies * weight_bytes / 1e6:.0f} MB")
+
+    run = lambda i: plans[i % copies].run()
+    warm = warm_up(dev, run, args.warmup)
+    # The timed region: K launches back to back, an event after each.
+    per, wall = time_launches(dev, run, args.steps)
+    ms_per_step = wall * 1e3 / args.steps
     value = algorithmic / (ms_per_step * 1e-3) / 1e9
-    achieved = algorithmic / (launch_ms * 1e-3) / 1e9
-
-    # Outputs of the last step, for the CPU parity check.
+    # The roofline: the median of at least ROOFLINE_LAUNCHES per-launch times.
+    if len(per) < ROOFLINE_LAUNCHES:
+        more, _ = time_launches(dev, lambda i: run(args.steps + i), ROOFLINE_LAUNCHES - len(per))
+        per = per + more
+    stats = launch_stats(per, algorithmic)
+    achieved = stats["GB_per_s_median"]
     gpu_out = [dev.to_array(y, np.float32, n) for y, (_, n, _) in zip(ybufs, prods)]
 
     # Per-product launches (the reference's one launch per product), for comparison.
-    for s in range(3):
+    def per_product(s):
         for i, (name, n, k) in enumerate(prods):
-            dev.lib.tmh_block_matmul(th.Q4_0, wbufs[s % copies].pointer, offsets[i], xbufs[i].pointer, k,
-                                     ybufs[i].pointer, 0, 1, n, k, 0)
-    dev.sync()
-    reps = 20
+            th.check("tmh_block_matmul", dev.lib.tmh_block_matmul(
+                th.Q4_0, wbufs[s % copies].pointer, offsets[i], xbufs[i].pointer, k, ybufs[i].pointer, 0, 1, n, k,
+                0))
+    warm_up(dev, per_product, 3, seconds=0.0)
     e0, e1 = dev.event(), dev.event()
     dev.record(e0)
-    for s in range(reps):
-        for i, (name, n, k) in enumerate(prods):
-            dev.lib.tmh_block_matmul(th.Q4_0, wbufs[s % copies].pointer, offsets[i], xbufs[i].pointer, k,
-                                     ybufs[i].pointer, 0, 1, n, k, 0)
+    for s in range(20):
+        per_product(s)
     dev.record(e1)
     dev.sync()
-    per_product_ms = dev.elapsed_ms(e0, e1) / reps
+    per_product_ms = dev.elapsed_ms(e0, e1) / 20
 
     result = {
         "metric": "Q4_0 matvec HBM GB/s (% peak); decode tokens/sec at 1.7B Llama shape",
@@ -262,18 +324,23 @@ def main():
             "algorithmic_bytes_per_step": algorithmic,
             "weight_copies_rotated": copies,
             "rotated_bytes": copies * weight_bytes,
-            "copy_bytes": int(packed.nbytes),
+            "copy_bytes": c2["packed_bytes"],
         },
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
         "roofline": {
             "kernel": plans[0].describe() + " (Q4_0; one launch = the 121 products of a token)",
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles(),
-            "launch_us_mean": round(launch_ms * 1e3, 2),
+            "traffic": traffic_from_profiles("traffic_q4_0_set_135m.json"),
+            "algorithmic_bytes_per_launch": algorithmic,
+            "launch_us_median": stats["median_us"],
+            "launch_us_mean": stats["mean_us"],
+            "launch_us_min": stats["min_us"],
+            "launch_us_max": stats["max_us"],
+            "launches": stats["launches"],
             "warmup_launches": warm,
         },
         "per_product_launches": {
@@ -283,50 +350,147 @@ def main():
         },
     }
     if not args.no_cpu:
-        log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(weights, xs, prods, gpu_out, args.cpu_seconds)
+        log("cpu baseline (config 2) ...")
+        result["cpu_baseline"] = cpu_baseline_config2(c2["weights"], c2["xs"], prods, gpu_out, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
-    for buf in wbufs:
+    for plan in plans:
+        plan.destroy()
+    for buf in wbufs + xbufs + ybufs:
         buf.release()
     dev.sync()
-    if not args.no_decode:
-        log("decode at the 1.7B shape ...")
-        result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
-                                            graph=not args.decode_eager)
-    print(json.dumps(result), flush=True)
+    return result
 
+
+# ---------------------------------------------------------------- config 1
+
+def config1(dev, args, batch=128, min_copies=1024):
+    """W [2304, 768] ~ N(0, 0.02) quantised to Q8_0, x
+    ~ N(0, 1), y = W·x. Two figures, both rotating through >= 1024 distinct
+    weight copies (1.9 GB, past the 256 MB Infinity Cache):
+      single   one tmh_block_matmul a launch (the one-row kernel), the median
+               of >= 100 per-launch event times;
+      batched  `batch` products a launch (a plan over distinct copies and
+               outputs, the same x), as the median per launch.
+    Bytes a product: weights + 4·K of x + 4·N of y (1,892,352 B)."""
+    import quant_host
+    import tensomite_hip as th
+
+    n, k = C_ATTN
+    wbytes = q8_0_bytes(n, k)
+    algorithmic = wbytes + 4 * k + 4 * n
+    copies = max(min_copies, math.ceil(2 * MALL_BYTES / wbytes))
+    copies = (copies + batch - 1) // batch * batch
+    host = quant_host.synthetic_weights("Q8_0", n, k, seed=0x5EED0001)
+    x_host = np.random.default_rng(0x5EED0001 + 1).standard_normal(k, dtype=np.float32)
+    stride = (wbytes + 255) // 256 * 256
+    per_buffer = 256  # copies a device buffer holds
+    buffers, views = [], []
+    first = dev.from_array(host)
+    for b in range(copies // per_buffer):
+        buf = dev.alloc(stride * per_buffer)
+        for j in range(per_buffer):
+            dev.copy(buf, first, wbytes, dst_offset=j * stride)
+            views.append(_View(buf, j * stride))
+        buffers.append(buf)
+    x = dev.from_array(x_host)
+    y = dev.alloc(4 * n)
+    ys = [dev.alloc(4 * n) for _ in range(batch)]
+    dev.sync()
+
+    def single(i):
+        th.check("tmh_block_matmul", dev.lib.tmh_block_matmul(th.Q8_0, views[i % copies].pointer, 0, x.pointer, k,
+                                                               y.pointer, 0, 1, n, k, 0))
+    warm_up(dev, single, args.warmup)
+    launches = max(ROOFLINE_LAUNCHES, args.steps)
+    per, wall = time_launches(dev, single, launches)
+    s_stats = launch_stats(per, algorithmic)
+    gpu_y = dev.to_array(y, np.float32, n)
+
+    plans = [dev.plan("Q8_0", [(views[p * batch + j], 0, x, ys[j], None, n, k) for j in range(batch)])
+             for p in range(copies // batch)]
+    run = lambda i: plans[i % len(plans)].run()
+    warm_up(dev, run, args.warmup)
+    per_b, _ = time_launches(dev, run, max(ROOFLINE_LAUNCHES, args.steps))
+    b_stats = launch_stats(per_b, algorithmic * batch)
+    batched_y = dev.to_array(ys[batch - 1], np.float32, n)
+    out = {
+        "workload": "config 1: GPT-2-small c_attn, Q8_0 W [2304, 768] x f32 [768] -> [2304]",
+        "algorithmic_bytes_per_product": algorithmic,
+        "weight_copies_rotated": copies,
+        "rotated_bytes": copies * wbytes,
+        "single": dict(s_stats, kernel="one tmh_block_matmul (k_matvec_row) a launch",
+                       roofline={"bound": "hbm", "achieved": s_stats["GB_per_s_median"], "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(s_stats["GB_per_s_median"] / HBM_PEAK_GBS, 4),
+                                 "traffic": traffic_from_profiles("traffic_q8_0_c_attn.json")}),
+        "batched": dict(b_stats, products_per_launch=batch, kernel=plans[0].describe(),
+                        roofline={"bound": "hbm", "achieved": b_stats["GB_per_s_median"], "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(b_stats["GB_per_s_median"] / HBM_PEAK_GBS, 4)}),
+    }
+    if not args.no_cpu:
+        from oracle import oracle
+        hostinfo = host_cpu()
+        builds = {}
+        for variant in dict.fromkeys(["portable", oracle.best_variant()]):
+            sets, elapsed, mismatched = cpu_products("Q8_0", [host], [x_host], [(n, k)], [gpu_y],
+                                                     args.cpu_seconds / 2, variant, hostinfo["cores"])
+            builds[variant] = {"GB_per_s": round(algorithmic * sets / elapsed / 1e9, 2),
+                               "us_per_product": round(elapsed / sets * 1e6, 2), "products": sets,
+                               "parity_mismatched": mismatched}
+        want = oracle.matmul("Q8_0", x_host, host, 1, n, k)[0]
+        best = max(builds, key=lambda v: builds[v]["GB_per_s"])
+        out["cpu_baseline"] = {
+            "value": builds[best]["GB_per_s"], "unit": "GB/s", "cores": hostinfo["cores"], "kind": "port",
+            "sample": f"the one product repeated for ~{args.cpu_seconds / 2:.0f} s per build (weights stay in the "
+                      f"host's caches: 1.9 MB); oracle Quant.matmul restatement, {hostinfo['cores']} threads; "
+                      f"value from the {best} build",
+            "builds": builds,
+            "batched_parity_ok": bool(np.array_equal(batched_y.view(np.uint32), want.view(np.uint32)))}
+    for plan in plans:
+        plan.destroy()
+    for buf in buffers + [first, x, y] + ys:
+        buf.release()
+    dev.sync()
+    return out
+
+
+# ---------------------------------------------------------------- config 5
 
 def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
-    """Config 5: greedy decode of a SmolLM2-1.7B-shaped Q4_0 Llama (random
-    block weights, tied head) through the device-resident decoder, after a
-    128-token prompt, at batch 1 and batch 8 (f32 KV capacity 2048). A step is
-    one token per row, replayed from a captured HIP graph; timed with HIP
-    events on the library's stream. The CPU figure is the oracle's forward
-    (the restatement of tensomite's host path) per decoded token after a
-    short prompt, on a bounded sample."""
+    """Config 5: greedy decode of a SmolLM2-1.7B-shaped Llama, every matrix
+    W ~ N(0, 0.02) quantised to Q4_0 (quant_host.synthetic_llama, tied head),
+    through the device-resident decoder, after a 128-token prompt, at batch 1
+    and batch 8 (f32 KV capacity 2048). A step is one token per row, replayed
+    from a captured HIP graph, timed with HIP events on the library's stream.
+    The CPU figure is the oracle's forward (the restatement of tensomite's
+    host path) per decoded token after the same 128-token prompt as the
+    GPU's batch 1, on a bounded sample; its tokens are compared with the
+    GPU's."""
     import quant_host
     import tensomite_hip as th
 
     config = dict(quant_host.SMOLLM2_1P7B)
     t0 = time.perf_counter()
-    weights = quant_host.random_block_llama(config, seed=0x5EED0005)
+    weights = quant_host.synthetic_llama(config, seed=0x5EED0005)
     log(f"1.7B weights in {time.perf_counter() - t0:.1f} s")
-    rng = np.random.default_rng(0x5EED0005)
-    out = {"model": "SmolLM2-1.7B shape, Q4_0, tied head (random block weights)", "prompt": 128,
-           "capacity": 2048}
+    rng = np.random.default_rng(0x5EED0005 + 1)
+    prompts = [[int(t) for t in rng.integers(0, config["vocab"], 128)] for _ in range(8)]
+    out = {"model": "SmolLM2-1.7B shape, Q4_0, tied head; W ~ N(0, 0.02) quantised (synthetic_llama), norms 1",
+           "prompt": 128, "capacity": 2048}
     weight_bytes = sum(w.nbytes for key in ("qkv", "o", "gate_up", "down") for w in weights[key]) + \
         weights["embed"].nbytes
     out["weight_bytes_per_token"] = weight_bytes
+    gpu_tokens = None
     for rows in (1, 8):
         model = th.HIPLlama(dev, config, weights, rows=rows, capacity=2048, max_tokens=128)
         prefill = []
         for r in range(rows):
-            prompt = list(rng.integers(0, config["vocab"], 128))
             t = time.perf_counter()
-            model.forward(prompt, row=r, last_only=True)
+            model.forward(prompts[r], row=r, last_only=True)
             prefill.append(time.perf_counter() - t)
-        model.generate(4, graph=graph)  # graph captured, state on the device
+        tokens = model.generate(steps, graph=graph)  # graph captured, state on the device
+        if rows == 1:
+            gpu_tokens = [int(t) for t in tokens[0]]
         for _ in range(4):
             model.step(graph=graph)
         dev.sync()
@@ -335,43 +499,48 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
         for _ in range(steps):
             model.step(graph=graph)
         dev.record(e1)
-        ms = dev.elapsed_ms(e0, e1) / steps
         dev.sync()
+        ms = dev.elapsed_ms(e0, e1) / steps
         out[f"batch{rows}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(rows * 1e3 / ms, 1), "graph": graph,
-                               "steps": steps, "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
+                               "steps": steps, "positions": f"{128 + steps + 3}..{128 + 2 * steps + 2}",
+                               "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
                                "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
         model.destroy()
         log(f"decode batch {rows}: {ms * 1e3:.0f} us/step")
     if with_cpu:
         from oracle import oracle
-        try:
-            cores = len(os.sched_getaffinity(0))
-        except AttributeError:
-            cores = os.cpu_count() or 1
-        cores = max(1, min(cores, 16))
+        host = host_cpu()
         variant = oracle.best_variant()
-        oracle.set_threads(cores, variant)
+        oracle.set_threads(host["cores"], variant)
         cpu = oracle.Llama(config, weights, variant)
-        cpu.forward(list(rng.integers(0, config["vocab"], 8)), last_only=True)
-        tokens, start = 0, time.perf_counter()
-        token = 0
-        while time.perf_counter() - start < cpu_seconds and tokens < 64:
-            token = oracle.argmax(cpu.forward([token], last_only=True)[0])
-            tokens += 1
+        logits = cpu.forward(prompts[0], last_only=True)[0]
+        cpu_tokens, start = [], time.perf_counter()
+        while True:
+            cpu_tokens.append(oracle.argmax(logits))
+            if time.perf_counter() - start >= cpu_seconds or len(cpu_tokens) >= 64:
+                break
+            logits = cpu.forward([cpu_tokens[-1]], last_only=True)[0]
         elapsed = time.perf_counter() - start
-        out["cpu_baseline"] = {"ms_per_token": round(elapsed / tokens * 1e3, 1), "cores": cores, "kind": "port",
-                               "sample": f"{tokens} greedy tokens after an 8-token prompt, batch 1; the oracle's "
-                                         f"Llama forward ({variant} build, {cores} threads)"}
+        decoded = len(cpu_tokens) - 1
+        out["cpu_baseline"] = {
+            "ms_per_token": round(elapsed / max(decoded, 1) * 1e3, 1), "cores": host["cores"], "kind": "port",
+            "sample": f"{decoded} greedy decode steps at positions 128..{128 + decoded - 1}, after the GPU's "
+                      f"batch-1 128-token prompt (prefill excluded); the oracle's Llama forward ({variant} build, "
+                      f"{host['cores']} threads)",
+            "tokens_equal_gpu": gpu_tokens is not None and cpu_tokens == gpu_tokens[:len(cpu_tokens)],
+            "tokens_compared": len(cpu_tokens)}
     return out
 
+
+# ---------------------------------------------------------------- config 3
 
 def batched_config3(dev, steps, warmup):
     """Config 3: Q4_1 batched-decode products, W [8192, 2048] and [2048, 8192]
     against B = 1, 2, 4, 8, 16 activation rows. One call is tmh_block_matmul
     over f32 x (the activation quantiser, then the lanes product); calls
     rotate through enough weight copies (>= 512 MB) that the 256 MB Infinity
-    Cache cannot serve them; HIP events over `steps` calls. Bytes a call:
-    weights + 4·B·K of x + 4·B·N of y."""
+    Cache cannot serve them; per-call HIP events, the median of >= 100.
+    Bytes a call: weights + 4·B·K of x + 4·B·N of y."""
     import quant_host
     out = {"metric": "Q4_1 batched-decode product GB/s (config 3)", "unit": "GB/s", "n_gpus": 1, "steps": steps,
            "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
@@ -385,22 +554,16 @@ def batched_config3(dev, steps, warmup):
         for w in ws[1:]:
             dev.copy(w, first, host.nbytes)
         for b in (1, 2, 4, 8, 16):
-            x = dev.from_array(rng.normal(0.0, 1.0, (b, k)).astype(np.float32))
+            x = dev.from_array(rng.standard_normal((b, k), dtype=np.float32))
             dst = dev.alloc(4 * b * n)
-            for i in range(warmup):
-                dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
-            dev.sync()
-            e0, e1 = dev.event(), dev.event()
-            dev.record(e0)
-            for i in range(steps):
-                dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
-            dev.record(e1)
-            dev.sync()
-            ms = dev.elapsed_ms(e0, e1) / steps
+            call = lambda i: dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
+            warm_up(dev, call, warmup)
+            per, _ = time_launches(dev, call, max(ROOFLINE_LAUNCHES, steps))
             nbytes = host.nbytes + 4 * b * k + 4 * b * n
-            out["shapes"][f"{n}x{k} B={b}"] = {"us_per_call": round(ms * 1e3, 2),
-                                               "GB_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                                               "hbm_peak_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            st = launch_stats(per, nbytes)
+            out["shapes"][f"{n}x{k} B={b}"] = {"us_per_call_median": st["median_us"], "us_per_call_mean": st["mean_us"],
+                                               "GB_per_s": st["GB_per_s_median"],
+                                               "hbm_peak_frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 3)}
             x.release()
             dst.release()
         for w in ws:
@@ -409,35 +572,38 @@ def batched_config3(dev, steps, warmup):
     return out
 
 
-def gemm_config4(dev, steps, warmup):
+# ---------------------------------------------------------------- config 4
+
+def gemm_config4(dev, steps, warmup, mode="auto"):
     """Config 4: the Q8_0 prefill GEMM at the Llama-1.7B shape, 512 tokens x
     K = 2048 against N = 2048 (attention projections) and N = 8192 (MLP
     up/gate). One call is tmh_block_matmul over f32 x (the activation
-    quantiser, then the matrix-core kernel, k_matmul_mfma); timed with HIP
-    events over `steps` calls. int8 work: 2 · 512 · 2048 · N ops a call."""
+    quantiser, then the matrix-core kernel, k_matmul_mfma); per-call HIP
+    events, the median of >= 100. int8 work: 2 · 512 · 2048 · N ops a call.
+    mode "unordered" runs the measurement kernel that sums the raw MFMA
+    results without the block-ordered epilogue."""
     import quant_host
+    import tensomite_hip as th
     rows, k = 512, 2048
     rng = np.random.default_rng(0x5EED0004)
-    x = dev.from_array(rng.normal(0.0, 1.0, (rows, k)).astype(np.float32))
+    x = dev.from_array(rng.standard_normal((rows, k), dtype=np.float32))
     out = {"metric": "Q8_0 prefill GEMM int8 TOP/s (config 4, 512 tokens x K=2048)", "unit": "TOP/s",
            "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
-           "data": "synthetic: W ~ N(0,0.02) quantised to Q8_0, x ~ N(0,1)", "shapes": {}}
+           "mode": mode, "data": "synthetic: W ~ N(0,0.02) quantised to Q8_0, x ~ N(0,1)", "shapes": {}}
     for n in (2048, 8192):
         w = dev.from_array(quant_host.synthetic_weights("Q8_0", n, k, seed=0x5EED0004 + n))
         dst = dev.alloc(4 * rows * n)
-        for _ in range(warmup):
-            dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst)
-        dev.sync()
-        e0, e1 = dev.event(), dev.event()
-        dev.record(e0)
-        for _ in range(steps):
-            dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst)
-        dev.record(e1)
-        dev.sync()
-        ms = dev.elapsed_ms(e0, e1) / steps
+        call = lambda i: dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst, mode=mode)
+        warm_up(dev, call, warmup)
+        per, _ = time_launches(dev, call, max(ROOFLINE_LAUNCHES, steps))
+        med = statistics.median(per)
         ops = 2.0 * rows * k * n
-        out["shapes"][f"N={n}"] = {"ms_per_call": round(ms, 4), "TOP_per_s": round(ops / (ms * 1e-3) / 1e12, 1),
-                                   "int8_mfma_peak_frac": round(ops / (ms * 1e-3) / 5.0e15, 4)}
+        tops = ops / (med * 1e-3) / 1e12
+        out["shapes"][f"N={n}"] = {"us_per_call_median": round(med * 1e3, 2),
+                                   "us_per_call_mean": round(sum(per) / len(per) * 1e3, 2),
+                                   "TOP_per_s": round(tops, 1),
+                                   "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                                                "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4)}}
         w.release()
         dst.release()
     out["value"] = out["shapes"]["N=8192"]["TOP_per_s"]
@@ -445,11 +611,57 @@ def gemm_config4(dev, steps, warmup):
 
 
 class _View:
-    """A buffer seen from a byte offset (a product's weights inside the packed buffer)."""
+    """A buffer seen from a byte offset (a product's weights inside a packed buffer)."""
 
     def __init__(self, buf, offset):
+        self.buffer = buf
         self.pointer = buf.pointer + offset
         self.bytesize = buf.bytesize - offset
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
+    ap.add_argument("--no-config1", action="store_true", help="skip the config-1 (GPT-2 c_attn) measurement")
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--batched", action="store_true",
+                    help="config 3 instead (Q4_1 batched-decode products, B = 1..16); its own JSON line")
+    ap.add_argument("--gemm", action="store_true",
+                    help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
+    ap.add_argument("--gemm-mode", default="auto", help="config 4's BlockMatMulMode (auto, matrix, unordered)")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
+              "a product shards by output rows across GPUs, each GPU running this kernel on its share",
+              file=sys.stderr)
+        sys.exit(1)
+
+    import tensomite_hip as th
+
+    dev = th.HIPDevice(0)
+    log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
+    if args.gemm:
+        print(json.dumps(gemm_config4(dev, args.steps, args.warmup, args.gemm_mode)), flush=True)
+        return
+    if args.batched:
+        print(json.dumps(batched_config3(dev, args.steps, args.warmup)), flush=True)
+        return
+    result = config2(dev, args)
+    if not args.no_config1:
+        log("config 1 ...")
+        result["config1"] = config1(dev, args)
+    if not args.no_decode:
+        log("decode at the 1.7B shape ...")
+        result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
+                                            graph=not args.decode_eager)
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

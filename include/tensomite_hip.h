@@ -189,6 +189,12 @@ int tmh_debug_fail_allocations(int32_t count);
  * (cuda.cr:1164-1172). */
 int tmh_debug_disable_kernels(int32_t off);
 
+/* Test hook: dst[i] (uint16, device) = the F16 bits the device's kernels
+ * round the float with bit pattern first + i to (F16.new, f16.cr:29-41),
+ * for i < count: lets a test sweep every f32 word through the device's own
+ * conversion (the activation scales and sums use it). Queued on the stream. */
+int tmh_debug_f16_words(uint32_t first, uint32_t count, uint64_t dst);
+
 /* ------------------------------------------------------------ events */
 
 /* Timing on the library's stream: cuEventCreate/Record/ElapsedTime
@@ -236,6 +242,13 @@ int tmh_block_matmul_quantised(uint32_t kind, uint64_t w, uint64_t w_byte_offset
  * host.cr:648-658). */
 int tmh_gather_blocks(uint32_t kind, uint64_t table, uint64_t table_byte_offset, int32_t table_rows, uint32_t width,
                       uint64_t ids, uint32_t count, uint64_t dst);
+
+/* Quantises `count` host f32 values (a whole number of blocks of 32) into
+ * host block bytes `out`: Quant.quantize (quant.cr:77-90, 497-535), the step
+ * Tensor#quantize runs on the host for every device (tensor/quantised.cr:11-19).
+ * Blocks are split over `threads` host threads (0: every core); the bytes do
+ * not depend on the split. Needs no GPU. */
+int tmh_quantize_weights(uint32_t kind, const float* values, uint64_t count, uint8_t* out, int32_t threads);
 
 /* ------------------------------------------------------------ plans */
 

@@ -17,7 +17,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libtensomite_hip.so")
-SOURCES = [os.path.join(HERE, "csrc", name) for name in ("tmh_runtime.hip", "tmh_kernels.hip", "tmh_decode.hip", "tmh_llama.hip", "tmh_gguf.hip")]
+SOURCES = [os.path.join(HERE, "csrc", name) for name in ("tmh_runtime.hip", "tmh_kernels.hip", "tmh_decode.hip", "tmh_llama.hip", "tmh_gguf.hip", "tmh_quant_host.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -35,9 +35,7 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, *SOURCES, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -47,6 +45,23 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every source to an object in parallel (the same flags), then
+    links the shared library; always recompiles."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objects = [os.path.join(objdir, os.path.basename(src) + ".o") for src in SOURCES]
+    jobs = [[HIPCC, *compile_flags, "-c", src, "-o", obj] for src, obj in zip(SOURCES, objects)]
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-fno-gpu-rdc", *objects, "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

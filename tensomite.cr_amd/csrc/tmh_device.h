@@ -26,7 +26,7 @@ __device__ __forceinline__ float half_value(uint32_t bits) {
 // Returns x rounded to the nearest half, ties to even, as a float: F16.new
 // (f16.cr:29-41) -- NaN becomes 0x7e00, values from 65520 up overflow,
 // subnormals are x * 2^24 rounded to even.
-__device__ __forceinline__ float round_to_half(float x) {
+__device__ __forceinline__ uint32_t round_to_half_bits(float x) {
     uint32_t word = __float_as_uint(x);
     uint32_t sign = (word >> 16) & 0x8000u;
     uint32_t magnitude = word & 0x7fffffffu;
@@ -35,8 +35,10 @@ __device__ __forceinline__ float round_to_half(float x) {
     else if (magnitude >= 0x477ff000u) h = sign | 0x7c00u;
     else if (magnitude < 0x38800000u) h = sign | (uint32_t)__builtin_rintf(__uint_as_float(magnitude) * 16777216.0f);
     else h = sign | ((magnitude - 0x38000000u + 0xfffu + ((magnitude >> 13) & 1u)) >> 13);
-    return half_value(h);
+    return h;
 }
+
+__device__ __forceinline__ float round_to_half(float x) { return half_value(round_to_half_bits(x)); }
 
 // ------------------------------------------------------ activation quantise
 

@@ -169,9 +169,15 @@ int Gguf::open(const char* file) {
         in.offset = r.get<uint64_t>();
         if (!r.ok) return TMH_ERROR_INVALID_VALUE;
     }
+    // general.alignment (32 by default, gguf.cr:312): a power of two of at
+    // most 1 MiB, so the rounding below cannot overflow.
     int64_t alignment = 32;
     auto a = metadata.find("general.alignment");
-    if (a != metadata.end() && a->second.i > 0) alignment = a->second.i;
+    if (a != metadata.end()) {
+        alignment = a->second.i;
+        if (alignment <= 0 || alignment > (1ll << 20) || (alignment & (alignment - 1)) != 0)
+            return TMH_ERROR_INVALID_VALUE;
+    }
     const uint64_t start = (r.pos + (uint64_t)alignment - 1) / (uint64_t)alignment * (uint64_t)alignment;
     for (const Info& in : infos) {
         GgufTensor t;
@@ -187,9 +193,12 @@ int Gguf::open(const char* file) {
         if (t.bytes == 0) return TMH_ERROR_DTYPE;  // a kind this reader does not know
         const bool block = t.kind == GGUF_Q4_0 || t.kind == GGUF_Q4_1 || t.kind == GGUF_Q8_0;
         if (block && t.shape.back() % 32 != 0) return TMH_ERROR_SHAPE;
-        t.offset = start + in.offset;
-        if (in.offset % (uint64_t)alignment != 0 || t.offset > size || t.bytes > size - t.offset)
+        // Offsets are checked against the file before they are added, so a
+        // damaged offset near 2^64 cannot wrap into the file (gguf.cr:320).
+        if (start > size || in.offset > size - start || in.offset % (uint64_t)alignment != 0)
             return TMH_ERROR_INVALID_VALUE;
+        t.offset = start + in.offset;
+        if (t.bytes > size - t.offset) return TMH_ERROR_INVALID_VALUE;
         index[t.name] = (int)tensors.size();
         tensors.push_back(t);
     }

@@ -162,6 +162,9 @@ hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations 
 hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations act, uint32_t rows, uint32_t H,
                                  uint32_t k, Activations glu, hipStream_t stream);
 
+// dst[i] = the F16 bits of the float with word first + i, i < count.
+hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream);
+
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);

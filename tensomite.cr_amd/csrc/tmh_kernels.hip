@@ -1389,7 +1389,21 @@ __global__ __launch_bounds__(256) void k_gather_blocks(const uint8_t* __restrict
     dst[i] = v;
 }
 
+// dst[i] = F16 bits of the float whose word is first + i (the test hook
+// tmh_debug_f16_words): the device's own f32 -> f16 rounding, swept.
+__global__ __launch_bounds__(256) void k_f16_words(uint32_t first, uint32_t count, uint16_t* __restrict__ dst) {
+    for (uint64_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += (uint64_t)gridDim.x * 256u)
+        dst[i] = (uint16_t)round_to_half_bits(__uint_as_float(first + (uint32_t)i));
+}
+
 // ---------------------------------------------------------------- launchers
+
+hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream) {
+    if (count == 0) return hipSuccess;
+    const uint32_t grid = std::min<uint32_t>((count + 255u) / 256u, 65536u);
+    hipLaunchKernelGGL(k_f16_words, dim3(grid), dim3(256), 0, stream, first, count, dst);
+    return hipGetLastError();
+}
 
 hipError_t launch_quantize(const float* x, uint32_t ldx, uint32_t rows, uint32_t k, float* scales, float* sums,
                            int32_t* totals, int8_t* qs, hipStream_t stream) {

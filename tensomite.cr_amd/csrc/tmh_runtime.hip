@@ -215,8 +215,8 @@ struct Device {
     // (cuda.cr:788-798); `launch` keeps a quantise pass and its product
     // together.
     std::mutex launch;
-    uint8_t* scratch = nullptr;
-    size_t scratch_bytes = 0;
+    uint8_t* act_scratch = nullptr;
+    size_t act_scratch_bytes = 0;
 
     Pool pool;
     Retired* retired = nullptr;
@@ -299,18 +299,18 @@ void recycle_retired(Device& d) {
 // Grows the activation scratch to at least `bytes`, waiting for the work
 // that may still read the old one.
 int ensure_scratch(Device& d, size_t bytes) {
-    if (bytes <= d.scratch_bytes) return TMH_SUCCESS;
+    if (bytes <= d.act_scratch_bytes) return TMH_SUCCESS;
     size_t grown = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
     hipError_t e = hipStreamSynchronize(d.stream);
     if (e != hipSuccess) return code(e);
-    if (d.scratch) (void)hipFree(d.scratch);
-    d.scratch = nullptr;
-    d.scratch_bytes = 0;
+    if (d.act_scratch) (void)hipFree(d.act_scratch);
+    d.act_scratch = nullptr;
+    d.act_scratch_bytes = 0;
     void* p = nullptr;
     e = device_malloc(&p, grown);
     if (e != hipSuccess) return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : code(e);
-    d.scratch = (uint8_t*)p;
-    d.scratch_bytes = grown;
+    d.act_scratch = (uint8_t*)p;
+    d.act_scratch_bytes = grown;
     return TMH_SUCCESS;
 }
 
@@ -630,6 +630,18 @@ int tmh_debug_disable_kernels(int32_t off) {
     return TMH_SUCCESS;
 }
 
+int tmh_debug_f16_words(uint32_t first, uint32_t count, uint64_t dst) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (count == 0) return TMH_SUCCESS;
+    if (!dst || dst % 2u != 0 || (uint64_t)first + count > (1ull << 32)) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = tmh::launch_f16_words(first, count, (uint16_t*)dst, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
 int tmh_event_create(uint64_t* event) {
     if (!event) return TMH_ERROR_INVALID_VALUE;
     int err;
@@ -710,7 +722,7 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     }
     std::lock_guard<std::mutex> guard(d->launch);
     if ((err = ensure_scratch(*d, scratch_need(rows, k))) != TMH_SUCCESS) return err;
-    tmh::Activations act = tmh::carve_scratch(d->scratch, rows, k);
+    tmh::Activations act = tmh::carve_scratch(d->act_scratch, rows, k);
     hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, (float*)act.scales, (float*)act.sums,
                                         (int32_t*)act.totals, (int8_t*)act.qs, d->stream);
     if (e == hipSuccess)

@@ -1,22 +1,28 @@
-"""Host-side weight quantisation for the HIP device, vectorised with numpy.
+"""Host-side weight quantisation for the HIP device.
 
 `Tensor#quantize` runs on the host even for a GPU device: it reads the values
 back, quantises them with `Quant.quantize` and uploads the blocks
-(src/tensomite/tensor/quantised.cr:11-19). This is that host step, whole
-matrices at a time: the bytes equal `Quant.quantize`'s (quant.cr:77-90,
-497-535) for every finite input, because every step is one IEEE f32
-operation in the reference's order:
+(src/tensomite/tensor/quantised.cr:11-19). `quantize` is that host step,
+done by the library's native quantiser (tmh_quantize_weights, over all host
+cores; quant.cr:77-90, 497-535):
 
   Q8_0  d = amax / 127; id = 1/d (0 when d is 0); q = round-half-away(x·id)
   Q4_0  m = the first value of largest magnitude; d = m / -8;
         q = min(15, trunc(x·id + 8.5))
   Q4_1  d = (max - min) / 15; q = min(15, trunc((x - min)·id + 0.5))
 
-and d (and min) are stored as F16, rounded to nearest even (numpy's f32 ->
-f16 conversion is IEEE's; a NaN is stored as 0x7e00 with its sign, as
-F16.new does, f16.cr:33-35).
+with d (and min) stored as F16, rounded to nearest even (F16.new, f16.cr:29-41).
+
+`synthetic_weights` and `synthetic_llama` make the BASELINE configs' weights,
+W ~ N(0, 0.02) quantised, deterministically from a seed: values come in
+fixed chunks, each from its own numpy generator seeded by (seed, chunk), so
+the bytes do not depend on how many threads make them.
 """
 from __future__ import annotations
+
+import ctypes
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -24,9 +30,18 @@ Q8_0, Q4_0, Q4_1 = 0, 1, 2
 KINDS = {"Q8_0": Q8_0, "Q4_0": Q4_0, "Q4_1": Q4_1}
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
 
+CHUNK_VALUES = 1 << 22  # values per generator chunk (a whole number of blocks)
+
 
 def _kind(kind) -> int:
     return KINDS[kind] if isinstance(kind, str) else int(kind)
+
+
+def _cores() -> int:
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return max(1, os.cpu_count() or 1)
 
 
 def f16_bits(values: np.ndarray) -> np.ndarray:
@@ -41,71 +56,70 @@ def f16_bits(values: np.ndarray) -> np.ndarray:
     return h
 
 
-def _round_away(v: np.ndarray) -> np.ndarray:
-    """round(:ties_away) for |v| < 2^31 (quant.cr:309-313): truncate, then step
-    away from zero when the dropped fraction is at least a half."""
-    whole = np.trunc(v)
-    fraction = v - whole
-    return whole + (fraction >= np.float32(0.5)) - (fraction <= np.float32(-0.5))
+def quantize(kind, values: np.ndarray, threads: int = 0) -> np.ndarray:
+    """Quant.quantize: f32 values, a whole number of blocks of 32, to block
+    bytes, by the library's host quantiser on `threads` threads (0: all)."""
+    import tensomite_hip as th
 
-
-def quantize(kind, values: np.ndarray) -> np.ndarray:
-    """Quant.quantize: f32 values, a whole number of blocks of 32, to block bytes."""
     k = _kind(kind)
+    if k not in BLOCK_BYTES:
+        raise th.DTypeError(f"kind {kind} is not a block format")
     v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
     if v.size % 32:
         raise ValueError(f"{v.size} values are not whole blocks of 32")
-    blocks = v.reshape(-1, 32)
-    nb = blocks.shape[0]
-    out = np.empty((nb, BLOCK_BYTES[k]), dtype=np.uint8)
-    f32 = np.float32
-    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
-        if k == Q8_0:
-            amax = np.abs(blocks).max(axis=1)
-            d = amax / f32(127.0)
-            idv = np.where(d == 0, f32(0.0), f32(1.0) / d).astype(np.float32)
-            q = _round_away(blocks * idv[:, None]).astype(np.int32).astype(np.int8)
-            out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
-            out[:, 2:] = q.view(np.uint8)
-        elif k == Q4_0:
-            first = np.argmax(np.abs(blocks), axis=1)  # first index of the largest magnitude
-            m = blocks[np.arange(nb), first]
-            d = m / f32(-8.0)
-            idv = np.where(d == 0, f32(0.0), f32(1.0) / d).astype(np.float32)
-            t = (blocks * idv[:, None]) + f32(8.5)
-            q = np.minimum(np.trunc(t).astype(np.int32).astype(np.int8), 15).astype(np.uint8)
-            out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
-            out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
-        elif k == Q4_1:
-            mn = blocks.min(axis=1)
-            mx = blocks.max(axis=1)
-            # Enumerable#min keeps the first of equal values: for a zero
-            # minimum, the sign is the first zero's.
-            zero = mn == 0
-            if zero.any():
-                rows = np.nonzero(zero)[0]
-                mn[rows] = blocks[rows, np.argmax(blocks[rows] == 0, axis=1)]
-            d = (mx - mn) / f32(15.0)
-            idv = np.where(d == 0, f32(0.0), f32(1.0) / d).astype(np.float32)
-            t = ((blocks - mn[:, None]) * idv[:, None]) + f32(0.5)
-            q = np.minimum(np.trunc(t).astype(np.int32).astype(np.int8), 15).astype(np.uint8)
-            out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
-            out[:, 2:4] = f16_bits(mn).view(np.uint8).reshape(nb, 2)
-            out[:, 4:] = q[:, :16] | (q[:, 16:] << 4)
-        else:
-            raise ValueError(f"kind {kind} is not a block format")
-    return out.reshape(-1)
+    out = np.empty(v.size // 32 * BLOCK_BYTES[k], dtype=np.uint8)
+    th.check("tmh_quantize_weights", th.library().tmh_quantize_weights(
+        k, v.ctypes.data_as(ctypes.c_void_p), v.size, out.ctypes.data_as(ctypes.c_void_p), int(threads)))
+    return out
 
 
-def synthetic_weights(kind, n: int, k: int, seed: int, std: float = 0.02, chunk_rows: int = 4096) -> np.ndarray:
-    """W[n, k] ~ N(0, std) in f32, quantised: the BASELINE configs' weights,
-    generated and quantised in row chunks to bound host memory."""
-    rng = np.random.default_rng(seed)
-    parts = []
-    for r0 in range(0, n, chunk_rows):
-        rows = min(chunk_rows, n - r0)
-        parts.append(quantize(kind, rng.normal(0.0, std, rows * k).astype(np.float32)))
-    return np.concatenate(parts)
+def synthetic_weights(kind, n: int, k: int, seed, std: float = 0.02) -> np.ndarray:
+    """W[n, k] ~ N(0, std) in f32, quantised: the BASELINE configs' weights.
+    Chunk c of CHUNK_VALUES values comes from default_rng([*seed, c]) as
+    standard normals in f32 times f32(std); chunks are made and quantised on
+    all host cores."""
+    kk = _kind(kind)
+    bb = BLOCK_BYTES[kk]
+    total = n * k
+    if total % 32:
+        raise ValueError(f"{n} x {k} values are not whole blocks of 32")
+    entropy = list(seed) if isinstance(seed, (list, tuple)) else [int(seed)]
+    out = np.empty(total // 32 * bb, dtype=np.uint8)
+    scale = np.float32(std)
+
+    def chunk(c):
+        lo = c * CHUNK_VALUES
+        hi = min(total, lo + CHUNK_VALUES)
+        v = np.random.default_rng(entropy + [c]).standard_normal(hi - lo, dtype=np.float32)
+        v *= scale
+        out[lo // 32 * bb:hi // 32 * bb] = quantize(kk, v, threads=1)
+
+    chunks = (total + CHUNK_VALUES - 1) // CHUNK_VALUES
+    with ThreadPoolExecutor(max_workers=min(_cores(), chunks)) as pool:
+        list(pool.map(chunk, range(chunks)))
+    return out
+
+
+def synthetic_llama(config: dict, seed: int, std: float = 0.02) -> dict:
+    """BASELINE config 5's weights at `config`'s shape: every matrix and the
+    embedding table (the tied head) W ~ N(0, std) quantised to config["kind"],
+    the RMSNorm weights 1 (Llama's initial norms), in the decoder's layout
+    (embed, head None, norm, per-layer attn_norm, ffn_norm, merged qkv, o,
+    merged gate_up, down). Matrix m of layer l comes from seed [seed, l, m]."""
+    c = config
+    fmt = c["kind"]
+    qn, kvn = c["heads"] * c["head_width"], c["kv_heads"] * c["head_width"]
+    ones = np.ones(c["width"], np.float32)
+    w = dict(embed=synthetic_weights(fmt, c["vocab"], c["width"], [seed, 1 << 20, 0], std), head=None,
+             norm=ones.copy(), attn_norm=[], ffn_norm=[], qkv=[], o=[], gate_up=[], down=[])
+    for layer in range(c["layers"]):
+        w["qkv"].append(synthetic_weights(fmt, qn + 2 * kvn, c["width"], [seed, layer, 0], std))
+        w["o"].append(synthetic_weights(fmt, c["width"], qn, [seed, layer, 1], std))
+        w["gate_up"].append(synthetic_weights(fmt, 2 * c["hidden"], c["width"], [seed, layer, 2], std))
+        w["down"].append(synthetic_weights(fmt, c["width"], c["hidden"], [seed, layer, 3], std))
+        w["attn_norm"].append(ones.copy())
+        w["ffn_norm"].append(ones.copy())
+    return w
 
 
 def random_blocks(fmt: str, n: int, k: int, rng, std: float = 0.02) -> np.ndarray:

@@ -152,6 +152,8 @@ SIGNATURES = {
     "tmh_block_matmul": (INT, [U32, U64, U64, U64, U32, U64, U64, U32, U32, U32, U32]),
     "tmh_block_matmul_quantised": (INT, [U32, U64, U64, U64, U64, U64, U64, U64, U64, U32, U32, U32, U32]),
     "tmh_gather_blocks": (INT, [U32, U64, U64, I32, U32, U64, U32, U64]),
+    "tmh_quantize_weights": (INT, [U32, VP, U64, VP, I32]),
+    "tmh_debug_f16_words": (INT, [U32, U32, U64]),
     "tmh_plan_create": (INT, [U32, ctypes.POINTER(Product), U32, ctypes.POINTER(U64)]),
     "tmh_plan_run": (INT, [U64]),
     "tmh_plan_destroy": (INT, [U64]),
@@ -549,6 +551,9 @@ class HIPDevice:
         ms = ctypes.c_float(0)
         check("tmh_event_elapsed_ms", self.lib.tmh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
         return ms.value
+
+    def destroy_event(self, event: int) -> None:
+        check("tmh_event_destroy", self.lib.tmh_event_destroy(event))
 
 
 class GGUFFile:

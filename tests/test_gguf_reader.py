@@ -56,3 +56,42 @@ def test_rows_not_whole_blocks_are_a_shape_error(tmp_path):
     write(path, [], [("w", "Q8_0", [2, 48], bytes(2 * 51))])
     with pytest.raises(th.ShapeError):
         th.GGUFFile(path)
+
+
+def _one_tensor_file(tmp_path, name, alignment=32, metadata=()):
+    path = str(tmp_path / name)
+    write(path, list(metadata), [("w", "Q8_0", [2, 64], bytes(2 * 68))], alignment=alignment)
+    return path
+
+
+def test_offsets_that_wrap_are_errors(tmp_path):
+    # A tensor offset near 2^64 that is a multiple of the alignment would
+    # wrap to an in-file address when added to the data start; it must be
+    # refused as a damaged file, never read (gguf.cr:320 refuses offsets
+    # past the file).
+    import struct
+    path = _one_tensor_file(tmp_path, "ok.gguf")
+    th.GGUFFile(path).close()
+    data = bytearray(open(path, "rb").read())
+    at = data.index(b"w", 24) + 1 + 4 + 2 * 8 + 4  # name, dims, shape, kind -> offset
+    assert struct.unpack_from("<Q", data, at)[0] == 0
+    for bad in (2 ** 64 - 32, 2 ** 64 - 4096, 2 ** 63, len(data)):
+        struct.pack_into("<Q", data, at, bad)
+        damaged = tmp_path / "wrapped.gguf"
+        damaged.write_bytes(bytes(data))
+        with pytest.raises(th.DeviceError):
+            th.GGUFFile(str(damaged))
+
+
+@pytest.mark.parametrize("alignment", [0, 3, 48, 1 << 21])
+def test_unreasonable_alignment_is_an_error(tmp_path, alignment):
+    path = _one_tensor_file(tmp_path, "align.gguf", metadata=[("general.alignment", alignment)])
+    with pytest.raises(th.DeviceError):
+        th.GGUFFile(path)
+
+
+def test_larger_power_of_two_alignment_reads(tmp_path):
+    path = _one_tensor_file(tmp_path, "align64.gguf", alignment=64, metadata=[("general.alignment", 64)])
+    f = th.GGUFFile(path)
+    assert f.entry("w") == ("Q8_0", [2, 64], 2 * 68)
+    f.close()

@@ -35,7 +35,7 @@ def bits(a):
 
 
 def weights(fmt, n, k, seed, scale=0.02):
-    values = np.random.default_rng(seed).normal(0.0, scale, n * k).astype(np.float32)
+    values = np.random.default_rng(seed).standard_normal(n * k, dtype=np.float32) * np.float32(scale)
     return oracle.quantize(fmt, values)
 
 
@@ -146,9 +146,12 @@ CONFIG_SHAPES = {
     "gate_up_135m": ("Q4_0", 3072, 576, 1),
     "down_135m": ("Q4_0", 576, 1536, 1),
     "head_135m": ("Q4_0", 49152, 576, 1),
-    # config 3: Q4_1 batched decode
+    # config 3: Q4_1 batched decode (one row: the quantise pass and the
+    # lanes product, as every one-row product over 4 MB of weights takes)
     "q41_up_b16": ("Q4_1", 8192, 2048, 16),
     "q41_down_b5": ("Q4_1", 2048, 8192, 5),
+    "q41_up_b1": ("Q4_1", 8192, 2048, 1),
+    "q41_down_b1": ("Q4_1", 2048, 8192, 1),
     # config 5: 1.7B Q4_0 products at batch 1 and 8
     "qkv_1p7b": ("Q4_0", 6144, 2048, 1),
     "gate_up_1p7b_b8": ("Q4_0", 16384, 2048, 8),
@@ -169,6 +172,22 @@ def test_config_shapes_bit_exact(dev, name):
     # run to run: the same bits again
     again = run_product(dev, fmt, wq, x, rows, n, k)
     assert np.array_equal(bits(again), bits(got))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("n,k", [(4096, 2048), (1024, 8192), (2500, 4096)])
+def test_one_row_over_4mb_with_bias(dev, fmt, n, k):
+    # One-row products of more than 4 MB of weights go through the quantise
+    # pass and the lanes product rather than the one-row kernel; with a bias
+    # added after each sum (host.cr:725-734), in every format.
+    say("one row > 4 MB", fmt, n, k)
+    wq = weights(fmt, n, k, n + k)
+    assert wq.nbytes > 4 << 20
+    x = acts(1, k, 5)
+    bias = acts(1, n, 6)
+    want = oracle.add_bias(oracle.matmul(fmt, x, wq, 1, n, k), bias)
+    got = run_product(dev, fmt, wq, x, 1, n, k, bias=bias)
+    assert np.array_equal(bits(got), bits(want))
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
@@ -258,6 +277,31 @@ def test_every_half_widens_exactly(dev):
     finite = ~np.isnan(want)
     assert np.array_equal(bits(got[finite]), bits(want[finite]))
     assert np.all(np.isnan(got[~finite]))
+
+
+def test_every_f32_rounds_to_half_exactly(dev):
+    # F16.new (f16.cr:29-41) on the device, for all 2^32 f32 words: the
+    # rounding the activation quantiser's scales and sums go through
+    # (round_to_half), swept by tmh_debug_f16_words in chunks of 2^28 and
+    # compared with the oracle's tmo_f16_bits on the same words.
+    from concurrent.futures import ThreadPoolExecutor
+
+    chunk = 1 << 28
+    out = dev.alloc(2 * chunk)
+    pool = ThreadPoolExecutor(4)
+    host = np.empty(chunk, np.uint16)
+    for c in range(1 << 32 >> 28):
+        first = c * chunk
+        say("f16 words", hex(first))
+        th.check("tmh_debug_f16_words", dev.lib.tmh_debug_f16_words(first, chunk, out.pointer))
+        dev.download(out, host)
+        words = np.arange(chunk, dtype=np.uint32) + np.uint32(first)
+        parts = np.array_split(words.view(np.float32), 4)
+        want = np.concatenate(list(pool.map(oracle.f16_bits_many, parts)))
+        bad = np.nonzero(host != want)[0]
+        assert bad.size == 0, (hex(first + int(bad[0])), hex(int(host[bad[0]])), hex(int(want[bad[0]])))
+    pool.shutdown()
+    out.release()
 
 
 def test_buffer_pool_reuse_and_counters(dev):
@@ -495,7 +539,8 @@ def test_plan_input_modes_need_the_streamed_kernel(dev, monkeypatch):
 
 MATRIX_SHAPES = [
     # (rows, n, k): config 4 prefill, ragged edges, short k, the 1.7B MLP
-    (512, 2048, 2048), (33, 100, 576), (64, 64, 64), (100, 130, 1024), (128, 8192, 2048), (40, 2048, 8192),
+    (512, 2048, 2048), (512, 8192, 2048), (33, 100, 576), (64, 64, 64), (100, 130, 1024), (128, 8192, 2048),
+    (40, 2048, 8192),
 ]
 
 
@@ -525,3 +570,24 @@ def test_matrix_cores_with_bias_and_slice(dev, fmt):
     say("matrix slice", fmt)
     got = run_product(dev, fmt, wq, x, rows, 40, k, mode="matrix", bias=bias, w_row=30)
     assert np.array_equal(bits(got), bits(want))
+
+
+def test_bench_config2_plan_bit_exact(dev):
+    # bench.py's timed launch exactly as it builds it (config 2: the 121
+    # products of a SmolLM2-135M token, the 49152 x 576 head included, packed
+    # at 256-byte offsets in one weight buffer, one k_matvec_stream plan),
+    # run twice: every product's bits equal the oracle's.
+    import bench
+
+    c2 = bench.build_config2(dev, copies=1)
+    plan = c2["plans"][0]
+    say("bench plan", plan.describe())
+    assert "stream" in plan.describe()
+    for _ in range(2):
+        plan.run()
+    dev.sync()
+    for i, (name, n, k) in enumerate(c2["prods"]):
+        got = dev.to_array(c2["ybufs"][i], np.float32, n)
+        want = oracle.matmul("Q4_0", c2["xs"][i], c2["weights"][i], 1, n, k)[0]
+        assert np.array_equal(bits(got), bits(want)), name
+    plan.destroy()

@@ -1,7 +1,9 @@
-"""The package's vectorised host quantiser (tensomite.cr_amd/quant_host.py)
-equals the oracle's Quant.quantize byte for byte: on the reference's fixture
-rows, on N(0, 0.02) matrices as the BASELINE configs use, and on edge
-values (signed zeros, ties, subnormal scales, constant blocks)."""
+"""The library's host quantiser (tmh_quantize_weights, through
+tensomite.cr_amd/quant_host.py; no GPU needed) equals the oracle's
+Quant.quantize byte for byte: on the reference's fixture rows, on N(0, 0.02)
+matrices as the BASELINE configs use, on edge values (signed zeros, ties,
+subnormal scales, constant blocks), whatever the thread count; and the
+synthetic weights do not depend on the thread count either."""
 import json
 import os
 
@@ -54,3 +56,31 @@ def test_f16_bits_match_oracle():
     assert np.array_equal(quant_host.f16_bits(values), oracle.f16_bits_many(values))
     nan = np.array([np.nan, -np.nan], dtype=np.float32)
     assert quant_host.f16_bits(nan).tolist() == [0x7E00, 0xFE00]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_threads_do_not_change_bytes(fmt):
+    v = np.random.default_rng(17).normal(0, 0.5, 32 * 70001).astype(np.float32)
+    want = oracle.quantize(fmt, v)
+    for threads in (1, 2, 3, 8, 0):
+        assert np.array_equal(quant_host.quantize(fmt, v, threads=threads), want), threads
+
+
+def test_synthetic_weights_are_chunked_by_seed_only(monkeypatch):
+    # chunk c of a matrix comes from default_rng([seed, c]), N(0,1) f32 times
+    # f32(0.02), quantised -- however many workers make them
+    n, k = 300, 32 * 1024  # 9.8M values: three chunks
+    got = quant_host.synthetic_weights("Q4_0", n, k, seed=[7, 1])
+    monkeypatch.setattr(quant_host, "_cores", lambda: 1)
+    assert np.array_equal(quant_host.synthetic_weights("Q4_0", n, k, seed=[7, 1]), got)
+    c = quant_host.CHUNK_VALUES
+    first = np.random.default_rng([7, 1, 1]).standard_normal(c, dtype=np.float32) * np.float32(0.02)
+    assert np.array_equal(got[c // 32 * 18:2 * c // 32 * 18], oracle.quantize("Q4_0", first))
+
+
+def test_quantiser_refuses_bad_input():
+    import tensomite_hip as th
+    with pytest.raises(th.DTypeError):
+        quant_host.quantize(3, np.zeros(32, np.float32))
+    with pytest.raises(ValueError):
+        quant_host.quantize("Q8_0", np.zeros(33, np.float32))
