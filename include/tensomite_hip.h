@@ -47,6 +47,14 @@ extern "C" {
                                         reported at tmh_sync (cuda.cr:967-983) */
 #define TMH_ERROR_NO_DEVICE 1006     /* no GPU, or a device index out of range */
 #define TMH_ERROR_BUSY 1007          /* the retired list is busy or full (buffer_pool.cr:101-111) */
+#define TMH_ERROR_NOT_READY 1008     /* tmh_block_matmul_fixed before tmh_init set the device up */
+#define TMH_ERROR_SCRATCH_LIMIT 1009 /* tmh_block_matmul_fixed: more than TMH_FIXED_SCRATCH_BYTES of
+                                        quantised activations */
+
+/* Bytes of quantised activations tmh_block_matmul_fixed can hold: per row,
+ * k int8 values and three 4-byte values per block of 32 (each of the four
+ * parts rounded up to 256 bytes over all rows), e.g. 512 rows of k = 2048. */
+#define TMH_FIXED_SCRATCH_BYTES (8u << 20)
 
 /* Block kinds, numbered as the reference's kernels number them (cuda.cr:774-781). */
 #define TMH_Q8_0 0 /* F16 d, 32 int8: x = q·d                      (34 bytes) */
@@ -226,6 +234,21 @@ int tmh_quantize_rows_q8(uint64_t x, uint32_t rows, uint32_t k, uint32_t ldx, ui
  * `mode` is a TMH_MODE_*. */
 int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
                      uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode);
+
+/* tmh_block_matmul without any allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, hosts that forbid it). Same arguments, kernels
+ * and bits as tmh_block_matmul, but the quantised activations live in a
+ * fixed per-GPU array of TMH_FIXED_SCRATCH_BYTES that the library holds
+ * until the process ends (one-row products the one-row kernel takes need
+ * none). tmh_init must have run first (it sets every device up):
+ * TMH_ERROR_NOT_READY otherwise; more than the array holds is
+ * TMH_ERROR_SCRATCH_LIMIT. Every call on a GPU shares its array and the
+ * library's one stream: calls are queued in order, but work captured from
+ * them into a graph and replayed later races with any other call of this
+ * entry point that overlaps it on that GPU. */
+int tmh_block_matmul_fixed(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
+                           uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode);
 
 /* The product of tmh_block_matmul from activations already quantised by
  * tmh_quantize_rows_q8 (its four outputs), for callers that share one

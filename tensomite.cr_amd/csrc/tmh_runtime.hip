@@ -72,6 +72,13 @@ Activations carve_scratch(uint8_t* base, uint32_t rows, uint32_t k) {
 
 }  // namespace tmh
 
+// Quantised activations of tmh_block_matmul_fixed: device memory that exists
+// from module load to process end, one copy per GPU, so that entry point
+// never allocates. Host code must not pass this name to a kernel (on the host
+// it is a stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress at set-up (Device::fixed_scratch).
+static __device__ __align__(256) uint8_t scratch[TMH_FIXED_SCRATCH_BYTES];
+
 namespace {
 
 using tmh::device_malloc;
@@ -218,6 +225,12 @@ struct Device {
     uint8_t* act_scratch = nullptr;
     size_t act_scratch_bytes = 0;
 
+    // This device's copy of the file-scope `scratch` array, looked up once at
+    // set-up (the allocation-free entry point's quantised activations), and
+    // the lock that keeps its quantise pass and product adjacent on the stream.
+    uint8_t* fixed_scratch = nullptr;
+    std::mutex fixed_launch;
+
     Pool pool;
     Retired* retired = nullptr;
     std::mutex staging_lock;
@@ -275,6 +288,7 @@ Device* current(int* err) {
             }
             if (e == hipSuccess) e = hipMalloc((void**)&d.errors, 3 * sizeof(int32_t));
             if (e == hipSuccess) e = hipMemset(d.errors, 0, 3 * sizeof(int32_t));
+            if (e == hipSuccess) e = hipGetSymbolAddress((void**)&d.fixed_scratch, HIP_SYMBOL(scratch));
             if (e != hipSuccess) {
                 *err = code(e);
                 return nullptr;
@@ -327,6 +341,8 @@ const char* library_name(int c) {
     case TMH_ERROR_EXECUTION: return "TMH_ERROR_EXECUTION";
     case TMH_ERROR_NO_DEVICE: return "TMH_ERROR_NO_DEVICE";
     case TMH_ERROR_BUSY: return "TMH_ERROR_BUSY";
+    case TMH_ERROR_NOT_READY: return "TMH_ERROR_NOT_READY";
+    case TMH_ERROR_SCRATCH_LIMIT: return "TMH_ERROR_SCRATCH_LIMIT";
     default: return nullptr;
     }
 }
@@ -342,6 +358,8 @@ const char* library_string(int c) {
     case TMH_ERROR_EXECUTION: return "a kernel found an index out of range";
     case TMH_ERROR_NO_DEVICE: return "no such GPU";
     case TMH_ERROR_BUSY: return "the retired list is busy or full";
+    case TMH_ERROR_NOT_READY: return "the device has not been set up: call tmh_init first";
+    case TMH_ERROR_SCRATCH_LIMIT: return "the product's quantised activations exceed the fixed scratch (8 MiB)";
     default: return nullptr;
     }
 }
@@ -375,7 +393,22 @@ extern "C" {
 
 int tmh_init(int32_t* count) {
     if (!count) return TMH_ERROR_INVALID_VALUE;
-    *count = count_devices();
+    const int n = count_devices();
+    // Sets every device up now (its stream, error buffer and the address of
+    // its fixed scratch), so no later call needs to; the calling thread keeps
+    // its device.
+    const int keep = t_device;
+    for (int i = 0; i < n; ++i) {
+        t_device = i;
+        int err;
+        if (!current(&err)) {
+            t_device = keep;
+            return err;
+        }
+    }
+    t_device = keep;
+    if (n > 0 && keep >= 0 && keep < n) (void)hipSetDevice(keep);
+    *count = n;
     return TMH_SUCCESS;
 }
 
@@ -728,6 +761,50 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     if (e == hipSuccess)
         e = tmh::launch_block_matmul(kind, mode, (const uint8_t*)(w + w_byte_offset), act, (float*)dst,
                                      (const float*)bias, rows, n, k, d->compute_units, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
+int tmh_block_matmul_fixed(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
+                           uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    const int n_devices = count_devices();
+    if (n_devices == 0 || t_device < 0 || t_device >= n_devices) return TMH_ERROR_NO_DEVICE;
+    Device* d = &g_devices[t_device];
+    // Set-up allocates (a stream, the error buffer): it must have happened
+    // in tmh_init or an earlier call, not here.
+    if (!d->ready || !d->fixed_scratch) return TMH_ERROR_NOT_READY;
+    int now = -1;
+    if (hipGetDevice(&now) != hipSuccess || now != t_device) {
+        hipError_t e = hipSetDevice(t_device);
+        if (e != hipSuccess) return code(e);
+    }
+    int err;
+    if ((err = check_product(kind, rows, n, k, mode)) != TMH_SUCCESS) return err;
+    if (ldx < k) return TMH_ERROR_SHAPE;
+    if (rows == 0 || n == 0) return TMH_SUCCESS;
+    if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
+    const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
+    // The same choice of kernels as tmh_block_matmul: a one-row product that
+    // the one-row kernel takes needs no scratch at all.
+    constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
+    if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
+        tmh::row_kernel_fits(mode, wrow, k)) {
+        hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
+                                       d->compute_units, d->stream);
+        if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+        return code(e);
+    }
+    if (scratch_need(rows, k) > TMH_FIXED_SCRATCH_BYTES) return TMH_ERROR_SCRATCH_LIMIT;
+    // Calls share this device's array; the lock keeps each call's quantise
+    // pass and product adjacent on the one stream, so they run in order.
+    std::lock_guard<std::mutex> guard(d->fixed_launch);
+    tmh::Activations act = tmh::carve_scratch(d->fixed_scratch, rows, k);
+    hipError_t e = tmh::launch_quantize((const float*)x, ldx, rows, k, (float*)act.scales, (float*)act.sums,
+                                        (int32_t*)act.totals, (int8_t*)act.qs, d->stream);
+    if (e == hipSuccess)
+        e = tmh::launch_block_matmul(kind, mode, wrow, act, (float*)dst, (const float*)bias, rows, n, k,
+                                     d->compute_units, d->stream);
     if (e == hipSuccess) d->gpu_ops.fetch_add(1);
     return code(e);
 }

@@ -40,6 +40,8 @@ ERROR_NO_KERNELS = 1003
 ERROR_OUT_OF_MEMORY = 1004
 ERROR_EXECUTION = 1005
 ERROR_NO_DEVICE = 1006
+ERROR_NOT_READY = 1008
+ERROR_SCRATCH_LIMIT = 1009
 
 
 class Error(Exception):
@@ -151,6 +153,7 @@ SIGNATURES = {
     "tmh_quantize_rows_q8": (INT, [U64, U32, U32, U32, U64, U64, U64, U64]),
     "tmh_block_matmul": (INT, [U32, U64, U64, U64, U32, U64, U64, U32, U32, U32, U32]),
     "tmh_block_matmul_quantised": (INT, [U32, U64, U64, U64, U64, U64, U64, U64, U64, U32, U32, U32, U32]),
+    "tmh_block_matmul_fixed": (INT, [U32, U64, U64, U64, U32, U64, U64, U32, U32, U32, U32]),
     "tmh_gather_blocks": (INT, [U32, U64, U64, I32, U32, U64, U32, U64]),
     "tmh_quantize_weights": (INT, [U32, VP, U64, VP, I32]),
     "tmh_debug_f16_words": (INT, [U32, U32, U64]),
