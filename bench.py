@@ -12,8 +12,8 @@ weights (>= 512 MB) that the 256 MB Infinity Cache cannot serve them.
 
 value = algorithmic bytes per step (weights + f32 x + f32 y) / wall time
 per step, in GB/s. The roofline object prices the launch against 8 TB/s
-from the median of at least 100 per-launch HIP event times (an event after
-every launch on the library's stream). The CPU baseline times the oracle's
+from the median per-launch time over at least 100 groups of 20 back-to-back
+launches (HIP events between groups on the library's stream). The CPU baseline times the oracle's
 restatement of tensomite's CPU path (Quant.matmul on every host core, in its
 portable and native builds) on the same bytes, and checks the GPU's output
 bits against it.
@@ -52,7 +52,8 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
-ROOFLINE_LAUNCHES = 100
+ROOFLINE_GROUPS = 100  # per-launch figures: the median over this many groups of launches
+GROUP = 20             # launches a group
 
 # config 2: (name, n, k) per layer, then the head
 LAYER = [("qkv", 960, 576), ("o", 576, 576), ("gate_up", 3072, 576), ("down", 576, 1536)]
@@ -118,20 +119,24 @@ def traffic_from_profiles(name):
         return None
 
 
-def time_launches(dev, launch, count):
+def time_launches(dev, launch, count, group=1):
     """Runs launch(i) for i < count, back to back on the library's stream,
-    with a HIP event after each: the per-launch times in ms and the wall time
-    of the whole (host clock, from the first enqueue to the end of the GPU's
-    work)."""
-    events = [dev.event() for _ in range(count + 1)]
+    with a HIP event after every `group` launches: the mean launch time of
+    each group in ms, and the wall time of the whole (host clock, from the
+    first enqueue to the end of the GPU's work). An event between every two
+    launches costs ~2.5 us of its own on MI355X (config 2: 18.0 us a launch
+    against 15.5 back to back), so groups of 20 keep that under 1%."""
+    groups = count // group
+    events = [dev.event() for _ in range(groups + 1)]
     t0 = time.perf_counter()
     dev.record(events[0])
-    for i in range(count):
-        launch(i)
-        dev.record(events[i + 1])
+    for g in range(groups):
+        for j in range(group):
+            launch(g * group + j)
+        dev.record(events[g + 1])
     dev.sync()
     wall = time.perf_counter() - t0
-    per = [dev.elapsed_ms(events[i], events[i + 1]) for i in range(count)]
+    per = [dev.elapsed_ms(events[g], events[g + 1]) / group for g in range(groups)]
     for ev in events:
         dev.destroy_event(ev)
     return per, wall
@@ -153,10 +158,11 @@ def warm_up(dev, launch, count, seconds=0.05):
     return done
 
 
-def launch_stats(per_ms, algorithmic_bytes):
+def launch_stats(per_ms, algorithmic_bytes, group=1):
     med = statistics.median(per_ms)
     mean = sum(per_ms) / len(per_ms)
-    return {"launches": len(per_ms), "median_us": round(med * 1e3, 3), "mean_us": round(mean * 1e3, 3),
+    return {"launches": len(per_ms) * group, "groups": len(per_ms), "launches_per_group": group,
+            "median_us": round(med * 1e3, 3), "mean_us": round(mean * 1e3, 3),
             "min_us": round(min(per_ms) * 1e3, 3), "max_us": round(max(per_ms) * 1e3, 3),
             "GB_per_s_median": round(algorithmic_bytes / (med * 1e-3) / 1e9, 1)}
 
@@ -276,15 +282,17 @@ def config2(dev, args):
 
     run = lambda i: plans[i % copies].run()
     warm = warm_up(dev, run, args.warmup)
-    # The timed region: K launches back to back, an event after each.
-    per, wall = time_launches(dev, run, args.steps)
+    # The timed region: K launches back to back, an event every GROUP.
+    group = GROUP if args.steps >= GROUP else 1
+    per, wall = time_launches(dev, run, args.steps, group)
     ms_per_step = wall * 1e3 / args.steps
     value = algorithmic / (ms_per_step * 1e-3) / 1e9
-    # The roofline: the median of at least ROOFLINE_LAUNCHES per-launch times.
-    if len(per) < ROOFLINE_LAUNCHES:
-        more, _ = time_launches(dev, lambda i: run(args.steps + i), ROOFLINE_LAUNCHES - len(per))
-        per = per + more
-    stats = launch_stats(per, algorithmic)
+    # The roofline: the median over at least ROOFLINE_GROUPS groups of
+    # GROUP back-to-back launches (per-launch time = the group's / GROUP).
+    if len(per) < ROOFLINE_GROUPS:
+        group = GROUP
+        per, _ = time_launches(dev, run, ROOFLINE_GROUPS * GROUP, GROUP)
+    stats = launch_stats(per, algorithmic, group)
     achieved = stats["GB_per_s_median"]
     gpu_out = [dev.to_array(y, np.float32, n) for y, (_, n, _) in zip(ybufs, prods)]
 
@@ -341,6 +349,8 @@ def config2(dev, args):
             "launch_us_min": stats["min_us"],
             "launch_us_max": stats["max_us"],
             "launches": stats["launches"],
+            "groups": stats["groups"],
+            "launches_per_group": stats["launches_per_group"],
             "warmup_launches": warm,
         },
         "per_product_launches": {
@@ -402,17 +412,16 @@ def config1(dev, args, batch=128, min_copies=1024):
         th.check("tmh_block_matmul", dev.lib.tmh_block_matmul(th.Q8_0, views[i % copies].pointer, 0, x.pointer, k,
                                                                y.pointer, 0, 1, n, k, 0))
     warm_up(dev, single, args.warmup)
-    launches = max(ROOFLINE_LAUNCHES, args.steps)
-    per, wall = time_launches(dev, single, launches)
-    s_stats = launch_stats(per, algorithmic)
+    per, wall = time_launches(dev, single, ROOFLINE_GROUPS * GROUP, GROUP)
+    s_stats = launch_stats(per, algorithmic, GROUP)
     gpu_y = dev.to_array(y, np.float32, n)
 
     plans = [dev.plan("Q8_0", [(views[p * batch + j], 0, x, ys[j], None, n, k) for j in range(batch)])
              for p in range(copies // batch)]
     run = lambda i: plans[i % len(plans)].run()
     warm_up(dev, run, args.warmup)
-    per_b, _ = time_launches(dev, run, max(ROOFLINE_LAUNCHES, args.steps))
-    b_stats = launch_stats(per_b, algorithmic * batch)
+    per_b, _ = time_launches(dev, run, ROOFLINE_GROUPS * 4, 4)
+    b_stats = launch_stats(per_b, algorithmic * batch, 4)
     batched_y = dev.to_array(ys[batch - 1], np.float32, n)
     out = {
         "workload": "config 1: GPT-2-small c_attn, Q8_0 W [2304, 768] x f32 [768] -> [2304]",
@@ -488,21 +497,24 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
             t = time.perf_counter()
             model.forward(prompts[r], row=r, last_only=True)
             prefill.append(time.perf_counter() - t)
-        tokens = model.generate(steps, graph=graph)  # graph captured, state on the device
+        tokens = model.generate(steps, graph=graph)  # the graph is captured on first use
         if rows == 1:
             gpu_tokens = [int(t) for t in tokens[0]]
-        for _ in range(4):
-            model.step(graph=graph)
-        dev.sync()
+        # The timed run: the same prompts again, then the `steps` greedy
+        # tokens (steps - 1 decode forwards at positions 128..126 + steps,
+        # each one graph launch), HIP events around the generate call.
+        model.reset()
+        for r in range(rows):
+            model.forward(prompts[r], row=r, last_only=True)
         e0, e1 = dev.event(), dev.event()
         dev.record(e0)
-        for _ in range(steps):
-            model.step(graph=graph)
+        again = model.generate(steps, graph=graph)
         dev.record(e1)
         dev.sync()
-        ms = dev.elapsed_ms(e0, e1) / steps
+        ms = dev.elapsed_ms(e0, e1) / (steps - 1)
         out[f"batch{rows}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(rows * 1e3 / ms, 1), "graph": graph,
-                               "steps": steps, "positions": f"{128 + steps + 3}..{128 + 2 * steps + 2}",
+                               "steps": steps, "positions": f"128..{126 + steps}",
+                               "repeat_tokens_equal": bool(np.array_equal(again, tokens)),
                                "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
                                "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
         model.destroy()
@@ -539,7 +551,7 @@ def batched_config3(dev, steps, warmup):
     against B = 1, 2, 4, 8, 16 activation rows. One call is tmh_block_matmul
     over f32 x (the activation quantiser, then the lanes product); calls
     rotate through enough weight copies (>= 512 MB) that the 256 MB Infinity
-    Cache cannot serve them; per-call HIP events, the median of >= 100.
+    Cache cannot serve them; HIP events every 10 calls, the median over 100 groups.
     Bytes a call: weights + 4·B·K of x + 4·B·N of y."""
     import quant_host
     out = {"metric": "Q4_1 batched-decode product GB/s (config 3)", "unit": "GB/s", "n_gpus": 1, "steps": steps,
@@ -558,9 +570,9 @@ def batched_config3(dev, steps, warmup):
             dst = dev.alloc(4 * b * n)
             call = lambda i: dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
             warm_up(dev, call, warmup)
-            per, _ = time_launches(dev, call, max(ROOFLINE_LAUNCHES, steps))
+            per, _ = time_launches(dev, call, ROOFLINE_GROUPS * 10, 10)
             nbytes = host.nbytes + 4 * b * k + 4 * b * n
-            st = launch_stats(per, nbytes)
+            st = launch_stats(per, nbytes, 10)
             out["shapes"][f"{n}x{k} B={b}"] = {"us_per_call_median": st["median_us"], "us_per_call_mean": st["mean_us"],
                                                "GB_per_s": st["GB_per_s_median"],
                                                "hbm_peak_frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 3)}
@@ -578,8 +590,8 @@ def gemm_config4(dev, steps, warmup, mode="auto"):
     """Config 4: the Q8_0 prefill GEMM at the Llama-1.7B shape, 512 tokens x
     K = 2048 against N = 2048 (attention projections) and N = 8192 (MLP
     up/gate). One call is tmh_block_matmul over f32 x (the activation
-    quantiser, then the matrix-core kernel, k_matmul_mfma); per-call HIP
-    events, the median of >= 100. int8 work: 2 · 512 · 2048 · N ops a call.
+    quantiser, then the matrix-core kernel, k_matmul_mfma); HIP events every
+    4 calls, the median over 100 groups. int8 work: 2 · 512 · 2048 · N ops a call.
     mode "unordered" runs the measurement kernel that sums the raw MFMA
     results without the block-ordered epilogue."""
     import quant_host
@@ -595,7 +607,7 @@ def gemm_config4(dev, steps, warmup, mode="auto"):
         dst = dev.alloc(4 * rows * n)
         call = lambda i: dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst, mode=mode)
         warm_up(dev, call, warmup)
-        per, _ = time_launches(dev, call, max(ROOFLINE_LAUNCHES, steps))
+        per, _ = time_launches(dev, call, ROOFLINE_GROUPS * 4, 4)
         med = statistics.median(per)
         ops = 2.0 * rows * k * n
         tops = ops / (med * 1e-3) / 1e12
