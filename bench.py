@@ -31,6 +31,7 @@ Beside it, in the same line:
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-decode]
     python bench.py --batched     # config 3, its own line
     python bench.py --gemm        # config 4, its own line
+    python bench.py --write-gguf DIR   # the configs' weights as GGUF files
 """
 from __future__ import annotations
 
@@ -648,7 +649,15 @@ def main():
     ap.add_argument("--gemm-mode", default="auto", help="config 4's BlockMatMulMode (auto, matrix, unordered)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
+    ap.add_argument("--write-gguf", metavar="DIR",
+                    help="write the configs' weights as GGUF files (the bytes measured here, for the reference's own "
+                         "timing where Crystal exists) into DIR, then exit; needs no GPU")
     args = ap.parse_args()
+    if args.write_gguf:
+        import gguf_export
+        for path in gguf_export.export_configs(args.write_gguf):
+            log(f"wrote {path} ({os.path.getsize(path)} bytes)")
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path runs on one GPU's share only (asked for --gpus {args.gpus}); "
               "a product shards by output rows across GPUs, each GPU running this kernel on its share",

@@ -132,51 +132,7 @@ from quant_host import random_block_llama, random_blocks  # noqa: E402,F401
 
 def write_llama_gguf(path: str, config: dict, weights: dict, norm_kind: str = "F32") -> None:
     """Writes `weights` (the decoder's layout, q/k in Hugging Face order) as a
-    llama.cpp GGUF: q/k rows permuted to llama.cpp's rotary pairing (the
-    inverse of Llama.unpermute), projections split, norms as F32, F16 or BF16."""
-    from gguf_io import write
+    llama.cpp GGUF, by the package's exporter (gguf_export.write_llama)."""
+    import gguf_export
 
-    c = config
-    fmt = c["kind"]
-    rb = c["width"] // 32 * BLOCK_BYTES[fmt]
-    qn, kvn = c["heads"] * c["head_width"], c["kv_heads"] * c["head_width"]
-
-    def permuted(data, heads):
-        rows = data.reshape(-1, rb)
-        out = np.empty_like(rows)
-        out[unpermute_order(rows.shape[0], heads)] = rows
-        return out.reshape(-1)
-
-    def norm(v):
-        v = np.asarray(v, np.float32)
-        if norm_kind == "F16":
-            return v.astype(np.float16).view(np.uint8)
-        if norm_kind == "BF16":
-            return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
-        return v.view(np.uint8)
-
-    meta = [("general.architecture", "llama"), ("llama.block_count", c["layers"]),
-            ("llama.embedding_length", c["width"]), ("llama.attention.head_count", c["heads"]),
-            ("llama.attention.head_count_kv", c["kv_heads"]), ("llama.feed_forward_length", c["hidden"]),
-            ("llama.context_length", c["context"]), ("llama.attention.layer_norm_rms_epsilon", float(c["eps"])),
-            ("llama.rope.freq_base", float(c["theta"]))]
-    W, H = c["width"], c["hidden"]
-    tensors = [("token_embd.weight", fmt, [c["vocab"], W], weights["embed"]),
-               ("output_norm.weight", norm_kind, [W], norm(weights["norm"]))]
-    if weights.get("head") is not None:
-        tensors.append(("output.weight", fmt, [c["vocab"], W], weights["head"]))
-    for l in range(c["layers"]):
-        b = f"blk.{l}."
-        qkv = weights["qkv"][l]
-        q, k, v = qkv[:qn * rb], qkv[qn * rb:(qn + kvn) * rb], qkv[(qn + kvn) * rb:]
-        gu = weights["gate_up"][l]
-        tensors += [(b + "attn_norm.weight", norm_kind, [W], norm(weights["attn_norm"][l])),
-                    (b + "attn_q.weight", fmt, [qn, W], permuted(q, c["heads"])),
-                    (b + "attn_k.weight", fmt, [kvn, W], permuted(k, c["kv_heads"])),
-                    (b + "attn_v.weight", fmt, [kvn, W], v),
-                    (b + "attn_output.weight", fmt, [W, qn], weights["o"][l]),
-                    (b + "ffn_norm.weight", norm_kind, [W], norm(weights["ffn_norm"][l])),
-                    (b + "ffn_gate.weight", fmt, [H, W], gu[:len(gu) // 2]),
-                    (b + "ffn_up.weight", fmt, [H, W], gu[len(gu) // 2:]),
-                    (b + "ffn_down.weight", fmt, [W, H], weights["down"][l])]
-    write(path, meta, tensors)
+    gguf_export.write_llama(path, config, weights, norm_kind)

@@ -95,3 +95,40 @@ def test_larger_power_of_two_alignment_reads(tmp_path):
     f = th.GGUFFile(path)
     assert f.entry("w") == ("Q8_0", [2, 64], 2 * 68)
     f.close()
+
+
+def test_exported_llama_reads_back_in_hugging_face_order(tmp_path):
+    # gguf_export.write_llama stores q/k rows in llama.cpp's rotary pairing;
+    # taking them back in Llama.unpermute's order (llama.cr:226-235) gives the
+    # decoder's rows, and every other tensor is stored as given.
+    import gguf_export
+    from llama_fixtures import random_llama, take_rows, unpermute_order
+    config = dict(layers=2, width=128, heads=4, kv_heads=2, head_width=32, hidden=256, vocab=300, context=64,
+                  eps=1e-5, theta=10000.0, kind="Q4_0")
+    w = random_llama(config, seed=3, norm_jitter=0.1)
+    path = str(tmp_path / "llama.gguf")
+    gguf_export.write_llama(path, config, w)
+    g = GGUF(path)
+    rb = 128 // 32 * 18
+    assert g.metadata["llama.block_count"] == 2 and g.metadata["llama.attention.head_count_kv"] == 2
+    assert np.array_equal(g.raw("token_embd.weight"), w["embed"])
+    for l in range(2):
+        q = take_rows(g.raw(f"blk.{l}.attn_q.weight"), rb, unpermute_order(128, 4))
+        k = take_rows(g.raw(f"blk.{l}.attn_k.weight"), rb, unpermute_order(64, 2))
+        v = g.raw(f"blk.{l}.attn_v.weight")
+        assert np.array_equal(np.concatenate([q, k, v]), w["qkv"][l])
+        gu = np.concatenate([g.raw(f"blk.{l}.ffn_gate.weight"), g.raw(f"blk.{l}.ffn_up.weight")])
+        assert np.array_equal(gu, w["gate_up"][l])
+        assert np.array_equal(g.f32(f"blk.{l}.ffn_norm.weight"), w["ffn_norm"][l])
+    lib = th.GGUFFile(path)
+    assert lib.entry("blk.1.attn_q.weight") == ("Q4_0", [128, 128], 128 * rb)
+    lib.close()
+
+
+def test_exported_config1_is_bench_bytes(tmp_path):
+    import gguf_export
+    import quant_host
+    [path] = gguf_export.export_configs(str(tmp_path), configs=(1,))
+    g = GGUF(path)
+    assert g.entries["c_attn.weight"][:2] == ("Q8_0", [2304, 768])
+    assert np.array_equal(g.raw("c_attn.weight"), quant_host.synthetic_weights("Q8_0", 2304, 768, seed=0x5EED0001))

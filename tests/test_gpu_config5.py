@@ -16,7 +16,6 @@ import json
 import os
 import sys
 
-import numpy as np
 import pytest
 
 import tensomite_hip as th
@@ -105,3 +104,20 @@ def test_fixture_row_equals_live_oracle(model_weights, expected):
         tokens.append(oracle.argmax(logits))
         logits = cpu.forward([tokens[-1]], last_only=True)[0]
     assert tokens == expected["rows"][7]["tokens"][:24]
+
+
+def test_exported_gguf_loads_to_the_same_tokens(dev, model_weights, expected, tmp_path):
+    # The config-5 weights written as a llama.cpp GGUF (what bench.py
+    # --write-gguf gives the reference), loaded back by Llama.load's path
+    # (tmh_llama_load_gguf: q/k unpermuted and projections merged while
+    # staging): prompt 0's tokens equal the CPU's.
+    import gguf_export
+    say("config 5 through GGUF")
+    path = str(tmp_path / "config5.gguf")
+    gguf_export.write_llama(path, fixture.config(), model_weights)
+    model = th.HIPLlama.load_gguf(dev, path, rows=1, capacity=2048, max_tokens=128)
+    assert model.config["layers"] == 24 and model.config["kind"] == "Q4_0"
+    logits = model.forward(expected["prompts"][0], last_only=True)[0]
+    assert fixture.logits_summary(logits) == expected["rows"][0]["prefill_logits"]
+    assert list(model.generate(256)[0]) == expected["rows"][0]["tokens"]
+    model.destroy()
