@@ -162,6 +162,26 @@ hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations 
 hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations act, uint32_t rows, uint32_t H,
                                  uint32_t k, Activations glu, hipStream_t stream);
 
+// One-row products over an f32 row x that each workgroup first takes through
+// RMSNorm (weights `norm`, eps) and the activation quantiser, with the bits
+// of the norm+quantise launch then the lanes product: dst[n]; and gate_up
+// with SwiGLU and the quantiser in its epilogue, as launch_gate_up_swiglu.
+// hipErrorInvalidValue when the shape is not for them (rows other than 1, k
+// above 2048, rows of an odd number of blocks, x or norm not 16-byte aligned).
+bool rms_product_fits(const uint8_t* w, uint32_t k, const float* x, uint32_t ldx, const float* norm);
+hipError_t launch_product_rms(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, const float* norm,
+                              float eps, float* dst, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                              hipStream_t stream);
+hipError_t launch_gate_up_swiglu_rms(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, const float* norm,
+                                     float eps, uint32_t rows, uint32_t H, uint32_t k, Activations glu,
+                                     hipStream_t stream);
+
+// One quantised activation row times w (n rows), dst[row] = Σ (+ bias[row]):
+// the weights of each workgroup's tile direct-loaded into LDS at its start.
+// hipErrorInvalidValue when the shape is not for it.
+hipError_t launch_product_one(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* bias,
+                              uint32_t n, uint32_t k, int compute_units, hipStream_t stream);
+
 // dst[i] = the F16 bits of the float with word first + i, i < count.
 hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream);
 

@@ -394,6 +394,278 @@ __global__ __launch_bounds__(256) void k_matvec_glu(const uint8_t* __restrict__ 
 }
 
 
+// ------------------------------------------------- one row, weights in LDS
+
+// Threads of a k_matvec_one workgroup: 8 waves, two a SIMD, so one wave's
+// waits overlap another's work.
+constexpr uint32_t ONE_THREADS = 512;
+constexpr uint32_t ONE_WAVES = ONE_THREADS / 64u;
+
+// Direct loads of `bytes` contiguous bytes at src into LDS at `to` (a byte
+// address), 1 KB a load, load i by the wave first + (i % waves); lanes past
+// the end read the last 16 bytes again (the LDS region holds whole
+// kilobytes). `bytes` a multiple of 16. Returns this wave's loads (0 for a
+// wave outside [first, first + waves)).
+// NT: the bytes are read once (weights), so they should not displace what
+// other workgroups read again from the caches (the activation row).
+template <bool NT>
+__device__ __forceinline__ uint32_t stage_bytes(const uint8_t* src, uint32_t bytes, uint32_t to, uint32_t wave,
+                                                uint32_t first, uint32_t waves) {
+    if (wave < first || wave >= first + waves) return 0;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uintptr_t base = (uintptr_t)src, last = base + bytes - 16u;
+    const uint32_t loads = (bytes + 1023u) >> 10;
+    uint32_t mine = 0;
+    for (uint32_t i = wave - first; i < loads; i += waves, ++mine) {
+        const uintptr_t at = base + (uintptr_t)i * 1024u + lane * 16u;
+        if constexpr (NT) lds_load16_nt((const void*)(at < last ? at : last), to + i * 1024u);
+        else lds_load16((const void*)(at < last ? at : last), to + i * 1024u);
+    }
+    return mine;
+}
+
+// Direct loads of `count` 4-byte values at src into LDS at `to`, 256 bytes
+// a load, by wave `by` only; returns this wave's loads.
+__device__ __forceinline__ uint32_t stage_words(const void* src, uint32_t count, uint32_t to, uint32_t wave,
+                                                uint32_t by) {
+    if (wave != by) return 0;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t mine = 0;
+    for (uint32_t c0 = 0; c0 < count; c0 += 64u, ++mine)
+        lds_load4((const uint32_t*)src + min(c0 + lane, count - 1u), to + c0 * 4u);
+    return mine;
+}
+
+// LDS layout of k_matvec_one, in bytes from the start of its dynamic LDS.
+struct OneLds {
+    uint32_t x, nw, qs, scales, sums, totals, w, w2, part, outs, end;
+};
+
+__host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_bytes, uint32_t stride, bool norm,
+                                          bool glu) {
+    const uint32_t nb = k >> 5;
+    auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
+    OneLds l;
+    l.x = 0;
+    l.nw = norm ? kb(4u * k) : 0u;
+    l.qs = norm ? 2u * kb(4u * k) : 0u;
+    l.scales = l.qs + kb(k);
+    l.sums = l.scales + ((4u * nb + 255u) & ~255u);
+    l.totals = l.sums + ((4u * nb + 255u) & ~255u);
+    l.w = l.totals + kb(4u * nb);
+    const uint32_t wbytes = glu ? (tr / 2u) * row_bytes : tr * row_bytes;
+    l.w2 = l.w + kb(wbytes);
+    l.part = glu ? l.w2 + kb(wbytes) : l.w2;
+    l.outs = l.part + 4u * tr * stride;
+    l.end = l.outs + (glu ? 4u * (tr + tr / 2u) : 0u);
+    return l;
+}
+
+// One activation row times a tile of `tr` weight rows per workgroup, the
+// tile's weight bytes (contiguous rows; GLU: its gate rows and its up rows)
+// brought into LDS by direct loads that waves 1..7 issue at the start,
+// while wave 0 loads the activations alone, so its wait for them never
+// waits for weights:
+//   NORM: x is the f32 row, taken through Op::RMSNorm (host.cr:374-386;
+//     weights nw, eps) and the activation quantiser -- the squares' sum in
+//     index order by speculation across wave 0, root = sqrtf(Σ/k + eps),
+//     v = x / root · nw, quantize_quad: the bits of k_rmsnorm_quantise_wave
+//     -- while the weights are in flight;
+//   else the row arrives quantised (act, as the quantise pass lays it out).
+// Then matvec_tile's per-pair contributions and ordered fold, from LDS:
+// dst[row] = Σ (+ bias[row], one rounding), or, GLU, SwiGLU and the
+// quantiser on the tile's gate/up outputs into glu. k a multiple of 64 with
+// ONE_THREADS % (k / 64) == 0 (whole rows of pairs per pass), rows whole
+// 16-byte pieces starting 16-byte aligned.
+template <int KIND, bool NORM, bool GLU>
+__global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ nw, float eps, Activations act,
+                                                            float* __restrict__ dst, const float* __restrict__ bias,
+                                                            uint32_t n, uint32_t k, uint32_t tr, uint32_t stride,
+                                                            Activations glu) {
+    extern __shared__ float4 lds4[];
+    uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
+    __shared__ float root_slot;
+    constexpr uint32_t PW = Fmt<KIND>::PW, BB = Fmt<KIND>::BB;
+    const uint32_t t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nb = k >> 5, np = nb >> 1, row_bytes = nb * BB;
+    const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
+    const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
+    const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU);
+    const uint32_t lbase = lds_address(base);
+
+    // Wave 0: the activations, issued before any weight load (the compute
+    // unit's loads queue in order, so the weights would delay them). Waves
+    // 1..7: the weights.
+    if constexpr (NORM) {
+        stage_bytes<false>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u, 1u);
+        stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, 0u, 1u);
+    } else {
+        stage_bytes<false>(reinterpret_cast<const uint8_t*>(act.qs), k, lbase + L.qs, wave, 0u, 1u);
+        stage_words(act.scales, nb, lbase + L.scales, wave, 0u);
+        if constexpr (KIND == 2) stage_words(act.sums, nb, lbase + L.sums, wave, 0u);
+        if constexpr (KIND == 1) stage_words(act.totals, nb, lbase + L.totals, wave, 0u);
+    }
+    lds_sync();
+    if constexpr (GLU) {
+        stage_bytes<true>(w + (size_t)g0 * row_bytes, h * row_bytes, lbase + L.w, wave, 1u, ONE_WAVES - 1u);
+        stage_bytes<true>(w + (size_t)(H + g0) * row_bytes, h * row_bytes, lbase + L.w2, wave, 1u, ONE_WAVES - 1u);
+    } else {
+        stage_bytes<true>(w + (size_t)row0 * row_bytes, rows * row_bytes, lbase + L.w, wave, 1u, ONE_WAVES - 1u);
+    }
+
+    int8_t* aq = reinterpret_cast<int8_t*>(base + L.qs);
+    float* asc = reinterpret_cast<float*>(base + L.scales);
+    float* asm_ = reinterpret_cast<float*>(base + L.sums);
+    int32_t* atot = reinterpret_cast<int32_t*>(base + L.totals);
+    if (wave == 0) {
+        wait_vm_lds<0>();  // wave 0 issued only the activations
+        if constexpr (NORM) {
+            const float* xs = reinterpret_cast<const float*>(base + L.x);
+            float sq[32];
+#pragma unroll
+            for (uint32_t i = 0; i < 32u; i += 4u) {
+                const uint32_t c = t * 32u + i;
+                const float4 v = c < k ? *reinterpret_cast<const float4*>(xs + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                sq[i] = v.x * v.x;
+                sq[i + 1] = v.y * v.y;
+                sq[i + 2] = v.z * v.z;
+                sq[i + 3] = v.w * v.w;
+            }
+            const float total = ordered_sum_wave<32>(sq);
+            if (t == 0) root_slot = __builtin_sqrtf(total / (float)k + eps);
+        }
+    }
+    lds_sync();  // the activations (and the root) are in
+    if constexpr (NORM) {
+        const float* xs = reinterpret_cast<const float*>(base + L.x);
+        const float* ws = reinterpret_cast<const float*>(base + L.nw);
+        const float root = root_slot;
+        for (uint32_t blk = t >> 3; blk < nb; blk += ONE_THREADS / 8u) {  // uniform across each 8-lane group
+            const uint32_t c = blk * 32u + (t & 7u) * 4u;
+            const float4 xq = *reinterpret_cast<const float4*>(xs + c);
+            const float4 wq = *reinterpret_cast<const float4*>(ws + c);
+            const float xj[4] = {xq.x, xq.y, xq.z, xq.w};
+            const float wj[4] = {wq.x, wq.y, wq.z, wq.w};
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float q = xj[i] / root;
+                v[i] = q * wj[i];
+            }
+            const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<uint32_t*>(aq + c) = q.packed;
+            if ((t & 7u) == 0) {
+                asc[blk] = q.scale;
+                asm_[blk] = q.sum;
+                atot[blk] = q.total;
+            }
+        }
+    }
+    wait_vm_lds<0>();  // this wave's weights
+    lds_sync();
+
+    // This thread's pair of the row (j = t % np: whole rows of pairs per pass).
+    const uint32_t j = t % np, rpass = ONE_THREADS / np;
+    uint32_t a[16];
+    {
+        const uint4* q4 = reinterpret_cast<const uint4*>(aq + (size_t)j * 64u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 v = q4[i];
+            a[4 * i] = v.x, a[4 * i + 1] = v.y, a[4 * i + 2] = v.z, a[4 * i + 3] = v.w;
+        }
+    }
+    const float sx0 = asc[2u * j], sx1 = asc[2u * j + 1u];
+    int e0 = 0, e1 = 0;
+    float mx0 = 0.0f, mx1 = 0.0f;
+    if constexpr (KIND == 1) e0 = -8 * atot[2u * j], e1 = -8 * atot[2u * j + 1u];
+    if constexpr (KIND == 2) mx0 = asm_[2u * j], mx1 = asm_[2u * j + 1u];
+    float* part = reinterpret_cast<float*>(base + L.part);
+    // up to UNITS rows' pairs read from LDS together, then their
+    // contributions (one LDS latency a batch rather than a row)
+    constexpr uint32_t UNITS = 4;
+    for (uint32_t r0 = t / np; r0 < rows; r0 += UNITS * rpass) {
+        uint32_t u[UNITS][PW];
+#pragma unroll
+        for (uint32_t q = 0; q < UNITS; ++q) {
+            const uint32_t r = min(r0 + q * rpass, rows - 1u);
+            const uint8_t* rp = GLU ? (r < h ? base + L.w + r * row_bytes : base + L.w2 + (r - h) * row_bytes)
+                                    : base + L.w + r * row_bytes;
+            const uint32_t* pw = reinterpret_cast<const uint32_t*>(rp + j * (PW * 4u));
+#pragma unroll
+            for (uint32_t i = 0; i < PW; ++i) u[q][i] = pw[i];
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < UNITS; ++q) {
+            const uint32_t r = r0 + q * rpass;
+            if (r < rows) {
+                float c0, c1;
+                Pair<KIND>::contribute(u[q], a, sx0, sx1, e0, e1, mx0, mx1, c0, c1);
+                *(float2*)(part + (size_t)r * stride + 2u * j) = make_float2(c0, c1);
+            }
+        }
+    }
+    lds_sync();
+    float* outs = reinterpret_cast<float*>(base + L.outs);
+    for (uint32_t o = t; o < rows; o += ONE_THREADS) {
+        // the row's contributions in block order, read 64 at a time into
+        // registers before they are added (an LDS read's latency once a batch)
+        const float* c = part + (size_t)o * stride;
+        float sum = 0.0f;
+        uint32_t i = 0;
+        for (; i + 64u <= nb; i += 64u) {
+            float4 v[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) v[q] = *(const float4*)(c + i + 4u * q);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                sum += v[q].x;
+                sum += v[q].y;
+                sum += v[q].z;
+                sum += v[q].w;
+            }
+        }
+        for (; i + 4 <= nb; i += 4) {
+            const float4 v = *(const float4*)(c + i);
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+        }
+        for (; i < nb; ++i) sum += c[i];
+        if constexpr (GLU) {
+            outs[o] = sum;
+        } else {
+            const uint32_t row = row0 + o;
+            dst[row] = bias ? sum + bias[row] : sum;
+        }
+    }
+    if constexpr (GLU) {
+        // SwiGLU one output a thread (the tile's h outputs), then the
+        // quantiser, 8 lanes a block of 32
+        lds_sync();
+        float* act_out = outs + tr;
+        for (uint32_t o = t; o < h; o += ONE_THREADS) act_out[o] = swiglu_value(outs[o], outs[h + o]);
+        lds_sync();
+        const uint32_t hb = h >> 5, sub = t & 7u;
+        for (uint32_t g = t >> 3; g < hb; g += ONE_THREADS / 8u) {
+            const float4 v4 = *reinterpret_cast<const float4*>(act_out + g * 32u + sub * 4u);
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+            const uint32_t col = g0 + g * 32u + sub * 4u;
+            *(uint32_t*)((int8_t*)glu.qs + col) = q.packed;
+            if (sub == 0) {
+                const size_t at = (g0 >> 5) + g;
+                ((float*)glu.scales)[at] = q.scale;
+                ((float*)glu.sums)[at] = q.sum;
+                ((int32_t*)glu.totals)[at] = q.total;
+            }
+        }
+    }
+}
+
 // ------------------------------------------- lanes, one row, fused quantise
 
 // Steps of weight loads issued together per thread (a batch of D pairs),
@@ -1888,6 +2160,93 @@ hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations ac
     case 0: return launch_glu<0>(w, act, rows, H, k, glu, stream);
     case 1: return launch_glu<1>(w, act, rows, H, k, glu, stream);
     default: return launch_glu<2>(w, act, rows, H, k, glu, stream);
+    }
+}
+
+// ----------------------------------------- one row, weights in LDS: launchers
+
+// LDS a k_matvec_one workgroup may take: one a compute unit.
+static constexpr size_t ONE_LDS_LIMIT = 150u * 1024u;
+
+// Rows of whole pairs per pass, and rows of whole 16-byte pieces starting
+// 16-byte aligned (the direct loads take 16 bytes a lane).
+static bool one_fits(uint32_t kind, const uint8_t* w, uint32_t k) {
+    const uint32_t nb = k >> 5, np = nb >> 1;
+    return lanes_fit(w, k) && np > 0 && ONE_THREADS % np == 0 && (nb * block_bytes(kind)) % 16u == 0 &&
+           ((uintptr_t)w & 15u) == 0;
+}
+
+// Rows a workgroup: about one workgroup a compute unit, within the LDS limit.
+static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units) {
+    const uint32_t nb = k >> 5, rb = nb * block_bytes(kind), stride = lanes_stride(nb);
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    uint32_t tr = std::max(1u, (n + cus - 1u) / cus);
+    while (tr > 1 && one_lds(k, tr, rb, stride, norm, false).end > ONE_LDS_LIMIT) --tr;
+    return tr;
+}
+
+template <int KIND, bool NORM>
+static hipError_t launch_one(const uint8_t* w, const float* x, const float* nw, float eps, Activations act, float* dst,
+                             const float* bias, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+    const uint32_t nb = k >> 5, stride = lanes_stride(nb);
+    const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units);
+    const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false);
+    if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end, stream, w, x, nw,
+                       eps, act, dst, bias, n, k, tr, stride, Activations{});
+    return hipGetLastError();
+}
+
+bool rms_product_fits(const uint8_t* w, uint32_t k, const float* x, uint32_t ldx, const float* norm) {
+    (void)ldx;
+    return k <= 2048u && norm && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)norm & 15u) == 0;
+}
+
+hipError_t launch_product_rms(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, const float* norm,
+                              float eps, float* dst, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                              hipStream_t stream) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (rows != 1 || !rms_product_fits(w, k, x, ldx, norm) || !one_fits(kind, w, k)) return hipErrorInvalidValue;
+    switch (kind) {
+    case 0: return launch_one<0, true>(w, x, norm, eps, Activations{}, dst, nullptr, n, k, compute_units, stream);
+    case 1: return launch_one<1, true>(w, x, norm, eps, Activations{}, dst, nullptr, n, k, compute_units, stream);
+    default: return launch_one<2, true>(w, x, norm, eps, Activations{}, dst, nullptr, n, k, compute_units, stream);
+    }
+}
+
+hipError_t launch_product_one(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* bias,
+                              uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    if (!one_fits(kind, w, k) || ((uintptr_t)act.qs & 15u) != 0) return hipErrorInvalidValue;
+    switch (kind) {
+    case 0: return launch_one<0, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
+    case 1: return launch_one<1, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
+    default: return launch_one<2, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
+    }
+}
+
+template <int KIND>
+static hipError_t launch_glu_one(const uint8_t* w, const float* x, const float* norm, float eps, uint32_t H,
+                                 uint32_t k, Activations glu, hipStream_t stream) {
+    const uint32_t nb = k >> 5, h = glu_half(nb), stride = lanes_stride(nb);
+    const OneLds L = one_lds(k, 2u * h, nb * Fmt<KIND>::BB, stride, true, true);
+    if (L.end > ONE_LDS_LIMIT || H % h != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_matvec_one<KIND, true, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w, x, norm, eps,
+                       Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up_swiglu_rms(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, const float* norm,
+                                     float eps, uint32_t rows, uint32_t H, uint32_t k, Activations glu,
+                                     hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    if (rows != 1 || !rms_product_fits(w, k, x, ldx, norm) || !one_fits(kind, w, k)) return hipErrorInvalidValue;
+    const uint32_t np = (k >> 5) / 2u;
+    if ((np & (np - 1u)) != 0) return hipErrorInvalidValue;
+    switch (kind) {
+    case 0: return launch_glu_one<0>(w, x, norm, eps, H, k, glu, stream);
+    case 1: return launch_glu_one<1>(w, x, norm, eps, H, k, glu, stream);
+    default: return launch_glu_one<2>(w, x, norm, eps, H, k, glu, stream);
     }
 }
 

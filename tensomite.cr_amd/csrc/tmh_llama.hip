@@ -22,6 +22,7 @@ using tmh::DeviceContext;
 int code(hipError_t e) { return e == hipErrorOutOfMemory ? TMH_ERROR_OUT_OF_MEMORY : (int)e; }
 
 
+
 int check_rope(uint32_t heads, uint32_t kv_heads, uint32_t width, uint32_t table_rows, uint32_t capacity) {
     if (width == 0 || width % 2u != 0 || heads == 0 || kv_heads == 0 || capacity == 0) return TMH_ERROR_SHAPE;
     if (capacity > table_rows) return TMH_ERROR_SHAPE;
@@ -105,6 +106,15 @@ hipError_t norm_quantise(const Llama& m, const DeviceContext& ctx, const float* 
 hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
                     uint32_t k, int& cur) {
     const uint32_t W = (uint32_t)m.c.width;
+    if (rows == 1) {
+        // one row: the weights of each workgroup's tile staged into LDS at once
+        hipError_t r = tmh::launch_product_one(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], W, k, ctx.compute_units,
+                                               ctx.stream);
+        if (r != hipErrorInvalidValue) {
+            cur ^= 1;
+            return r;
+        }
+    }
     hipError_t r = tmh::launch_product_residual(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], rows, W, k,
                                                 ctx.compute_units, ctx.stream);
     if (r != hipErrorInvalidValue) {
@@ -131,14 +141,25 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
     const uint32_t W = (uint32_t)c.width, H = (uint32_t)c.hidden, hw = (uint32_t)c.head_width;
     const float scale = (float)(1.0 / std::sqrt((double)hw));
     const bool quant_att = hw % 32u == 0;
+    const bool rows_fused = tokens == 1;
     int cur = 0;
     hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x[cur], ctx.errors, ctx.stream);
     const tmh::Activations a_in = tmh::carve_scratch(m.scratch[0], tokens, W);
     for (int32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
         float* keys = m.keys + (size_t)l * m.layer_cache;
         float* values = m.values + (size_t)l * m.layer_cache;
-        e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in);
-        if (e == hipSuccess) e = product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out, nullptr);
+        // one row: the norm and quantiser in the product's prologue (one
+        // launch); else RMSNorm+quantise, then the product
+        hipError_t f = rows_fused ? tmh::launch_product_rms(c.kind, m.qkv[l], m.x[cur], W, m.attn_norm[l], c.eps,
+                                                            m.qkv_out, tokens, m.nqkv, W, ctx.compute_units,
+                                                            ctx.stream)
+                                  : hipErrorInvalidValue;
+        if (f == hipErrorInvalidValue) {
+            e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in);
+            if (e == hipSuccess) e = product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out, nullptr);
+        } else {
+            e = f;
+        }
         const tmh::Activations a_att = tmh::carve_scratch(m.scratch[1], tokens, m.qn);
         tmh::RopeWrite r{m.qkv_out, m.nqkv, (uint32_t)c.heads, (uint32_t)c.kv_heads, hw, m.cos, m.sin,
                          m.slots, m.rows, m.capacity, m.q, keys, values, ctx.errors};
@@ -155,9 +176,19 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
         }
         if (e == hipSuccess && !quant_att) e = quantise(ctx, m.att, tokens, m.qn, a_att);
         if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur);
-        if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in);
         const tmh::Activations a_hid = tmh::carve_scratch(m.scratch[1], tokens, H);
-        if (e == hipSuccess) {
+        // one row: RMSNorm in gate_up's prologue, SwiGLU and the quantiser in
+        // its epilogue (one launch)
+        hipError_t fg = (e == hipSuccess && rows_fused)
+                            ? tmh::launch_gate_up_swiglu_rms(c.kind, m.gate_up[l], m.x[cur], W, m.ffn_norm[l], c.eps,
+                                                             tokens, H, W, a_hid, ctx.stream)
+                            : hipErrorInvalidValue;
+        if (fg != hipErrorInvalidValue) {
+            e = fg;
+        } else if (e == hipSuccess) {
+            e = norm_quantise(m, ctx, m.x[cur], m.ffn_norm[l], tokens, a_in);
+        }
+        if (e == hipSuccess && fg == hipErrorInvalidValue) {
             // gate_up with SwiGLU and the quantiser in its epilogue where the
             // shape allows, else the product then SwiGLU+quantise
             hipError_t g = tmh::launch_gate_up_swiglu(c.kind, m.gate_up[l], a_in, tokens, H, W, a_hid, ctx.stream);
@@ -172,10 +203,15 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
         if (e == hipSuccess) e = residual(m, ctx, m.down[l], a_hid, tokens, H, cur);
     }
     const tmh::Activations a_fin = tmh::carve_scratch(m.scratch[0], final_rows, W);
+    float* logits = m.logits + (size_t)logits_row * c.vocab;
+    hipError_t fh = (e == hipSuccess && final_rows == 1)
+                        ? tmh::launch_product_rms(c.kind, m.head, m.x[cur] + (size_t)final_from * W, W, m.norm, c.eps,
+                                                  logits, final_rows, (uint32_t)c.vocab, W, ctx.compute_units,
+                                                  ctx.stream)
+                        : hipErrorInvalidValue;
+    if (fh != hipErrorInvalidValue) return fh;
     if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur] + (size_t)final_from * W, m.norm, final_rows, a_fin);
-    if (e == hipSuccess)
-        e = product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, m.logits + (size_t)logits_row * c.vocab,
-                    nullptr);
+    if (e == hipSuccess) e = product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, logits, nullptr);
     return e;
 }
 
