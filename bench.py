@@ -591,10 +591,11 @@ def gemm_config4(dev, steps, warmup, mode="auto"):
     """Config 4: the Q8_0 prefill GEMM at the Llama-1.7B shape, 512 tokens x
     K = 2048 against N = 2048 (attention projections) and N = 8192 (MLP
     up/gate). One call is tmh_block_matmul over f32 x (the activation
-    quantiser, then the matrix-core kernel, k_matmul_mfma); HIP events every
+    quantiser, then the matrix-core kernel, k_matmul_mx); HIP events every
     4 calls, the median over 100 groups. int8 work: 2 · 512 · 2048 · N ops a call.
-    mode "unordered" runs the measurement kernel that sums the raw MFMA
-    results without the block-ordered epilogue."""
+    mode "unordered" runs the same kernel with each block's contribution
+    added by one fused multiply-add (measurement only: it prices the
+    host-ordered, separately rounded fold)."""
     import quant_host
     import tensomite_hip as th
     rows, k = 512, 2048

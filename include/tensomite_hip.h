@@ -62,11 +62,15 @@ extern "C" {
 #define TMH_Q4_1 2 /* F16 d, F16 m, 16 bytes of nibbles: x = q·d + m (20 bytes) */
 
 /* How a product divides its work: BlockMatMulMode (quant.cr:5-28). AUTO,
- * THREAD, LANES and MATRIX give the host's bits; UNORDERED is for
- * measurement only and may differ in the last bits. LOADS, STREAM and
- * STREAM_ACTIVATIONS are Metal measurement modes the reference runs as LANES
- * elsewhere; so does this device. MATRIX has no counterpart in the
- * reference: the int8 matrix-core path for many activation rows. */
+ * THREAD, LANES and MATRIX give the host's bits. UNORDERED is for
+ * measurement only (quant.cr:14-17 prices the ordered sum the same way):
+ * from 32 activation rows, where k is a multiple of 256, it runs the
+ * matrix-core kernel with each block's contribution added by one fused
+ * multiply-add, and its results may differ in the last bits; elsewhere it
+ * runs as LANES. LOADS, STREAM and STREAM_ACTIVATIONS are Metal measurement
+ * modes the reference runs as LANES elsewhere; so does this device. MATRIX
+ * has no counterpart in the reference: the int8 matrix-core path for many
+ * activation rows. */
 #define TMH_MODE_AUTO 0
 #define TMH_MODE_THREAD 1
 #define TMH_MODE_LANES 2

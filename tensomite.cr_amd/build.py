@@ -7,6 +7,10 @@ Flags that the results depend on:
                           ordered fold
   -Xclang -target-feature -Xclang -packed-fp32-ops
                           no packed f32 arithmetic in generated code
+  -mllvm -amdgpu-mfma-vgpr-form=1
+                          MFMA results in VGPRs, not AGPRs: the matrix-core
+                          kernels read every result with VALU operations,
+                          and an AGPR would cost a v_accvgpr_read each
 """
 from __future__ import annotations
 
@@ -29,6 +33,7 @@ FLAGS = [
     "-ffp-contract=off",
     "-fno-gpu-rdc",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-result",
     "-I", os.path.join(ROOT, "include"),

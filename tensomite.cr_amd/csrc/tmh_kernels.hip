@@ -1566,6 +1566,378 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const uint8_t* __restrict__
         }
 }
 
+// ------------------------------------------ matrix cores: stages of 8 blocks
+
+// x · wᵀ for many activation rows on the int8 matrix cores, for k a multiple
+// of 256 and 16-byte aligned weights and activation parts. Workgroup tile 64
+// activation rows x 64 outputs, 4 waves (one a SIMD), each a 32 x 32 tile:
+// per block, one v_mfma_i32_32x32x32_i8 gives the tile's 1024 integer dot
+// products of that block alone, exact (a lane holds 16 outputs: column
+// lane % 32, rows 8 (i / 4) + 4 (lane / 32) + i % 4), and every output adds
+// the block's contribution, in the host's expression, to its running f32 sum
+// in block order (the expressions of k_matmul_mfma above). The factors
+// those expressions take per output come from f16 MFMAs over operands whose
+// k slots other than one hold zeros: d·sx and m·mx (products of two halves,
+// exact in f32 -- the host's products) for Q8_0 and Q4_1, and d and sx
+// themselves (times 1) for Q4_0. Each lane thus folds 16 outputs at three
+// VALU operations each.
+//
+// The k axis goes in stages of 8 blocks, one workgroup barrier a stage, every
+// byte brought by direct loads (global_load_lds_dwordx4: 16 bytes a lane, no
+// VGPR holds data in flight, each wave waits for its own loads by count):
+// the 64 weight rows' 8 blocks as they lie in memory, with the activation
+// rows' scales (and Q4_1 sums), three stages ahead; the 64 activation rows'
+// 256 int8 values (272 bytes apart in LDS), two stages ahead. While stage s
+// is computed, the workgroup repacks the weights of stage s + 1: each
+// block's 32 values 16-byte aligned (Q4 nibbles as bytes, Q4_0 less 8),
+// rows 272 bytes apart, so that the 8 lanes the LDS serves together read 16
+// bytes each from different banks; scales as f16 MFMA operands. A
+// workgroup's tile comes from its id so that the 8 activation tiles of one
+// weight tile run on one XCD (ids go round-robin over the 8 XCDs): the
+// weight tile comes from HBM once, into that XCD's L2.
+//
+// FUSED (TMH_MODE_UNORDERED, measurement only) adds each contribution with
+// one fused multiply-add instead of the host's separately rounded product
+// and sum: the same work with one VALU operation fewer an output and block,
+// which prices the exact fold; its results may differ in the last bits.
+constexpr uint32_t MX_TILE = 64;
+constexpr uint32_t MX_STAGE = 8;
+constexpr uint32_t MX_THREADS = 256;
+constexpr uint32_t MX_ROW = 272;   // LDS bytes per activation row and packed weight row (256 + a 16-byte pad)
+constexpr uint32_t MX_TAB_ROW = MX_TILE + 1u;  // a table's entries per block: 64 rows and a zero
+
+template <int KIND>
+struct Mx {
+    static constexpr uint32_t RB = MX_STAGE * Fmt<KIND>::BB;  // a weight row's bytes in a stage
+    static constexpr uint32_t RC = RB / 16u;
+    // Raw weight group (three buffers): weights [64][RB], scales [64][8]
+    // f32, Q4_1 sums [64][8] f32.
+    static constexpr uint32_t W_S = MX_TILE * RB;
+    static constexpr uint32_t W_E = W_S + MX_TILE * MX_STAGE * 4u;
+    static constexpr uint32_t W_BYTES = W_E + (KIND == 2 ? MX_TILE * MX_STAGE * 4u : 0u);
+    static constexpr uint32_t W_LOADS = W_BYTES / 1024u;
+    // Raw activations (three buffers): [64][MX_ROW].
+    static constexpr uint32_t A_BYTES = MX_TILE * MX_ROW;
+    static constexpr uint32_t A_LOADS = A_BYTES / 1024u;
+    // Packed (two buffers): values [64][MX_ROW], then tables [8][65] of
+    // 8-byte f16 MFMA operands (the half in the first k slot) by block, so
+    // that 16 lanes' reads of one block fill the 32 banks: D (d of each
+    // weight row), S (sx of each activation row), Q4_1 also M (m), E (mx);
+    // entry 64 of each block is zero, for the lanes whose k slots must be.
+    static constexpr uint32_t TAB = MX_STAGE * MX_TAB_ROW * 8u;
+    static constexpr uint32_t TABLES = KIND == 2 ? 4u : 2u;
+    static constexpr uint32_t P_D = MX_TILE * MX_ROW;
+    static constexpr uint32_t P_S = P_D + TAB;
+    static constexpr uint32_t P_M = P_S + TAB;
+    static constexpr uint32_t P_E = P_M + (KIND == 2 ? TAB : 0u);
+    static constexpr uint32_t P_BYTES = P_E + (KIND == 2 ? TAB : 0u);
+    static constexpr uint32_t RW = 0, RA = 3u * W_BYTES, PK = RA + 3u * A_BYTES;
+    static constexpr uint32_t LDS = PK + 2u * P_BYTES;
+    static_assert(W_BYTES % 1024u == 0 && A_BYTES % 1024u == 0, "whole wave loads");
+    static_assert(LDS <= 160u * 1024u, "one workgroup's LDS");
+};
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef long v2l __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ long mx_half_op(float x) { return (long)__builtin_bit_cast(uint16_t, (_Float16)x); }
+
+__device__ __forceinline__ v4h mx_op(long v) { return __builtin_bit_cast(v4h, v); }
+
+// The nibbles of one dword of a Q4 block (values 4 i .. as low nibbles,
+// 16 + 4 i .. as high) as bytes, dwords i and 4 + i of the block's values;
+// Q4_0 less 8 (for v in 0..15, ((v ^ 8) + 0x78) ^ 0x78 is v - 8 as a byte,
+// with no carry between bytes).
+template <int KIND>
+__device__ __forceinline__ void mx_unpack(uint32_t v, uint32_t& lo, uint32_t& hi) {
+    lo = v & 0x0f0f0f0fu;
+    hi = (v >> 4) & 0x0f0f0f0fu;
+    if constexpr (KIND == 1) {
+        lo = ((lo ^ 0x08080808u) + 0x78787878u) ^ 0x78787878u;
+        hi = ((hi ^ 0x08080808u) + 0x78787878u) ^ 0x78787878u;
+    }
+}
+
+// Repacks a raw weight group into a packed buffer: thread t takes pair
+// t % 4 of weight row t / 4, and blocks 2 (t % 4) + 0, 1 of activation row
+// t / 4's scales.
+template <int KIND>
+__device__ __forceinline__ void mx_repack(const uint8_t* raw, uint8_t* pk, uint32_t t) {
+    using M = Mx<KIND>;
+    constexpr uint32_t PB = 2u * Fmt<KIND>::BB;  // bytes of a raw pair
+    const uint32_t c = t >> 2, p = t & 3u;
+    const uint32_t* r = (const uint32_t*)(raw + c * M::RB + PB * p);
+    uint32_t v[16];
+    long d0, d1;
+    if constexpr (KIND == 0) {
+        uint32_t e[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) e[i] = r[i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = funnel(e[i + 1], e[i], 2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[8 + i] = e[9 + i];
+        d0 = (long)(e[0] & 0xffffu), d1 = (long)(e[8] >> 16);
+    } else if constexpr (KIND == 1) {
+        uint32_t e[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) e[i] = r[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mx_unpack<KIND>(funnel(e[i + 1], e[i], 2), v[i], v[4 + i]);
+            mx_unpack<KIND>(e[5 + i], v[8 + i], v[12 + i]);
+        }
+        d0 = (long)(e[0] & 0xffffu), d1 = (long)(e[4] >> 16);
+    } else {
+        uint32_t e[10];
+#pragma unroll
+        for (int i = 0; i < 10; ++i) e[i] = r[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mx_unpack<KIND>(e[1 + i], v[i], v[4 + i]);
+            mx_unpack<KIND>(e[6 + i], v[8 + i], v[12 + i]);
+        }
+        d0 = (long)(e[0] & 0xffffu), d1 = (long)(e[5] & 0xffffu);
+            long* mt = (long*)(pk + M::P_M) + 2u * p * MX_TAB_ROW + c;
+        mt[0] = (long)(e[0] >> 16), mt[MX_TAB_ROW] = (long)(e[5] >> 16);
+    }
+    uint8_t* dst = pk + c * MX_ROW + 64u * p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(uint4*)(dst + 16u * i) = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    const uint32_t at = 2u * p * MX_TAB_ROW + c;  // entry of block 2p, row c
+    long* dt = (long*)(pk + M::P_D) + at;
+    dt[0] = d0, dt[MX_TAB_ROW] = d1;
+    const float2 sx = *(const float2*)(raw + M::W_S + (c * 8u + 2u * p) * 4u);
+    long* st = (long*)(pk + M::P_S) + at;
+    st[0] = mx_half_op(sx.x), st[MX_TAB_ROW] = mx_half_op(sx.y);
+    if constexpr (KIND == 2) {
+        const float2 mx = *(const float2*)(raw + M::W_E + (c * 8u + 2u * p) * 4u);
+        long* et = (long*)(pk + M::P_E) + at;
+        et[0] = mx_half_op(mx.x), et[MX_TAB_ROW] = mx_half_op(mx.y);
+    }
+}
+
+// One block's MFMA results: the dot products and the factors of the
+// contributions ([0]: d·sx, or Q4_0 d; [1]: Q4_1 m·mx, Q4_0 sx).
+struct MxBlock {
+    v16i t;
+    v16f f[2];
+};
+
+// Operand bases of a lane within a stage (the tables' for lanes 0-31;
+// zeros for the others, whose k slots must be zero).
+struct MxBase {
+    const uint8_t* a;     // activation row + 16 (lane / 32)
+    const uint8_t* w;     // packed weight row + 16 (lane / 32)
+    const uint8_t* d;     // D row (Q4_1: M at + P_M - P_D)
+    const uint8_t* s;     // S row (Q4_1: E at + P_E - P_S)
+    const uint8_t* m;     // Q4_1: M row
+    const uint8_t* e;     // Q4_1: E row
+};
+
+// One block's operands, read from LDS a stage at a time.
+struct MxOps {
+    v4i a, w;
+    long d, s, m, e;
+};
+
+template <int KIND>
+__device__ __forceinline__ void mx_operands(MxOps& o, const MxBase& B, uint32_t b) {
+    o.a = *(const v4i*)(B.a + 32u * b);
+    o.w = *(const v4i*)(B.w + 32u * b);
+    o.d = *(const long*)(B.d + 8u * MX_TAB_ROW * b);
+    o.s = *(const long*)(B.s + 8u * MX_TAB_ROW * b);
+    if constexpr (KIND == 2) {
+        o.m = *(const long*)(B.m + 8u * MX_TAB_ROW * b);
+        o.e = *(const long*)(B.e + 8u * MX_TAB_ROW * b);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void mx_block(MxBlock& o, const MxOps& p, long one) {
+    const v16i zi = {};
+    const v16f zf = {};
+    o.t = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.a, p.w, zi, 0, 0, 0);
+    if constexpr (KIND == 1) {
+        o.f[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(mx_op(one), mx_op(p.d), zf, 0, 0, 0);
+        o.f[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(mx_op(p.s), mx_op(one), zf, 0, 0, 0);
+    } else {
+        o.f[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(mx_op(p.s), mx_op(p.d), zf, 0, 0, 0);
+        if constexpr (KIND == 2) o.f[1] = __builtin_amdgcn_mfma_f32_32x32x8f16(mx_op(p.e), mx_op(p.m), zf, 0, 0, 0);
+    }
+}
+
+// Adds one block's contributions to the lane's 16 sums.
+template <int KIND, bool FUSED>
+__device__ __forceinline__ void mx_add(float (&acc)[16], const MxBlock& o) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float ft = (float)o.t[i];
+        if constexpr (KIND == 0) {
+            if constexpr (FUSED) acc[i] = __builtin_fmaf(ft, o.f[0][i], acc[i]);
+            else acc[i] += ft * o.f[0][i];
+        } else if constexpr (KIND == 1) {
+            const float p = ft * o.f[0][i];
+            if constexpr (FUSED) acc[i] = __builtin_fmaf(p, o.f[1][i], acc[i]);
+            else acc[i] += p * o.f[1][i];
+        } else {
+            if constexpr (FUSED) {
+                acc[i] = __builtin_fmaf(o.f[0][i], ft, acc[i] + o.f[1][i]);
+            } else {
+                const float f = o.f[0][i] * ft;
+                acc[i] += f + o.f[1][i];
+            }
+        }
+    }
+}
+
+template <int KIND, bool FUSED>
+__global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_matmul_mx(
+    const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst, const float* __restrict__ bias,
+    uint32_t m, uint32_t n, uint32_t k, uint32_t tiles_m, uint32_t tiles) {
+    using M = Mx<KIND>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[M::LDS];
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t l32 = lane & 31u, half = lane >> 5;
+    const uint32_t nb = k >> 5, stages = nb / MX_STAGE;
+    uint32_t g = blockIdx.x;
+    if (tiles % 8u == 0) g = (g & 7u) * (tiles >> 3) + (g >> 3);
+    const uint32_t n0 = (g / tiles_m) * MX_TILE, m0 = (g % tiles_m) * MX_TILE;
+    const uint32_t mw = (wave & 1u) * 32u, nw = (wave >> 1) * 32u;
+    const size_t row_bytes = (size_t)nb * Fmt<KIND>::BB;
+    // The tables' zero entries (the repack never writes them).
+    if (t < 2u * M::TABLES * MX_STAGE) {
+        const uint32_t buffer = t / (M::TABLES * MX_STAGE), table = (t / MX_STAGE) % M::TABLES, b = t % MX_STAGE;
+        ((long*)(lds + M::PK + buffer * M::P_BYTES + M::P_D + table * M::TAB))[b * MX_TAB_ROW + MX_TILE] = 0;
+    }
+
+    // This wave's direct loads: weight-group instructions iw = wave + 4 j
+    // (below W_LOADS) and activation instructions ia with (ia + W_LOADS) % 4
+    // = wave; lane l fills bytes 1024 i + 16 l of the group's buffer, from
+    // src + stage · step. (A pad chunk of an activation row brings the row's
+    // last chunk again.)
+    constexpr uint32_t WAVES = MX_THREADS / 64u;
+    constexpr uint32_t WJ = (M::W_LOADS + WAVES - 1u) / WAVES, AJ = (M::A_LOADS + WAVES - 1u) / WAVES;
+    const uint8_t* wsrc[WJ];
+    uint32_t wstep[WJ], wcount = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < WJ; ++j) {
+        const uint32_t i = wave + WAVES * j, at = 1024u * i + 16u * lane;
+        wsrc[j] = w, wstep[j] = 0;
+        if (i >= M::W_LOADS) continue;
+        ++wcount;
+        if (at < M::W_S) {
+            const uint32_t p = at / 16u, row = p / M::RC, chunk = p % M::RC;
+            wsrc[j] = w + (size_t)min(n0 + row, n - 1u) * row_bytes + 16u * chunk;
+            wstep[j] = M::RB;
+        } else {
+            const bool ex = at >= M::W_E;
+            const uint32_t e = (at - (ex ? M::W_E : M::W_S)) / 16u, row = e >> 1;
+            const float* from = ex ? act.sums : act.scales;
+            wsrc[j] = (const uint8_t*)(from + (size_t)min(m0 + row, m - 1u) * nb + 4u * (e & 1u));
+            wstep[j] = MX_STAGE * 4u;
+        }
+    }
+    const uint8_t* asrc[AJ];
+    const uint32_t afirst = (wave + WAVES - M::W_LOADS % WAVES) % WAVES;
+    uint32_t acount = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < AJ; ++j) {
+        const uint32_t i = afirst + WAVES * j;
+        asrc[j] = (const uint8_t*)act.qs;
+        if (i >= M::A_LOADS) continue;
+        ++acount;
+        const uint32_t p = 64u * i + lane, row = p / 17u, chunk = min(p % 17u, 15u);
+        asrc[j] = (const uint8_t*)act.qs + (size_t)min(m0 + row, m - 1u) * k + 16u * chunk;
+    }
+    auto issue_w = [&](uint32_t s) {
+        const uint32_t to = lds_address(lds + M::RW + (s % 3u) * M::W_BYTES) + wave * 1024u;
+#pragma unroll
+        for (uint32_t j = 0; j < WJ; ++j)
+            if (wave + WAVES * j < M::W_LOADS) lds_load16(wsrc[j] + (size_t)s * wstep[j], to + j * (WAVES * 1024u));
+    };
+    auto issue_a = [&](uint32_t s) {
+        const uint32_t to = lds_address(lds + M::RA + (s % 3u) * M::A_BYTES) + afirst * 1024u;
+#pragma unroll
+        for (uint32_t j = 0; j < AJ; ++j)
+            if (afirst + WAVES * j < M::A_LOADS) lds_load16(asrc[j] + (size_t)s * 256u, to + j * (WAVES * 1024u));
+    };
+    auto barrier = [&](uint32_t outstanding) {
+        asm volatile("" ::: "memory");
+        wait_vm_lds_upto<16>(outstanding);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+    // Weights of stages 0-2 and activations of 0-1 in flight; stage 0
+    // repacked.
+    issue_w(0);
+    issue_a(0);
+    if (stages > 1u) issue_w(1), issue_a(1);
+    if (stages > 2u) issue_w(2);
+    barrier((stages > 1u ? acount : 0u) + (stages > 2u ? wcount : 0u));
+    mx_repack<KIND>(lds + M::RW, lds + M::PK, t);
+    barrier(63);
+
+    const long one = half == 0 ? 0x3c00l : 0l;  // the f16 operand (1, 0, 0, 0) for lanes 0-31
+    for (uint32_t s = 0; s < stages; ++s) {
+        if (s + 3u < stages) issue_w(s + 3u);
+        if (s + 2u < stages) issue_a(s + 2u);
+        const uint8_t* pk = lds + M::PK + (s & 1u) * M::P_BYTES;
+        MxBase B;
+        B.a = lds + M::RA + (s % 3u) * M::A_BYTES + (mw + l32) * MX_ROW + 16u * half;
+        B.w = pk + (nw + l32) * MX_ROW + 16u * half;
+        const uint32_t wcol = half == 0 ? (nw + l32) * 8u : MX_TILE * 8u;  // the zero entry for lanes 32-63
+        const uint32_t arow = half == 0 ? (mw + l32) * 8u : MX_TILE * 8u;
+        B.d = pk + M::P_D + wcol;
+        B.s = pk + M::P_S + arow;
+        B.m = pk + M::P_M + wcol;
+        B.e = pk + M::P_E + arow;
+        // The stage's operand reads go out together, then the repack of
+        // stage s + 1 (its LDS traffic and VALU work overlap their latency),
+        // then the blocks: the MFMAs of block b + 1 before the additions of
+        // block b.
+        MxOps ops[MX_STAGE];
+#pragma unroll
+        for (uint32_t b = 0; b < MX_STAGE; ++b) mx_operands<KIND>(ops[b], B, b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1u < stages)
+            mx_repack<KIND>(lds + M::RW + ((s + 1u) % 3u) * M::W_BYTES, lds + M::PK + ((s + 1u) & 1u) * M::P_BYTES, t);
+        MxBlock cur, nxt;
+        mx_block<KIND>(cur, ops[0], one);
+#pragma unroll
+        for (uint32_t b = 0; b < MX_STAGE; ++b) {
+            if (b + 1u < MX_STAGE) mx_block<KIND>(nxt, ops[b + 1u], one);
+            mx_add<KIND, FUSED>(acc, cur);
+            cur = nxt;
+        }
+        // The stage's sums are complete before the barrier: the compiler
+        // would otherwise move the additions after it.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(acc[i]));
+        // Weights of stage s + 2 and activations of s + 1 have landed (the
+        // loads issued above stay in flight); every wave is done with this
+        // stage's buffers.
+        if (s + 1u < stages) barrier((s + 3u < stages ? wcount : 0u) + (s + 2u < stages ? acount : 0u));
+    }
+
+    const uint32_t col = n0 + nw + l32;
+    const float b = (bias && col < n) ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t row = m0 + mw + 8u * (i / 4) + 4u * half + (i % 4);
+        if (row < m && col < n) dst[(size_t)row * n + col] = bias ? acc[i] + b : acc[i];
+    }
+}
+
 // ------------------------------------------------- thread per output
 
 // One thread per output, adding its blocks in order from byte loads: any
@@ -2062,6 +2434,29 @@ static hipError_t launch_mfma(const uint8_t* w, Activations act, float* dst, con
     return hipGetLastError();
 }
 
+// The staged matrix-core kernel takes k a multiple of 256 (whole stages of
+// 8 blocks) over 16-byte aligned weights and activation parts (its direct
+// loads bring 16 bytes a lane).
+static bool mx_fits(const uint8_t* w, const Activations& act, uint32_t kind, uint32_t k) {
+    const uint32_t nb = k >> 5;
+    const uintptr_t extra = kind == 2 ? (uintptr_t)act.sums : 0;
+    return k % 32u == 0 && nb >= MX_STAGE && nb % MX_STAGE == 0 &&
+           (((uintptr_t)w | (uintptr_t)act.qs | (uintptr_t)act.scales | extra) % 16u) == 0;
+}
+
+template <int KIND>
+static hipError_t launch_mx(bool fused, const uint8_t* w, Activations act, float* dst, const float* bias,
+                            uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
+    const uint32_t tiles_m = (rows + MX_TILE - 1u) / MX_TILE, tiles = tiles_m * ((n + MX_TILE - 1u) / MX_TILE);
+    if (fused)
+        hipLaunchKernelGGL((k_matmul_mx<KIND, true>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
+                           rows, n, k, tiles_m, tiles);
+    else
+        hipLaunchKernelGGL((k_matmul_mx<KIND, false>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
+                           rows, n, k, tiles_m, tiles);
+    return hipGetLastError();
+}
+
 // Activation rows from which AUTO takes the matrix cores rather than lanes.
 static constexpr uint32_t MATRIX_ROWS = 32;
 
@@ -2071,6 +2466,14 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
     if (rows == 0 || n == 0) return hipSuccess;
     const bool fits = lanes_fit(w, k);
     const bool matrix = fits && (mode == 7u /* MATRIX */ || (mode == 0u /* AUTO */ && rows >= MATRIX_ROWS));
+    const bool fused = mode == 3u /* UNORDERED */ && rows >= MATRIX_ROWS;
+    if ((matrix || fused) && mx_fits(w, act, kind, k)) {
+        switch (kind) {
+        case 0: return launch_mx<0>(fused, w, act, dst, bias, rows, n, k, stream);
+        case 1: return launch_mx<1>(fused, w, act, dst, bias, rows, n, k, stream);
+        default: return launch_mx<2>(fused, w, act, dst, bias, rows, n, k, stream);
+        }
+    }
     if (matrix) {
         switch (kind) {
         case 0: return launch_mfma<0>(w, act, dst, bias, rows, n, k, stream);

@@ -559,6 +559,25 @@ def test_matrix_cores_bit_exact(dev, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
+def test_matrix_cores_subnormal_scales(dev, fmt):
+    # Weights and activations small enough that the block scales d, the
+    # activation scales and the Q4_1 sums are subnormal halves: the f16
+    # products of the matrix-core kernel must keep them, not flush them.
+    rows, n, k = 64, 128, 512
+    say("matrix subnormal", fmt)
+    wq = weights(fmt, n, k, 920, scale=1e-4)
+    x = acts(rows, k, 921, scale=1e-3)
+    want = oracle.matmul(fmt, x, wq, rows, n, k)
+    got = run_product(dev, fmt, wq, x, rows, n, k, mode="matrix")
+    assert np.array_equal(bits(got), bits(want))
+    size = {"Q8_0": 34, "Q4_0": 18, "Q4_1": 20}[fmt]
+    d_bits = np.asarray(wq, np.uint8).reshape(-1, size)[:, :2].copy().view(np.uint16)
+    assert ((d_bits & 0x7c00) == 0).mean() > 0.5  # most weight scales are subnormal halves
+    s, _, _ = oracle.quantize_activations(x[:k], with_sums=True)
+    assert (np.abs(s) < 6.1e-5).any() and (np.abs(s) > 0).all()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
 def test_matrix_cores_with_bias_and_slice(dev, fmt):
     rows, n, k = 70, 96, 1280
     rng = np.random.default_rng(5)
@@ -570,6 +589,21 @@ def test_matrix_cores_with_bias_and_slice(dev, fmt):
     say("matrix slice", fmt)
     got = run_product(dev, fmt, wq, x, rows, 40, k, mode="matrix", bias=bias, w_row=30)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_unordered_matrix_close(dev, fmt):
+    # UNORDERED from 32 rows runs the matrix-core kernel with each block's
+    # contribution added by one fused multiply-add: the host's sums to within
+    # the rounding of 32 products and sums (k = 1024), not its bits.
+    rows, n, k = 64, 192, 1024
+    say("unordered matrix", fmt)
+    wq = weights(fmt, n, k, 910)
+    x = acts(rows, k, 911)
+    want = oracle.matmul(fmt, x, wq, rows, n, k)
+    got = run_product(dev, fmt, wq, x, rows, n, k, mode="unordered")
+    scale = float(np.abs(want).max())
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * scale)
 
 
 def test_bench_config2_plan_bit_exact(dev):
