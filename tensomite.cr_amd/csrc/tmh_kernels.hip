@@ -1602,7 +1602,8 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const uint8_t* __restrict__
 // which prices the exact fold; its results may differ in the last bits.
 constexpr uint32_t MX_TILE = 64;
 constexpr uint32_t MX_STAGE = 8;
-constexpr uint32_t MX_THREADS = 256;
+constexpr uint32_t MX_THREADS = 512;  // 4 compute waves (one a SIMD) and 4 producer waves
+constexpr uint32_t MX_COMPUTE = 4;
 constexpr uint32_t MX_ROW = 272;   // LDS bytes per activation row and packed weight row (256 + a 16-byte pad)
 constexpr uint32_t MX_TAB_ROW = MX_TILE + 1u;  // a table's entries per block: 64 rows and a zero
 
@@ -1795,19 +1796,21 @@ __device__ __forceinline__ void mx_add(float (&acc)[16], const MxBlock& o) {
 }
 
 template <int KIND, bool FUSED>
-__global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_matmul_mx(
+__global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_matmul_mx(
     const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst, const float* __restrict__ bias,
     uint32_t m, uint32_t n, uint32_t k, uint32_t tiles_m, uint32_t tiles) {
     using M = Mx<KIND>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[M::LDS];
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const bool producer = wave >= MX_COMPUTE;
+    const uint32_t pw = wave - MX_COMPUTE, pt = t - 64u * MX_COMPUTE;  // producer wave, thread
     const uint32_t l32 = lane & 31u, half = lane >> 5;
     const uint32_t nb = k >> 5, stages = nb / MX_STAGE;
     uint32_t g = blockIdx.x;
     if (tiles % 8u == 0) g = (g & 7u) * (tiles >> 3) + (g >> 3);
     const uint32_t n0 = (g / tiles_m) * MX_TILE, m0 = (g % tiles_m) * MX_TILE;
-    const uint32_t mw = (wave & 1u) * 32u, nw = (wave >> 1) * 32u;
+    const uint32_t mw = (wave & 1u) * 32u, nw = ((wave >> 1) & 1u) * 32u;
     const size_t row_bytes = (size_t)nb * Fmt<KIND>::BB;
     // The tables' zero entries (the repack never writes them).
     if (t < 2u * M::TABLES * MX_STAGE) {
@@ -1815,20 +1818,20 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1
         ((long*)(lds + M::PK + buffer * M::P_BYTES + M::P_D + table * M::TAB))[b * MX_TAB_ROW + MX_TILE] = 0;
     }
 
-    // This wave's direct loads: weight-group instructions iw = wave + 4 j
+    // A producer wave's direct loads: weight-group instructions iw = pw + 4 j
     // (below W_LOADS) and activation instructions ia with (ia + W_LOADS) % 4
-    // = wave; lane l fills bytes 1024 i + 16 l of the group's buffer, from
+    // = pw; lane l fills bytes 1024 i + 16 l of the group's buffer, from
     // src + stage · step. (A pad chunk of an activation row brings the row's
     // last chunk again.)
-    constexpr uint32_t WAVES = MX_THREADS / 64u;
-    constexpr uint32_t WJ = (M::W_LOADS + WAVES - 1u) / WAVES, AJ = (M::A_LOADS + WAVES - 1u) / WAVES;
+    constexpr uint32_t PW = MX_THREADS / 64u - MX_COMPUTE;
+    constexpr uint32_t WJ = (M::W_LOADS + PW - 1u) / PW, AJ = (M::A_LOADS + PW - 1u) / PW;
     const uint8_t* wsrc[WJ];
     uint32_t wstep[WJ], wcount = 0;
 #pragma unroll
     for (uint32_t j = 0; j < WJ; ++j) {
-        const uint32_t i = wave + WAVES * j, at = 1024u * i + 16u * lane;
+        const uint32_t i = pw + PW * j, at = 1024u * i + 16u * lane;
         wsrc[j] = w, wstep[j] = 0;
-        if (i >= M::W_LOADS) continue;
+        if (!producer || i >= M::W_LOADS) continue;
         ++wcount;
         if (at < M::W_S) {
             const uint32_t p = at / 16u, row = p / M::RC, chunk = p % M::RC;
@@ -1843,28 +1846,28 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1
         }
     }
     const uint8_t* asrc[AJ];
-    const uint32_t afirst = (wave + WAVES - M::W_LOADS % WAVES) % WAVES;
+    const uint32_t afirst = (pw + PW - M::W_LOADS % PW) % PW;
     uint32_t acount = 0;
 #pragma unroll
     for (uint32_t j = 0; j < AJ; ++j) {
-        const uint32_t i = afirst + WAVES * j;
+        const uint32_t i = afirst + PW * j;
         asrc[j] = (const uint8_t*)act.qs;
-        if (i >= M::A_LOADS) continue;
+        if (!producer || i >= M::A_LOADS) continue;
         ++acount;
         const uint32_t p = 64u * i + lane, row = p / 17u, chunk = min(p % 17u, 15u);
         asrc[j] = (const uint8_t*)act.qs + (size_t)min(m0 + row, m - 1u) * k + 16u * chunk;
     }
     auto issue_w = [&](uint32_t s) {
-        const uint32_t to = lds_address(lds + M::RW + (s % 3u) * M::W_BYTES) + wave * 1024u;
+        const uint32_t to = lds_address(lds + M::RW + (s % 3u) * M::W_BYTES) + pw * 1024u;
 #pragma unroll
         for (uint32_t j = 0; j < WJ; ++j)
-            if (wave + WAVES * j < M::W_LOADS) lds_load16(wsrc[j] + (size_t)s * wstep[j], to + j * (WAVES * 1024u));
+            if (pw + PW * j < M::W_LOADS) lds_load16(wsrc[j] + (size_t)s * wstep[j], to + j * (PW * 1024u));
     };
     auto issue_a = [&](uint32_t s) {
         const uint32_t to = lds_address(lds + M::RA + (s % 3u) * M::A_BYTES) + afirst * 1024u;
 #pragma unroll
         for (uint32_t j = 0; j < AJ; ++j)
-            if (afirst + WAVES * j < M::A_LOADS) lds_load16(asrc[j] + (size_t)s * 256u, to + j * (WAVES * 1024u));
+            if (afirst + PW * j < M::A_LOADS) lds_load16(asrc[j] + (size_t)s * 256u, to + j * (PW * 1024u));
     };
     auto barrier = [&](uint32_t outstanding) {
         asm volatile("" ::: "memory");
@@ -1879,56 +1882,62 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1
 
     // Weights of stages 0-2 and activations of 0-1 in flight; stage 0
     // repacked.
-    issue_w(0);
-    issue_a(0);
-    if (stages > 1u) issue_w(1), issue_a(1);
-    if (stages > 2u) issue_w(2);
+    if (producer) {
+        issue_w(0);
+        issue_a(0);
+        if (stages > 1u) issue_w(1), issue_a(1);
+        if (stages > 2u) issue_w(2);
+    }
     barrier((stages > 1u ? acount : 0u) + (stages > 2u ? wcount : 0u));
-    mx_repack<KIND>(lds + M::RW, lds + M::PK, t);
+    if (producer) mx_repack<KIND>(lds + M::RW, lds + M::PK, pt);
     barrier(63);
 
     const long one = half == 0 ? 0x3c00l : 0l;  // the f16 operand (1, 0, 0, 0) for lanes 0-31
     for (uint32_t s = 0; s < stages; ++s) {
-        if (s + 3u < stages) issue_w(s + 3u);
-        if (s + 2u < stages) issue_a(s + 2u);
-        const uint8_t* pk = lds + M::PK + (s & 1u) * M::P_BYTES;
-        MxBase B;
-        B.a = lds + M::RA + (s % 3u) * M::A_BYTES + (mw + l32) * MX_ROW + 16u * half;
-        B.w = pk + (nw + l32) * MX_ROW + 16u * half;
-        const uint32_t wcol = half == 0 ? (nw + l32) * 8u : MX_TILE * 8u;  // the zero entry for lanes 32-63
-        const uint32_t arow = half == 0 ? (mw + l32) * 8u : MX_TILE * 8u;
-        B.d = pk + M::P_D + wcol;
-        B.s = pk + M::P_S + arow;
-        B.m = pk + M::P_M + wcol;
-        B.e = pk + M::P_E + arow;
-        // The stage's operand reads go out together, then the repack of
-        // stage s + 1 (its LDS traffic and VALU work overlap their latency),
-        // then the blocks: the MFMAs of block b + 1 before the additions of
-        // block b.
-        MxOps ops[MX_STAGE];
+        if (producer) {
+            // The loads of stage s + 3 (weights) and s + 2 (activations),
+            // and the repack of stage s + 1.
+            if (s + 3u < stages) issue_w(s + 3u);
+            if (s + 2u < stages) issue_a(s + 2u);
+            if (s + 1u < stages)
+                mx_repack<KIND>(lds + M::RW + ((s + 1u) % 3u) * M::W_BYTES,
+                                lds + M::PK + ((s + 1u) & 1u) * M::P_BYTES, pt);
+        } else {
+            const uint8_t* pk = lds + M::PK + (s & 1u) * M::P_BYTES;
+            MxBase B;
+            B.a = lds + M::RA + (s % 3u) * M::A_BYTES + (mw + l32) * MX_ROW + 16u * half;
+            B.w = pk + (nw + l32) * MX_ROW + 16u * half;
+            const uint32_t wcol = half == 0 ? (nw + l32) * 8u : MX_TILE * 8u;  // the zero entry for lanes 32-63
+            const uint32_t arow = half == 0 ? (mw + l32) * 8u : MX_TILE * 8u;
+            B.d = pk + M::P_D + wcol;
+            B.s = pk + M::P_S + arow;
+            B.m = pk + M::P_M + wcol;
+            B.e = pk + M::P_E + arow;
+            // The stage's operand reads go out together, then the blocks:
+            // the MFMAs of block b + 1 before the additions of block b.
+            MxOps ops[MX_STAGE];
 #pragma unroll
-        for (uint32_t b = 0; b < MX_STAGE; ++b) mx_operands<KIND>(ops[b], B, b);
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 1u < stages)
-            mx_repack<KIND>(lds + M::RW + ((s + 1u) % 3u) * M::W_BYTES, lds + M::PK + ((s + 1u) & 1u) * M::P_BYTES, t);
-        MxBlock cur, nxt;
-        mx_block<KIND>(cur, ops[0], one);
+            for (uint32_t b = 0; b < MX_STAGE; ++b) mx_operands<KIND>(ops[b], B, b);
+            MxBlock cur, nxt;
+            mx_block<KIND>(cur, ops[0], one);
 #pragma unroll
-        for (uint32_t b = 0; b < MX_STAGE; ++b) {
-            if (b + 1u < MX_STAGE) mx_block<KIND>(nxt, ops[b + 1u], one);
-            mx_add<KIND, FUSED>(acc, cur);
-            cur = nxt;
+            for (uint32_t b = 0; b < MX_STAGE; ++b) {
+                if (b + 1u < MX_STAGE) mx_block<KIND>(nxt, ops[b + 1u], one);
+                mx_add<KIND, FUSED>(acc, cur);
+                cur = nxt;
+            }
+            // The stage's sums are complete before the barrier: the
+            // compiler would otherwise move the additions after it.
+#pragma unroll
+            for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(acc[i]));
         }
-        // The stage's sums are complete before the barrier: the compiler
-        // would otherwise move the additions after it.
-#pragma unroll
-        for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(acc[i]));
         // Weights of stage s + 2 and activations of s + 1 have landed (the
         // loads issued above stay in flight); every wave is done with this
         // stage's buffers.
         if (s + 1u < stages) barrier((s + 3u < stages ? wcount : 0u) + (s + 2u < stages ? acount : 0u));
     }
 
+    if (producer) return;
     const uint32_t col = n0 + nw + l32;
     const float b = (bias && col < n) ? bias[col] : 0.0f;
 #pragma unroll
