@@ -1947,6 +1947,268 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 }
 
+// ------------------------------------ matrix cores: a few activation rows
+
+// x · wᵀ for up to 16 activation rows (batched decode) on the int8 matrix
+// cores, k a multiple of 512, weights and activation parts 16-byte aligned.
+// Workgroup: 16 outputs (weight rows) for all rows over the whole of k, 8
+// waves; the weights are read from HBM once whatever the row count (the
+// lanes kernels read them once per group of 8 rows and take ~13 VALU
+// operations a row and block for the dot products).
+//
+// The k axis goes in stages of 16 blocks through a ring of DEPTH LDS
+// buffers, the loads of stages s + 1 .. s + DEPTH - 1 in flight while stage
+// s is computed, one workgroup barrier a stage; all of it by direct loads
+// (raw weight rows, the activation rows 528 bytes apart, their scales and
+// extras). In a stage, wave v issues the v_mfma_i32_16x16x32_i8 of blocks
+// 2v and 2v + 1 (the 16 x 16 tile of rows x outputs of one block; operands
+// read where the blocks lie: Q8_0 values
+// funnel-shifted in even blocks, Q4 nibbles unpacked a dword at a time with
+// the activations taken in the same order; Q4_0's -8·Σq as the MFMA's C),
+// forms each output's contribution of the block in the host's expression
+// (Q8_0 float(t)·(d·sx); Q4_0 (float(t)·d)·sx; Q4_1 (d·sx)·float(t) + m·mx,
+// each operation rounded as the host rounds it) and writes it to LDS by
+// block, row and output. In the next stage each of the first 256 threads
+// adds one output's contributions (row t / 16, output t % 16) in block
+// order: the ordered fold is spread one output a lane over the workgroup.
+
+// The B operand (8 int8 values) of a lane for block b of a stage, from the
+// stage's raw weight row at `row` (LDS); q is the lane's k quarter.
+//   Q8_0  the lane's 8 bytes 2 + 8 q .. of the block's 34: dword-aligned in
+//         odd blocks, two bytes off in even ones (funnel shifts);
+//   Q4_x  one dword of nibbles, bytes 4 q .. 4 q + 3 of the 16: its low
+//         nibbles are values 4 q .., its high ones 16 + 4 q .. (few_acts
+//         takes the activations in the same order).
+template <int KIND>
+__device__ __forceinline__ long few_weights(const uint8_t* row, uint32_t b, uint32_t q) {
+    if constexpr (KIND == 0) {
+        if (b % 2u == 0) {
+            const uint32_t* p = (const uint32_t*)(row + 34u * b + 8u * q);
+            const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+            return (long)funnel(d1, d0, 2) | ((long)funnel(d2, d1, 2) << 32);
+        }
+        const uint32_t* p = (const uint32_t*)(row + 34u * b + 2u + 8u * q);
+        return (long)p[0] | ((long)p[1] << 32);
+    } else {
+        uint32_t v;
+        if constexpr (KIND == 1) {
+            if (b % 2u == 0) {
+                const uint32_t* p = (const uint32_t*)(row + 18u * b + 4u * q);
+                v = funnel(p[1], p[0], 2);
+            } else {
+                v = *(const uint32_t*)(row + 18u * b + 2u + 4u * q);
+            }
+        } else {
+            v = *(const uint32_t*)(row + 20u * b + 4u + 4u * q);
+        }
+        return (long)(v & 0x0f0f0f0fu) | ((long)((v >> 4) & 0x0f0f0f0fu) << 32);
+    }
+}
+
+// The A operand of block b from the stage's activation row at `row` (LDS):
+// the 8 values few_weights pairs with.
+template <int KIND>
+__device__ __forceinline__ long few_acts(const uint8_t* row, uint32_t b, uint32_t q) {
+    if constexpr (KIND == 0) {
+        return *(const long*)(row + 32u * b + 8u * q);
+    } else {
+        const uint32_t* p = (const uint32_t*)(row + 32u * b);
+        return (long)p[q] | ((long)p[4u + q] << 32);
+    }
+}
+
+constexpr uint32_t FEW_ROWS = 16;
+constexpr uint32_t FEW_COLS = 16;
+constexpr uint32_t FEW_STAGE = 16;  // blocks a stage at least (k a multiple of 512)
+constexpr uint32_t FEW_THREADS = 512;
+constexpr uint32_t FEW_WAVES = FEW_THREADS / 64u;
+
+// Stages of SB blocks through a ring of DEPTH buffers.
+template <int KIND, uint32_t DEPTH, uint32_t SB>
+struct Few {
+    static constexpr uint32_t PER = SB / FEW_WAVES;      // blocks of a stage a wave takes
+    static constexpr uint32_t AROW = SB * 32u + 16u;     // LDS bytes per activation row: values + a 16-byte pad
+    static constexpr uint32_t ACH = AROW / 16u;          // its 16-byte pieces
+    static constexpr uint32_t BB = Fmt<KIND>::BB;
+    static constexpr uint32_t RB = SB * BB;  // a weight row's bytes in a stage
+    static constexpr uint32_t RC = RB / 16u;
+    static constexpr uint32_t KB1 = 1024u;
+    static constexpr uint32_t W_BYTES = (FEW_COLS * RB + KB1 - 1u) / KB1 * KB1;  // whole 1 KB wave loads
+    static constexpr uint32_t A_CHUNKS = FEW_ROWS * ACH;
+    static constexpr uint32_t A_BYTES = (FEW_ROWS * AROW + KB1 - 1u) / KB1 * KB1;
+    static constexpr uint32_t S_BYTES = FEW_ROWS * SB * 4u;  // scales [row][SB]
+    static constexpr uint32_t E_BYTES = KIND == 0 ? 0u : S_BYTES;  // Q4_0 Σq, Q4_1 sums
+    // a raw stage: weights, activations, scales, extras
+    static constexpr uint32_t R_A = W_BYTES, R_S = R_A + A_BYTES, R_E = R_S + S_BYTES, R_BYTES = R_E + E_BYTES;
+    static constexpr uint32_t LOADS = R_BYTES / KB1;
+    // a stage's contributions [block][row][output], f32
+    static constexpr uint32_t P_BYTES = SB * FEW_ROWS * FEW_COLS * 4u;
+    static constexpr uint32_t NBUF = DEPTH;
+    static constexpr uint32_t RAW = 0, PK = NBUF * R_BYTES, LDS = PK + 2u * P_BYTES;
+    static_assert(NBUF >= 3u, "a ring of three stages at least");
+    static_assert(R_BYTES % KB1 == 0, "whole wave loads");
+    static_assert(LDS <= 160u * 1024u, "one workgroup's LDS");
+};
+
+template <int KIND, uint32_t DEPTH, uint32_t SB>
+__global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __restrict__ w, Activations act,
+                                                            float* __restrict__ dst, const float* __restrict__ bias,
+                                                            uint32_t bias_ld, uint32_t rows, uint32_t n, uint32_t k) {
+    using F = Few<KIND, DEPTH, SB>;
+    constexpr uint32_t PER = F::PER;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[F::LDS];
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t lr = lane & 15u, lq = lane >> 4;
+    const uint32_t nb = k >> 5, stages = nb / SB;
+    const uint32_t n0 = blockIdx.x * FEW_COLS;
+    const size_t row_bytes = (size_t)nb * F::BB;
+
+    // This wave's direct loads of a stage: instructions i = wave + 4 j below
+    // LOADS; lane l fills bytes 1024 i + 16 l of the stage's buffer, from
+    // src + stage · step. (Lanes past a part's data bring a piece of it
+    // again, into the part's padding.)
+    constexpr uint32_t J = (F::LOADS + FEW_WAVES - 1u) / FEW_WAVES;
+    const uint8_t* src[J];
+    uint32_t step[J], mine = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) {
+        const uint32_t i = wave + FEW_WAVES * j, at = 1024u * i + 16u * lane;
+        src[j] = w, step[j] = 0;
+        if (i >= F::LOADS) continue;
+        ++mine;
+        if (at < F::R_A) {
+            const uint32_t p = min(at / 16u, FEW_COLS * F::RC - 1u), col = p / F::RC, chunk = p % F::RC;
+            src[j] = w + (size_t)min(n0 + col, n - 1u) * row_bytes + 16u * chunk;
+            step[j] = F::RB;
+        } else if (at < F::R_S) {
+            const uint32_t p = min((at - F::R_A) / 16u, F::A_CHUNKS - 1u), row = p / F::ACH;
+            const uint32_t chunk = min(p % F::ACH, F::ACH - 2u);
+            src[j] = (const uint8_t*)act.qs + (size_t)min(row, rows - 1u) * k + 16u * chunk;
+            step[j] = SB * 32u;
+        } else {
+            const bool ex = at >= F::R_E;
+            const uint32_t p = (at - (ex ? F::R_E : F::R_S)) / 16u, row = p / (SB / 4u);
+            const void* from = !ex ? (const void*)act.scales
+                                   : (KIND == 1 ? (const void*)act.totals : (const void*)act.sums);
+            src[j] = (const uint8_t*)from + ((size_t)min(row, rows - 1u) * nb + 4u * (p % (SB / 4u))) * 4u;
+            step[j] = SB * 4u;
+        }
+    }
+    auto issue = [&](uint32_t s) {
+        const uint32_t to = lds_address(lds + F::RAW + (s % F::NBUF) * F::R_BYTES) + wave * 1024u;
+#pragma unroll
+        for (uint32_t j = 0; j < J; ++j)
+            if (wave + FEW_WAVES * j < F::LOADS) lds_load16(src[j] + (size_t)s * step[j], to + j * (FEW_WAVES * 1024u));
+    };
+    auto barrier = [&](uint32_t outstanding) {
+        asm volatile("" ::: "memory");
+        wait_vm_lds_upto<32>(outstanding);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // Stages 0 .. NBUF - 2 in flight; wait for stage 0.
+    const uint32_t ahead = min(stages, F::NBUF - 1u);
+    for (uint32_t s = 0; s < ahead; ++s) issue(s);
+    barrier((ahead - 1u) * mine);
+
+    const uint32_t fr = t >> 4, fc = t & 15u;  // the output this thread adds up
+    float acc = 0.0f;
+    for (uint32_t s = 0; s <= stages; ++s) {
+        if (s + F::NBUF - 1u < stages) issue(s + F::NBUF - 1u);
+        if (s < stages) {
+            // This wave's blocks of stage s (2v, 2v + 1): their
+            // contributions, written as the MFMA result lies (block, lane,
+            // the lane's 4 rows), one 16-byte write a block.
+            const uint8_t* raw = lds + F::RAW + (s % F::NBUF) * F::R_BYTES;
+            uint8_t* pk = lds + F::PK + (s & 1u) * F::P_BYTES;
+            const uint8_t* wrow = raw + lr * F::RB;
+            const uint8_t* arow = raw + F::R_A + lr * F::AROW;
+            // the lane's 4 rows' scales (and extras) of the wave's blocks
+            float sxv[4][PER], exv[4][PER];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (uint32_t u = 0; u < PER; u += 2u) {
+                    const uint32_t at = ((4u * lq + i) * SB + PER * wave + u) * 4u;
+                    const float2 x = *(const float2*)(raw + F::R_S + at);
+                    sxv[i][u] = x.x, sxv[i][u + 1u] = x.y;
+                    if constexpr (KIND != 0) {
+                        const float2 e = *(const float2*)(raw + F::R_E + at);
+                        exv[i][u] = e.x, exv[i][u + 1u] = e.y;
+                    }
+                }
+            // Every read of the wave's blocks first (the LDS writes below would
+            // otherwise hold each block's reads behind the previous block's
+            // write), then the MFMAs, then the contributions and writes.
+            long av[PER], bv[PER];
+            uint32_t dm[PER];
+#pragma unroll
+            for (uint32_t u = 0; u < PER; ++u) {
+                const uint32_t b = PER * wave + u;
+                av[u] = few_acts<KIND>(arow, b, lq);
+                bv[u] = few_weights<KIND>(wrow, b, lq);
+                if constexpr (KIND == 2) dm[u] = *(const uint32_t*)(wrow + 20u * b);
+                else dm[u] = *(const uint16_t*)(wrow + F::BB * b);
+            }
+            v4i tv[PER];
+#pragma unroll
+            for (uint32_t u = 0; u < PER; ++u) {
+                v4i c = {0, 0, 0, 0};
+                if constexpr (KIND == 1) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) c[i] = -8 * __float_as_int(exv[i][u]);
+                }
+                tv[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u], c, 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < PER; ++u) {
+                const uint32_t b = PER * wave + u;
+                const float d = half_value(dm[u] & 0xffffu);
+                const float m = KIND == 2 ? half_value(dm[u] >> 16) : 0.0f;
+                float cv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float x = sxv[i][u], ft = (float)tv[u][i];
+                    if constexpr (KIND == 0) {
+                        const float sc = d * x;
+                        cv[i] = ft * sc;
+                    } else if constexpr (KIND == 1) {
+                        const float p = ft * d;
+                        cv[i] = p * x;
+                    } else {
+                        const float sc = d * x;
+                        const float f = sc * ft;
+                        const float g = m * exv[i][u];
+                        cv[i] = f + g;
+                    }
+                }
+                *(float4*)(pk + (b * 64u + lane) * 16u) = make_float4(cv[0], cv[1], cv[2], cv[3]);
+            }
+        }
+        if (s > 0 && t < FEW_ROWS * FEW_COLS) {
+            // Stage s - 1's contributions to this thread's output, in block
+            // order: output (row r, column c) is element r % 4 of lane
+            // c + 16 (r / 4).
+            const float* ct = (const float*)(lds + F::PK + ((s - 1u) & 1u) * F::P_BYTES) +
+                              (fc + 16u * (fr >> 2)) * 4u + (fr & 3u);
+#pragma unroll
+            for (uint32_t b = 0; b < SB; ++b) acc += ct[b * 256u];
+        }
+        // Stage s + 1 has landed (the loads of later stages stay in
+        // flight); the contributions written above are complete, and the
+        // ones read are done.
+        if (s < stages) barrier(min(stages - 1u - min(s + 1u, stages - 1u), F::NBUF - 2u) * mine);
+    }
+    const uint32_t col = n0 + fc;
+    if (t < FEW_ROWS * FEW_COLS && fr < rows && col < n) {
+        float v = acc;
+        if (bias) v = v + bias[(size_t)fr * bias_ld + col];
+        dst[(size_t)fr * n + col] = v;
+    }
+}
+
 // ------------------------------------------------- thread per output
 
 // One thread per output, adding its blocks in order from byte loads: any
@@ -2469,6 +2731,44 @@ static hipError_t launch_mx(bool fused, const uint8_t* w, Activations act, float
 // Activation rows from which AUTO takes the matrix cores rather than lanes.
 static constexpr uint32_t MATRIX_ROWS = 32;
 
+// AUTO takes the few-rows kernel from 9 rows to 16, where the lanes kernels
+// would read the weights twice (measured on config 3's shapes: at 8 rows the
+// lanes kernel is as fast or faster, at 16 the few-rows one is 1.2-1.8x).
+static constexpr uint32_t FEW_MIN_ROWS = 9;
+
+// The few-rows kernel: up to 16 rows, whole stages of 16 blocks, 16-byte
+// aligned weights and activation parts (its direct loads).
+static bool few_fits(const uint8_t* w, const Activations& act, uint32_t kind, uint32_t rows, uint32_t k) {
+    const uint32_t nb = k >> 5;
+    const uintptr_t extra = kind == 1 ? (uintptr_t)act.totals : kind == 2 ? (uintptr_t)act.sums : 0;
+    return rows >= FEW_MIN_ROWS && rows <= FEW_ROWS && k % 32u == 0 && nb >= FEW_STAGE && nb % FEW_STAGE == 0 &&
+           (((uintptr_t)w | (uintptr_t)act.qs | (uintptr_t)act.scales | extra) % 16u) == 0;
+}
+
+// A ring of 3 stage buffers leaves LDS for two workgroups a compute unit
+// (wide products: more than 256 workgroups); narrow ones take a ring of 6.
+template <int KIND>
+static hipError_t launch_few(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t bias_ld,
+                             uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
+    const uint32_t grid = (n + FEW_COLS - 1u) / FEW_COLS;
+    if (grid > 256u)
+        hipLaunchKernelGGL((k_matmul_few<KIND, 3, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                           bias_ld, rows, n, k);
+    else
+        hipLaunchKernelGGL((k_matmul_few<KIND, 6, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                           bias_ld, rows, n, k);
+    return hipGetLastError();
+}
+
+static hipError_t launch_few_kind(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* bias,
+                                  uint32_t bias_ld, uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
+    switch (kind) {
+    case 0: return launch_few<0>(w, act, dst, bias, bias_ld, rows, n, k, stream);
+    case 1: return launch_few<1>(w, act, dst, bias, bias_ld, rows, n, k, stream);
+    default: return launch_few<2>(w, act, dst, bias, bias_ld, rows, n, k, stream);
+    }
+}
+
 hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, Activations act, float* dst,
                                const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
                                hipStream_t stream) {
@@ -2483,6 +2783,8 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
         default: return launch_mx<2>(fused, w, act, dst, bias, rows, n, k, stream);
         }
     }
+    if (mode == 0u /* AUTO */ && few_fits(w, act, kind, rows, k))
+        return launch_few_kind(kind, w, act, dst, bias, 0, rows, n, k, stream);
     if (matrix) {
         switch (kind) {
         case 0: return launch_mfma<0>(w, act, dst, bias, rows, n, k, stream);
@@ -2508,6 +2810,7 @@ hipError_t launch_product_residual(uint32_t kind, const uint8_t* w, Activations 
                                   uint32_t rows, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
     if (!lanes_fit(w, k) || rows >= MATRIX_ROWS) return hipErrorInvalidValue;
+    if (few_fits(w, act, kind, rows, k)) return launch_few_kind(kind, w, act, dst, residual, n, rows, n, k, stream);
     switch (kind) {
     case 0: return launch_lanes<0>(w, act, dst, residual, rows, n, k, compute_units, stream, n);
     case 1: return launch_lanes<1>(w, act, dst, residual, rows, n, k, compute_units, stream, n);

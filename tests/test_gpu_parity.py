@@ -558,6 +558,28 @@ def test_matrix_cores_bit_exact(dev, fmt, shape):
         assert np.array_equal(bits(got), bits(want)), mode
 
 
+FEW_SHAPES = [
+    # (rows, n, k): AUTO takes the few-rows matrix-core kernel for 9-16 rows
+    # where k is a multiple of 512: ragged outputs, config 3's two shapes at
+    # B = 16, one row short of a tile
+    (9, 100, 512), (12, 37, 1024), (10, 2048, 1024), (15, 130, 512), (16, 8192, 2048), (16, 2048, 8192),
+]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("shape", FEW_SHAPES)
+def test_few_rows_bit_exact(dev, fmt, shape):
+    rows, n, k = shape
+    say("few rows", fmt, rows, n, k)
+    rng = np.random.default_rng(930 + rows)
+    wq = weights(fmt, n, k, 931 + n)
+    x = acts(rows, k, 932 + rows)
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    want = oracle.add_bias(oracle.matmul(fmt, x, wq, rows, n, k), bias)
+    got = run_product(dev, fmt, wq, x, rows, n, k, mode="auto", bias=bias)
+    assert np.array_equal(bits(got), bits(want))
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_matrix_cores_subnormal_scales(dev, fmt):
     # Weights and activations small enough that the block scales d, the
