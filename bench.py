@@ -31,6 +31,7 @@ Beside it, in the same line:
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-decode]
     python bench.py --batched     # config 3, its own line
     python bench.py --gemm        # config 4, its own line
+    python bench.py --decode-only # config 5, its own line
     python bench.py --write-gguf DIR   # the configs' weights as GGUF files
 """
 from __future__ import annotations
@@ -648,6 +649,8 @@ def main():
     ap.add_argument("--gemm", action="store_true",
                     help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
     ap.add_argument("--gemm-mode", default="auto", help="config 4's BlockMatMulMode (auto, matrix, unordered)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="config 5 only (decode at batch 1 and 8); its own JSON line")
     ap.add_argument("--decode-eager", action="store_true",
                     help="launch decode steps one kernel at a time, not from a captured graph (for kernel tracers)")
     ap.add_argument("--write-gguf", metavar="DIR",
@@ -674,6 +677,10 @@ def main():
         return
     if args.batched:
         print(json.dumps(batched_config3(dev, args.steps, args.warmup)), flush=True)
+        return
+    if args.decode_only:
+        print(json.dumps(decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
+                                     graph=not args.decode_eager)), flush=True)
         return
     result = config2(dev, args)
     if not args.no_config1:
