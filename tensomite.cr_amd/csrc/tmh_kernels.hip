@@ -2880,8 +2880,9 @@ hipError_t launch_gate_up_swiglu(uint32_t kind, const uint8_t* w, Activations ac
 
 // ----------------------------------------- one row, weights in LDS: launchers
 
-// LDS a k_matvec_one workgroup may take: one a compute unit.
-static constexpr size_t ONE_LDS_LIMIT = 150u * 1024u;
+// LDS a k_matvec_one workgroup may take: one a compute unit (160 KB on
+// gfx950, less 2 KB for the kernel's own LDS).
+static constexpr size_t ONE_LDS_LIMIT = 158u * 1024u;
 
 // Rows of whole pairs per pass, and rows of whole 16-byte pieces starting
 // 16-byte aligned (the direct loads take 16 bytes a lane).
@@ -2891,13 +2892,17 @@ static bool one_fits(uint32_t kind, const uint8_t* w, uint32_t k) {
            ((uintptr_t)w & 15u) == 0;
 }
 
-// Rows a workgroup: about one workgroup a compute unit, within the LDS limit.
+// Rows a workgroup: about one workgroup a compute unit, within the LDS limit;
+// when the rows take more than one round of workgroups, rounds of equal
+// tiles (a last round of a few workgroups would take as long as a full one).
 static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units) {
     const uint32_t nb = k >> 5, rb = nb * block_bytes(kind), stride = lanes_stride(nb);
     const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
     uint32_t tr = std::max(1u, (n + cus - 1u) / cus);
     while (tr > 1 && one_lds(k, tr, rb, stride, norm, false).end > ONE_LDS_LIMIT) --tr;
-    return tr;
+    const uint64_t per_round = (uint64_t)cus * tr;
+    const uint64_t rounds = (n + per_round - 1u) / per_round;
+    return std::max(1u, (uint32_t)((n + cus * rounds - 1u) / (cus * rounds)));
 }
 
 template <int KIND, bool NORM>
