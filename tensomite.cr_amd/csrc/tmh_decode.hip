@@ -709,12 +709,18 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
             float dot = 0.0f;
             if (width == 64u) {
                 // q in registers; a position's 64 keys lie in one 1 KB piece
-                // (four rows a piece), read at immediate offsets
+                // (four rows a piece), read at immediate offsets, all before
+                // the first add (one LDS round trip, then a chain of adds)
                 const float4* k4 = reinterpret_cast<const float4*>(l.kt + (pl >> 2) * 260u + (pl & 3u) * 64u);
+                float4 kr[16];
+#pragma unroll
+                for (uint32_t c4 = 0; c4 < 16u; ++c4) kr[c4] = k4[c4];
+#pragma unroll
+                for (uint32_t c4 = 0; c4 < 16u; ++c4) asm volatile("" : "+v"(kr[c4].x), "+v"(kr[c4].y), "+v"(kr[c4].z), "+v"(kr[c4].w));
 #pragma unroll
                 for (uint32_t c4 = 0; c4 < 16u; ++c4) {
                     const float4 q = qr[c4];
-                    const float4 k = k4[c4];
+                    const float4 k = kr[c4];
                     dot += q.x * k.x;
                     dot += q.y * k.y;
                     dot += q.z * k.z;
@@ -738,26 +744,90 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
             top = x > top ? x : top;
         }
     }
+    // Width 64, chunks of 256 positions, the current position last: the
+    // values of the first chunk's positions but the current one are folded
+    // from registers, 64 positions a wave (wave w: positions 64w ... 64w +
+    // 63, lane c: column c), read from LDS while the softmax runs (waves
+    // 1-3 while wave 0 takes the total). Rows from nreg on are zeroed first
+    // (and their weights below), so each of them adds +0.0, which leaves a
+    // running sum from +0.0 unchanged.
+    const bool regs = width == 64u && cp == 256u && cur == (int32_t)n - 1;
+    const uint32_t nreg = regs ? (n <= cp ? n - 1u : cp) : 0u;
+    float vreg[64];
+    auto preload = [&]() {
+        const uint32_t lane = tid & 63u, q0 = wave * 64u;
+#pragma unroll
+        for (uint32_t i = 0; i < 64u; ++i) vreg[i] = l.vrows[(q0 + i) * 64u + lane];
+    };
+    if (regs) wait_vm_lds<0>();  // this wave's loads of the first value chunk
     top = wave_top(top);
     if ((tid & 63u) == 0) tops[tid >> 6] = top;
-    lds_sync();
+    lds_sync();  // (and every wave's values are in)
     top = tops[0];
 #pragma unroll
     for (int i = 1; i < 4; ++i) top = tops[i] > top ? tops[i] : top;
     if (l.sc[0] != l.sc[0]) top = l.sc[0];  // the host's top is a NaN at position 0
+    if (regs)
+        for (uint32_t i = nreg * 64u + tid; i < cp * 64u; i += 256u) l.vrows[i] = 0.0f;
     for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = maths_exp(l.sc[p] - top);
     lds_sync();
     if (tid < 64u) {
         const float sum = n <= WAVE_SUM_MAX ? ordered_sum_by_wave(l.sc, n) : ordered_sum(l.sc, n);
         if (tid == 0) total_slot = sum;
+    } else if (regs) {
+        preload();
     }
     lds_sync();
     const float total = total_slot;
     for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = l.sc[p] / total;
+    if (regs) {
+        // past the last position (capacity ≥ cp), by the thread whose wave
+        // reads the weight below, as the divisions above are for p < 256
+        if (tid >= n) l.sc[tid] = 0.0f;
+        if (wave == 0) preload();
+    }
 
     // Σ_p weight_p · v_p[c] in position order, one lane per column.
     float acc = 0.0f;
-    for (uint32_t p0 = 0; p0 < n; p0 += cp) {
+    uint32_t from = 0;  // the first position the chunk loop folds
+    if (regs) {
+        // Every wave its 64 products (each rounded once) together, from
+        // weights that its own threads wrote (LDS operations of a wave take
+        // effect in order, so no barrier is needed); then wave after wave
+        // adds its products in order to the running sums it receives
+        // through l.out, a chain of adds from registers.
+        const uint32_t lane = tid & 63u, q0 = wave * 64u;
+        float pr[64];
+#pragma unroll
+        for (uint32_t i = 0; i < 64u; i += 4u) {
+            const float4 w4 = *reinterpret_cast<const float4*>(l.sc + q0 + i);
+            pr[i] = w4.x * vreg[i];
+            pr[i + 1u] = w4.y * vreg[i + 1u];
+            pr[i + 2u] = w4.z * vreg[i + 2u];
+            pr[i + 3u] = w4.w * vreg[i + 3u];
+        }
+        for (uint32_t v = 0; v < 4u; ++v) {
+            if (wave == v) {
+                float a = v == 0 ? 0.0f : l.out[lane];
+                if (q0 < nreg) {
+#pragma unroll
+                    for (uint32_t i = 0; i < 64u; ++i) a += pr[i];
+                }
+                l.out[lane] = a;
+            }
+            lds_sync();
+        }
+        if (tid < 64u) {
+            acc = l.out[tid];
+            // the current position last, from LDS (not yet in the cache)
+            if (n <= cp) {
+                const float prod = l.sc[n - 1u] * l.vcur[tid];
+                acc += prod;
+            }
+        }
+        from = n <= cp ? n : cp;
+    }
+    for (uint32_t p0 = from; p0 < n; p0 += cp) {
         const uint32_t cnt = min(cp, n - p0);
         if (p0 > 0) {
             lds_sync();  // the last chunk's values are read
@@ -781,7 +851,8 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     lds_sync();
 }
 
-__global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite r) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attention_decode(Attention a,
+                                                                                                       RopeWrite r) {
     extern __shared__ float4 lds4[];
     const AttDecodeLds l = att_decode_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -463,9 +463,9 @@ __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_
 
 // One activation row times a tile of `tr` weight rows per workgroup, the
 // tile's weight bytes (contiguous rows; GLU: its gate rows and its up rows)
-// brought into LDS by direct loads that waves 1..7 issue at the start,
-// while wave 0 loads the activations alone, so its wait for them never
-// waits for weights:
+// brought into LDS by direct loads that waves 1..7 (NORM: 2..7) issue at
+// the start, while wave 0 loads the activations alone (NORM: x, wave 1 the
+// norm's weights), so its wait for them never waits for weights:
 //   NORM: x is the f32 row, taken through Op::RMSNorm (host.cr:374-386;
 //     weights nw, eps) and the activation quantiser -- the squares' sum in
 //     index order by speculation across wave 0, root = sqrtf(Σ/k + eps),
@@ -495,12 +495,14 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU);
     const uint32_t lbase = lds_address(base);
 
-    // Wave 0: the activations, issued before any weight load (the compute
-    // unit's loads queue in order, so the weights would delay them). Waves
-    // 1..7: the weights.
+    // Wave 0: the activations (NORM: x, while wave 1 brings the norm's
+    // weights, so wave 0's wait before Σx² is for x alone), issued before
+    // any weight load (the compute unit's loads queue in order, so the
+    // weights would delay them). The other waves: the weights.
+    constexpr uint32_t WFIRST = NORM ? 2u : 1u;  // the first wave of the weights
     if constexpr (NORM) {
         stage_bytes<false>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u, 1u);
-        stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, 0u, 1u);
+        stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, 1u, 1u);
     } else {
         stage_bytes<false>(reinterpret_cast<const uint8_t*>(act.qs), k, lbase + L.qs, wave, 0u, 1u);
         stage_words(act.scales, nb, lbase + L.scales, wave, 0u);
@@ -509,10 +511,11 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     }
     lds_sync();
     if constexpr (GLU) {
-        stage_bytes<true>(w + (size_t)g0 * row_bytes, h * row_bytes, lbase + L.w, wave, 1u, ONE_WAVES - 1u);
-        stage_bytes<true>(w + (size_t)(H + g0) * row_bytes, h * row_bytes, lbase + L.w2, wave, 1u, ONE_WAVES - 1u);
+        stage_bytes<true>(w + (size_t)g0 * row_bytes, h * row_bytes, lbase + L.w, wave, WFIRST, ONE_WAVES - WFIRST);
+        stage_bytes<true>(w + (size_t)(H + g0) * row_bytes, h * row_bytes, lbase + L.w2, wave, WFIRST,
+                          ONE_WAVES - WFIRST);
     } else {
-        stage_bytes<true>(w + (size_t)row0 * row_bytes, rows * row_bytes, lbase + L.w, wave, 1u, ONE_WAVES - 1u);
+        stage_bytes<true>(w + (size_t)row0 * row_bytes, rows * row_bytes, lbase + L.w, wave, WFIRST, ONE_WAVES - WFIRST);
     }
 
     int8_t* aq = reinterpret_cast<int8_t*>(base + L.qs);
@@ -537,6 +540,7 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
             if (t == 0) root_slot = __builtin_sqrtf(total / (float)k + eps);
         }
     }
+    if (NORM && wave == 1) wait_vm_lds<0>();  // wave 1 issued only the norm's weights
     lds_sync();  // the activations (and the root) are in
     if constexpr (NORM) {
         const float* xs = reinterpret_cast<const float*>(base + L.x);
