@@ -768,7 +768,8 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     for (int i = 1; i < 4; ++i) top = tops[i] > top ? tops[i] : top;
     if (l.sc[0] != l.sc[0]) top = l.sc[0];  // the host's top is a NaN at position 0
     if (regs)
-        for (uint32_t i = nreg * 64u + tid; i < cp * 64u; i += 256u) l.vrows[i] = 0.0f;
+        for (uint32_t i = nreg * 16u + tid; i < cp * 16u; i += 256u)
+            reinterpret_cast<float4*>(l.vrows)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t p = tid; p < n; p += 256u) l.sc[p] = maths_exp(l.sc[p] - top);
     lds_sync();
     if (tid < 64u) {
@@ -851,8 +852,7 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
     lds_sync();
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attention_decode(Attention a,
-                                                                                                       RopeWrite r) {
+__global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite r) {
     extern __shared__ float4 lds4[];
     const AttDecodeLds l = att_decode_lds(reinterpret_cast<float*>(lds4), a.width, a.capacity);
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
