@@ -2354,16 +2354,30 @@ static constexpr size_t LANES_LDS_LIMIT = 56u * 1024u;
 // Chooses the rows per workgroup: a multiple of the rows one step covers,
 // with every output's fold on its own thread and the contributions within
 // the LDS limit, as large as still leaves about two workgroups per compute
-// unit, else the smallest.
+// unit, else the smallest. From 8 activation rows, whose reads of each
+// pair's activations the rows of a workgroup share: the tile with the
+// fewest rows on the busiest compute unit (rounds of workgroups × rows),
+// the larger on a tie.
 static uint32_t lanes_tile(uint32_t nb, uint32_t nbatch, uint32_t n, int compute_units) {
     const uint32_t np = nb / 2u;
     const uint32_t rpi = 256u / np;
     const uint32_t stride = lanes_stride(nb);
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    auto fits = [&](uint32_t tr) { return nbatch * tr <= 256u && (size_t)nbatch * tr * stride * 4u <= LANES_LDS_LIMIT; };
     uint32_t best = rpi;
-    const uint64_t want = (uint64_t)2u * (uint32_t)(compute_units > 0 ? compute_units : 256);
+    if (nbatch >= 8u) {
+        uint64_t best_cost = ~0ull;
+        for (uint32_t tr = rpi; fits(tr); tr += rpi) {
+            const uint64_t groups = (n + tr - 1u) / tr;
+            const uint64_t cost = (groups + cus - 1u) / cus * tr;
+            if (cost <= best_cost) best_cost = cost, best = tr;
+        }
+        return best;
+    }
+    const uint64_t want = (uint64_t)2u * cus;
     for (uint32_t m = 2;; ++m) {
         const uint32_t tr = rpi * m;
-        if (nbatch * tr > 256u || (size_t)nbatch * tr * stride * 4u > LANES_LDS_LIMIT) break;
+        if (!fits(tr)) break;
         if ((n + tr - 1u) / tr < want) break;
         best = tr;
     }

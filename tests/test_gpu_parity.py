@@ -84,6 +84,32 @@ def test_quantised_activations_bit_exact(dev, k):
         assert np.array_equal(g_totals[r * nb:(r + 1) * nb], q.reshape(nb, 32).astype(np.int32).sum(1)), r
 
 
+@pytest.mark.parametrize("rows,k,ldx", [(600, 2048, 2048), (333, 3200, 3200), (400, 2080, 2081)])
+def test_quantised_activations_large(dev, rows, k, ldx):
+    # Prefill-sized inputs (tens of thousands of blocks, about a thousand
+    # workgroups): the same bytes and scales as the oracle, with a ragged
+    # last workgroup (333 x 100 blocks) and unaligned rows (ldx 2081).
+    say("quantise large", rows, k, ldx)
+    x = np.zeros(rows * ldx, np.float32)
+    body = acts(rows, k, 7 + k).reshape(rows, k)
+    body[1, :32] = 0
+    body[2, 64:96] = [127.0 if j == 0 else j - 15.5 for j in range(32)]
+    x.reshape(rows, ldx)[:, :k] = body
+    xbuf = dev.from_array(x)
+    scales, sums, totals, qs = dev.quantize_rows(xbuf, rows, k, ldx)
+    nb = k // 32
+    g_scales = dev.to_array(scales, np.float32, rows * nb).reshape(rows, nb)
+    g_sums = dev.to_array(sums, np.float32, rows * nb).reshape(rows, nb)
+    g_totals = dev.to_array(totals, np.int32, rows * nb).reshape(rows, nb)
+    g_qs = dev.to_array(qs, np.int8, rows * k).reshape(rows, k)
+    for r in range(rows):
+        s, m, q = oracle.quantize_activations(body[r], with_sums=True)
+        assert np.array_equal(g_qs[r], q), r
+        assert np.array_equal(bits(g_scales[r]), bits(s)), r
+        assert np.array_equal(bits(g_sums[r]), bits(m)), r
+        assert np.array_equal(g_totals[r], q.reshape(nb, 32).astype(np.int32).sum(1)), r
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("mode", ["auto", "thread", "lanes", "unordered"])
 def test_matches_cpu_with_bias_every_mode(dev, fmt, mode):
