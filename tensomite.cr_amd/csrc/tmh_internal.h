@@ -176,6 +176,31 @@ hipError_t launch_gate_up_swiglu_rms(uint32_t kind, const uint8_t* w, const floa
                                      float eps, uint32_t rows, uint32_t H, uint32_t k, Activations glu,
                                      hipStream_t stream);
 
+// Input modes of the few-rows products with weights in LDS.
+constexpr uint32_t NB_QUANT = 0;  // rows quantised already (act, as the quantise pass lays them out)
+constexpr uint32_t NB_F32 = 1;    // f32 rows x, quantised by each workgroup
+constexpr uint32_t NB_NORM = 2;   // f32 rows x through RMSNorm (weights nw, eps), then quantised
+
+// dst[rows, n] = rows of activations times w (n rows), + bias[b · bias_ld +
+// row] as a separate rounding: groups of 8, 4 and 2 rows a launch, each
+// workgroup's weight tile direct-loaded into LDS at its start and, for
+// F32/NORM, the rows quantised (NORM: through RMSNorm first) by every
+// workgroup in its prologue; the bits of the quantise pass (or norm +
+// quantise) then the product. hipErrorInvalidValue, nothing launched, when
+// the shape is not for it (F32/NORM: k above 2048; rows of an odd number of
+// blocks; x, norm or the activations not 16-byte aligned).
+hipError_t launch_rows_product(uint32_t kind, uint32_t mode, const uint8_t* w, const float* x, uint32_t ldx,
+                               const float* nw, float eps, Activations act, float* dst, const float* bias,
+                               uint32_t bias_ld, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                               hipStream_t stream);
+
+// gate_up of rows (NORM: x through RMSNorm; QUANT: act) with SwiGLU and
+// the quantiser in the epilogue, as launch_gate_up_swiglu_rms for several
+// rows: glu receives [rows, H] quantised as the quantise pass lays them out.
+hipError_t launch_rows_gate_up(uint32_t kind, uint32_t mode, const uint8_t* w, const float* x, uint32_t ldx,
+                               const float* nw, float eps, Activations act, uint32_t rows, uint32_t H, uint32_t k,
+                               Activations glu, hipStream_t stream);
+
 // One quantised activation row times w (n rows), dst[row] = Σ (+ bias[row]):
 // the weights of each workgroup's tile direct-loaded into LDS at its start.
 // hipErrorInvalidValue when the shape is not for it.

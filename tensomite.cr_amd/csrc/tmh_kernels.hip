@@ -20,6 +20,7 @@
 #include "tmh_internal.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 namespace tmh {
 
@@ -1984,6 +1985,37 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 //         nibbles are values 4 q .., its high ones 16 + 4 q .. (few_acts
 //         takes the activations in the same order).
 template <int KIND>
+__device__ __forceinline__ long few_weights(const uint8_t* row, uint32_t b, uint32_t q);
+
+// few_weights for a block b whose parity is known where it is called (the
+// two layouts of a pair's blocks, without a branch between them).
+template <int KIND, bool ODD>
+__device__ __forceinline__ long few_weights_at(const uint8_t* row, uint32_t b, uint32_t q) {
+    if constexpr (KIND == 0) {
+        if constexpr (!ODD) {
+            const uint32_t* p = (const uint32_t*)(row + 34u * b + 8u * q);
+            const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+            return (long)funnel(d1, d0, 2) | ((long)funnel(d2, d1, 2) << 32);
+        }
+        const uint32_t* p = (const uint32_t*)(row + 34u * b + 2u + 8u * q);
+        return (long)p[0] | ((long)p[1] << 32);
+    } else {
+        uint32_t v;
+        if constexpr (KIND == 1) {
+            if constexpr (!ODD) {
+                const uint32_t* p = (const uint32_t*)(row + 18u * b + 4u * q);
+                v = funnel(p[1], p[0], 2);
+            } else {
+                v = *(const uint32_t*)(row + 18u * b + 2u + 4u * q);
+            }
+        } else {
+            v = *(const uint32_t*)(row + 20u * b + 4u + 4u * q);
+        }
+        return (long)(v & 0x0f0f0f0fu) | ((long)((v >> 4) & 0x0f0f0f0fu) << 32);
+    }
+}
+
+template <int KIND>
 __device__ __forceinline__ long few_weights(const uint8_t* row, uint32_t b, uint32_t q) {
     if constexpr (KIND == 0) {
         if (b % 2u == 0) {
@@ -2210,6 +2242,406 @@ __global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __res
         float v = acc;
         if (bias) v = v + bias[(size_t)fr * bias_ld + col];
         dst[(size_t)fr * n + col] = v;
+    }
+}
+
+// ------------------------------------------- a few rows, weights in LDS
+
+// Threads of a k_matvec_nb workgroup: 8 waves, two a SIMD.
+constexpr uint32_t NB_THREADS = 512;
+constexpr uint32_t NB_WAVES = NB_THREADS / 64u;
+// Blocks of a fold chunk: the contributions of NB_CHUNK blocks are held in
+// LDS at a time, NB_PER consecutive blocks a wave.
+constexpr uint32_t NB_CHUNK = 64;
+constexpr uint32_t NB_PER = NB_CHUNK / NB_WAVES;
+static_assert(NB_PER == 8, "a wave's blocks of a chunk: two 16-byte table reads and writes");
+
+// LDS of k_matvec_nb in bytes from the start of its dynamic LDS:
+//   [0, w)   F32/NORM: the f32 rows [NB][xrow] and the norm's weights while
+//            the prologue reads them; then (and for QUANT from the start)
+//            the quantised rows qs [NB][k] and their tables [NB][nb]
+//            (scales; Q4_1 sums; Q4_0 totals), the contributions part
+//            [NB][16][pstride] of one tile of 16 weight rows and one chunk
+//            of blocks, and the GLU outputs;
+//   [w, end) the weight tile, direct-loaded (GLU: its gate rows at w, its
+//            up rows at w2).
+struct NbLds {
+    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, outs, w, w2, wrow, end;
+};
+
+// The LDS stride of rows of `bytes` bytes (a multiple of 16) read 16 rows at
+// a time by the matrix-core operands: bytes plus whole 16-byte pieces, so
+// that 16 rows start on 16 different 4-bank groups (stride / 4 an odd
+// multiple of 4, modulo the 64 banks).
+__host__ __device__ inline uint32_t nb_row_stride(uint32_t bytes) {
+    uint32_t s = bytes + 16u;
+    while ((((s >> 2) & 63u) >> 2 & 1u) == 0) s += 16u;
+    return s;
+}
+
+__host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint32_t row_bytes,
+                                        uint32_t mode, bool glu) {
+    const uint32_t nb = k >> 5;
+    auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
+    NbLds l;
+    l.qs = 0;
+    l.arow = nb_row_stride(k);
+    l.trow = nb_row_stride(4u * nb);
+    const uint32_t tab = kb(nbatch * l.trow);
+    l.scales = kb(nbatch * l.arow);
+    l.sums = l.scales + tab;
+    l.totals = l.sums + (kind == 2 ? tab : 0u);
+    const uint32_t act_end = l.totals + (kind == 1 ? tab : 0u);
+    l.pstride = ((nb < NB_CHUNK ? nb : NB_CHUNK) + 3u) / 4u * 4u + 4u;  // 16-byte rows, apart by 4 banks
+    l.part = act_end;
+    l.outs = l.part + 4u * nbatch * 16u * l.pstride;
+    const uint32_t outs_end = l.outs + (glu ? 4u * nbatch * (tr + tr / 2u) : 0u);
+    l.x = 0;
+    l.xrow = kb(4u * k);  // whole kilobytes: a row's last direct load may write past its end
+    l.nw = nbatch * l.xrow;
+    const uint32_t x_end = mode == NB_QUANT ? 0u : l.nw + (mode == NB_NORM ? kb(4u * k) : 0u);
+    l.w = kb(x_end > outs_end ? x_end : outs_end);
+    l.wrow = nb_row_stride(row_bytes);
+    const uint32_t half = kb((tr / 2u) * l.wrow);
+    l.w2 = glu ? l.w + half : l.w;
+    l.end = glu ? l.w2 + half : l.w + kb(tr * l.wrow);
+    return l;
+}
+
+// Direct loads of `rows` rows of `bytes` bytes (a multiple of 16) at src,
+// src_stride apart, into LDS rows `dst_stride` bytes apart from `to` (a
+// byte address; the region holds whole kilobytes), 1 KB a load, load i by
+// wave first + (i % waves): lane l of load i fills LDS piece 64 i + l of the
+// region with the row piece that lies there (a padding piece, or a piece
+// past the last row, takes a copy of a piece of the row). Returns this
+// wave's loads (0 for a wave outside [first, first + waves)).
+template <bool NT>
+__device__ __forceinline__ uint32_t stage_rows(const uint8_t* src, uint32_t bytes, size_t src_stride, uint32_t rows,
+                                               uint32_t to, uint32_t dst_stride, uint32_t wave, uint32_t first,
+                                               uint32_t waves) {
+    if (wave < first || wave >= first + waves) return 0;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t pp = dst_stride >> 4, per = bytes >> 4;
+    const uint32_t loads = (rows * pp + 63u) >> 6;
+    // piece q of the region is piece q % pp of row q / pp: the quotient by
+    // a float reciprocal, exact here (q + 1/2 never lies within 2^-11 of a
+    // multiple of pp, which is below 2^10, for q below 2^16)
+    const float inv = 1.0f / (float)pp;
+    uint32_t mine = 0;
+    for (uint32_t i = wave - first; i < loads; i += waves, ++mine) {
+        const uint32_t q = i * 64u + lane;
+        uint32_t r = (uint32_t)(((float)q + 0.5f) * inv);
+        uint32_t e = q - r * pp;
+        if (r >= rows) r = rows - 1u, e = per - 1u;
+        if (e >= per) e = per - 1u;
+        const uint8_t* at = src + (size_t)r * src_stride + 16u * e;
+        if constexpr (NT) lds_load16_nt(at, to + i * 1024u);
+        else lds_load16(at, to + i * 1024u);
+    }
+    return mine;
+}
+
+// NB (at most 16) activation rows times a tile of `tr` weight rows per
+// workgroup, the tile's weights direct-loaded into LDS at the start (as
+// k_matvec_one does for one row). Every wave issues its share of the
+// activations first, then of the weights, so that its wait for the
+// activations never waits for weights.
+//   F32/NORM (k <= 2048, NB <= 8): NORM first takes each row through
+//     Op::RMSNorm (host.cr:374-386): Σx² in index order by speculation
+//     across one wave a row (ordered_sum_wave), root = sqrtf(Σ/k + eps),
+//     v = x / root · nw; then the quantiser (quantize_quad, 8 lanes a
+//     block) into LDS, spread over the workgroup, while the weights are in
+//     flight;
+//   QUANT: the rows arrive quantised.
+// Products on the int8 matrix cores: per tile of 16 weight rows and block,
+// one v_mfma_i32_16x16x32_i8 of the activation rows (A; rows past NB zero)
+// against the weight rows (B), operands taken where the blocks lie
+// (few_acts, few_weights; Q4_0's -8·Σq as C); each (row, output, block)
+// contribution is formed in the host's expression (Q8_0 float(t)·(d·sx);
+// Q4_0 (float(t)·d)·sx; Q4_1 (d·sx)·float(t) + m·mx) and written to LDS, a
+// chunk of NB_CHUNK blocks at a time, wave v taking blocks v, v + 8, ...;
+// then thread b·16 + r adds output (b, r)'s contributions of the chunk in
+// block order to its running sum (quant.cr:447-455). dst[b][row] = Σ (+
+// bias[b · bias_ld + row], one rounding); GLU: SwiGLU and the quantiser on
+// the tile's gate/up outputs into glu, as k_matvec_one. Each output depends
+// on its own activation row only, so the bits are those of one row at a
+// time.
+template <int KIND, uint32_t MODE, bool GLU, int NB>
+__global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                          uint32_t ldx, const float* __restrict__ nw, float eps,
+                                                          Activations act, float* __restrict__ dst,
+                                                          const float* __restrict__ bias, uint32_t bias_ld, uint32_t n,
+                                                          uint32_t k, uint32_t tr, Activations glu) {
+    static_assert(NB >= 1 && NB <= 16 && (MODE == NB_QUANT || NB <= 8), "activation rows of a launch");
+    extern __shared__ float4 lds4[];
+    uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
+    constexpr uint32_t BB = Fmt<KIND>::BB;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nb = k >> 5, row_bytes = nb * BB;
+    const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
+    const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
+    const NbLds L = nb_lds(NB, KIND, k, tr, row_bytes, MODE, GLU);
+    const uint32_t lbase = lds_address(base);
+
+    // Activations first, every wave its share, then the weights.
+    if constexpr (MODE == NB_QUANT) {
+        // rows and tables contiguous (the quantise pass's layout); NB·nb a
+        // multiple of 4 and the tables 16-byte aligned
+        stage_rows<false>(reinterpret_cast<const uint8_t*>(act.qs), k, k, NB, lbase + L.qs, L.arow, wave, 0u,
+                          NB_WAVES);
+        stage_rows<false>(reinterpret_cast<const uint8_t*>(act.scales), 4u * nb, 4u * nb, NB, lbase + L.scales, L.trow,
+                          wave, 0u, NB_WAVES);
+        if constexpr (KIND == 2)
+            stage_rows<false>(reinterpret_cast<const uint8_t*>(act.sums), 4u * nb, 4u * nb, NB, lbase + L.sums, L.trow,
+                              wave, 0u, NB_WAVES);
+        if constexpr (KIND == 1)
+            stage_rows<false>(reinterpret_cast<const uint8_t*>(act.totals), 4u * nb, 4u * nb, NB, lbase + L.totals,
+                              L.trow, wave, 0u, NB_WAVES);
+    } else {
+#pragma unroll
+        for (uint32_t b = 0; b < (uint32_t)NB; ++b)
+            stage_bytes<false>(reinterpret_cast<const uint8_t*>(x + (size_t)b * ldx), 4u * k,
+                               lbase + L.x + b * L.xrow, wave, b % NB_WAVES, 1u);
+        if constexpr (MODE == NB_NORM)
+            stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, NB % NB_WAVES, 1u);
+    }
+    uint32_t mine;
+    if constexpr (GLU) {
+        mine = stage_rows<true>(w + (size_t)g0 * row_bytes, row_bytes, row_bytes, h, lbase + L.w, L.wrow, wave, 0u,
+                                NB_WAVES);
+        mine += stage_rows<true>(w + (size_t)(H + g0) * row_bytes, row_bytes, row_bytes, h, lbase + L.w2, L.wrow, wave,
+                                 0u, NB_WAVES);
+    } else {
+        mine = stage_rows<true>(w + (size_t)row0 * row_bytes, row_bytes, row_bytes, rows, lbase + L.w, L.wrow, wave,
+                                0u, NB_WAVES);
+    }
+    wait_vm_lds_upto(mine);  // this wave's activation loads (issued before its weights) have landed
+    lds_sync();
+
+    int8_t* aq = reinterpret_cast<int8_t*>(base + L.qs);
+    float* asc = reinterpret_cast<float*>(base + L.scales);
+    float* asm_ = reinterpret_cast<float*>(base + L.sums);
+    int32_t* atot = reinterpret_cast<int32_t*>(base + L.totals);
+    if constexpr (MODE != NB_QUANT) {
+        // NORM: wave b takes Σx² of row b, lane c its chunk of 32 values
+        // (lanes past the row hold zeros); every thread takes the 4-value
+        // quarters j = t, t + 512, ... of the rows' blocks (row j / (8 nb),
+        // block j / 8 % nb, quarter j % 8), read before the quantised rows
+        // overwrite them.
+        __shared__ float roots[8];
+        constexpr uint32_t JOBS = NB * 64u * 8u / NB_THREADS;  // quarters a thread at k = 2048
+        const uint32_t jobs = NB * nb * 8u;
+        float4 xv[JOBS], wv[JOBS];
+#pragma unroll
+        for (uint32_t i = 0; i < JOBS; ++i) {
+            const uint32_t j = t + NB_THREADS * i;
+            if (j < jobs) {
+                const uint32_t b = j / (8u * nb), c = (j - b * 8u * nb) * 4u;
+                xv[i] = *reinterpret_cast<const float4*>(base + L.x + b * L.xrow + 4u * c);
+                if constexpr (MODE == NB_NORM) wv[i] = *reinterpret_cast<const float4*>(base + L.nw + 4u * c);
+            }
+        }
+        if constexpr (MODE == NB_NORM) {
+            if (wave < (uint32_t)NB) {
+                const float* xs = reinterpret_cast<const float*>(base + L.x + wave * L.xrow) + lane * 32u;
+                const bool live = lane < nb;
+                float sq[32];
+#pragma unroll
+                for (int i = 0; i < 32; i += 4) {
+                    const float4 q = live ? *reinterpret_cast<const float4*>(xs + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    sq[i] = q.x * q.x, sq[i + 1] = q.y * q.y, sq[i + 2] = q.z * q.z, sq[i + 3] = q.w * q.w;
+                }
+                const float total = ordered_sum_wave<32>(sq);
+                if (lane == 0) roots[wave] = __builtin_sqrtf(total / (float)k + eps);
+            }
+        }
+        lds_sync();  // the roots are in, and every value has been read
+#pragma unroll
+        for (uint32_t i = 0; i < JOBS; ++i) {
+            const uint32_t j = t + NB_THREADS * i;
+            if (j < jobs) {  // the same for the 8 lanes of a block (jobs a multiple of 8)
+                const uint32_t b = j / (8u * nb), c = (j - b * 8u * nb) * 4u, blk = c >> 5;
+                float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+                if constexpr (MODE == NB_NORM) {
+                    const float root = roots[b];
+                    const float g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float q = v[e] / root;
+                        v[e] = q * g[e];
+                    }
+                }
+                const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<uint32_t*>(aq + (size_t)b * L.arow + c) = q.packed;
+                if ((t & 7u) == 0) {
+                    const uint32_t at = b * (L.trow >> 2) + blk;
+                    asc[at] = q.scale;
+                    if constexpr (KIND == 2) asm_[at] = q.sum;
+                    if constexpr (KIND == 1) atot[at] = q.total;
+                }
+            }
+        }
+    }
+    wait_vm_lds<0>();  // this wave's weights
+    lds_sync();
+
+    // The lane's MFMA operands: activation row lr (A; zero past NB), k
+    // quarter lq; weight row 16·c + lr of tile c (B); its outputs are rows
+    // 4·lq + i of weight row 16·c + lr.
+    const uint32_t lr = lane & 15u, lq = lane >> 4;
+    const uint32_t chunk = min(nb, NB_CHUNK), pstride = L.pstride;
+    float* part = reinterpret_cast<float*>(base + L.part);
+    float* outs = reinterpret_cast<float*>(base + L.outs);
+    const uint8_t* arow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(lr, (uint32_t)NB - 1u) * L.arow;
+    const uint32_t tstride = L.trow >> 2, wstride = L.wrow;
+    const bool alive = lr < (uint32_t)NB;
+    const uint32_t fb = t >> 4, fr = t & 15u;  // the output this thread adds up: row fb, weight row 16·c + fr
+    for (uint32_t c = 0; c * 16u < rows; ++c) {
+        const uint32_t wr = min(16u * c + lr, rows - 1u);  // a clamped row's contributions are not written
+        const uint8_t* wrow = GLU ? (wr < h ? base + L.w + wr * wstride : base + L.w2 + (wr - h) * wstride)
+                                  : base + L.w + wr * wstride;
+        const bool wlive = 16u * c + lr < rows;
+        float acc = 0.0f;
+        for (uint32_t q0 = 0; q0 < nb; q0 += chunk) {
+            const uint32_t cl = min(chunk, nb - q0);  // blocks of this chunk, a multiple of 8
+            const uint32_t u0 = NB_PER * wave;        // this wave's first block of the chunk
+            if (u0 < cl) {
+                // Every operand read of the wave's 8 blocks first, then the
+                // MFMAs, then the contributions.
+                typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
+                typedef int i4a __attribute__((ext_vector_type(4), aligned(16)));
+                long av[NB_PER], bv[NB_PER];
+                uint32_t dm[NB_PER];
+                float sx[4][NB_PER], ex[4][NB_PER];
+#pragma unroll
+                for (uint32_t p = 0; p < NB_PER; ++p) {
+                    const uint32_t b = q0 + u0 + p;  // of p's parity (q0, u0 even)
+                    const long a = few_acts<KIND>(arow, b, lq);  // arow clamped: a valid row
+                    av[p] = alive ? a : 0l;
+                    bv[p] = p % 2u ? few_weights_at<KIND, true>(wrow, b, lq) : few_weights_at<KIND, false>(wrow, b, lq);
+                    if constexpr (KIND == 2) dm[p] = *reinterpret_cast<const uint32_t*>(wrow + 20u * b);
+                    else dm[p] = *reinterpret_cast<const uint16_t*>(wrow + BB * b);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // 16-byte aligned: table rows of whole 16-byte pieces, chunks of 64, 8 blocks a wave
+                    const uint32_t at = min(4u * lq + i, (uint32_t)NB - 1u) * tstride + q0 + u0;
+                    const f4a s0 = *reinterpret_cast<const f4a*>(asc + at);
+                    const f4a s1 = *reinterpret_cast<const f4a*>(asc + at + 4u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sx[i][e] = s0[e], sx[i][4 + e] = s1[e], ex[i][e] = ex[i][4 + e] = 0.0f;
+                    if constexpr (KIND == 2) {
+                        const f4a e0 = *reinterpret_cast<const f4a*>(asm_ + at);
+                        const f4a e1 = *reinterpret_cast<const f4a*>(asm_ + at + 4u);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ex[i][e] = e0[e], ex[i][4 + e] = e1[e];
+                    }
+                    if constexpr (KIND == 1) {
+                        const i4a e0 = *reinterpret_cast<const i4a*>(atot + at);
+                        const i4a e1 = *reinterpret_cast<const i4a*>(atot + at + 4u);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            ex[i][e] = __int_as_float(-8 * e0[e]), ex[i][4 + e] = __int_as_float(-8 * e1[e]);
+                    }
+                }
+                v4i tv[NB_PER];
+#pragma unroll
+                for (uint32_t p = 0; p < NB_PER; ++p) {
+                    v4i cin = {0, 0, 0, 0};
+                    if constexpr (KIND == 1) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) cin[i] = __float_as_int(ex[i][p]);
+                    }
+                    tv[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[p], bv[p], cin, 0, 0, 0);
+                }
+                float cv[4][NB_PER];
+#pragma unroll
+                for (uint32_t p = 0; p < NB_PER; ++p) {
+                    const float d = half_value(dm[p] & 0xffffu);
+                    const float m = KIND == 2 ? half_value(dm[p] >> 16) : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float ft = (float)tv[p][i];
+                        if constexpr (KIND == 0) {
+                            const float sc = d * sx[i][p];
+                            cv[i][p] = ft * sc;
+                        } else if constexpr (KIND == 1) {
+                            const float pr = ft * d;
+                            cv[i][p] = pr * sx[i][p];
+                        } else {
+                            const float sc = d * sx[i][p];
+                            const float f = sc * ft;
+                            const float g = m * ex[i][p];
+                            cv[i][p] = f + g;
+                        }
+                    }
+                }
+                if (wlive) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (4u * lq + i < (uint32_t)NB) {
+                            f4a* to = reinterpret_cast<f4a*>(part + ((4u * lq + i) * 16u + lr) * pstride + u0);
+                            const f4a c0 = {cv[i][0], cv[i][1], cv[i][2], cv[i][3]};
+                            const f4a c1 = {cv[i][4], cv[i][5], cv[i][6], cv[i][7]};
+                            to[0] = c0;
+                            to[1] = c1;
+                        }
+                    }
+                }
+            }
+            lds_sync();
+            if (fb < (uint32_t)NB && 16u * c + fr < rows) {
+                // the chunk's contributions in block order, read 32 at a
+                // time into registers before they are added
+                const float* cp = part + (fb * 16u + fr) * pstride;
+                uint32_t i = 0;
+                for (; i + 32u <= cl; i += 32u) {
+                    float2 vv[16];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        acc += vv[e].x;
+                        acc += vv[e].y;
+                    }
+                }
+                for (; i < cl; ++i) acc += cp[i];
+            }
+            lds_sync();
+        }
+        if (fb < (uint32_t)NB && 16u * c + fr < rows) {
+            const uint32_t r = 16u * c + fr;
+            if constexpr (GLU) {
+                outs[fb * tr + r] = acc;
+            } else {
+                const uint32_t row = row0 + r;
+                dst[(size_t)fb * n + row] = bias ? acc + bias[(size_t)fb * bias_ld + row] : acc;
+            }
+        }
+    }
+    if constexpr (GLU) {
+        // SwiGLU one output a thread, then the quantiser, 8 lanes a block
+        lds_sync();
+        float* act_out = outs + NB * tr;
+        for (uint32_t o = t; o < (uint32_t)NB * h; o += NB_THREADS) {
+            const uint32_t b = o / h, i = o - b * h;
+            act_out[o] = swiglu_value(outs[b * tr + i], outs[b * tr + h + i]);
+        }
+        lds_sync();
+        const uint32_t hb = h >> 5, Hb = H >> 5, sub = t & 7u;
+        for (uint32_t g = t >> 3; g < (uint32_t)NB * hb; g += NB_THREADS / 8u) {  // uniform across each 8-lane group
+            const uint32_t b = g / hb, blk = g - b * hb;
+            const float4 v4 = *reinterpret_cast<const float4*>(act_out + b * h + blk * 32u + sub * 4u);
+            const Q8Quad q = quantize_quad(v4.x, v4.y, v4.z, v4.w);
+            const uint32_t col = g0 + blk * 32u + sub * 4u;
+            *(uint32_t*)((int8_t*)glu.qs + (size_t)b * H + col) = q.packed;
+            if (sub == 0) {
+                const size_t at = (size_t)b * Hb + (g0 >> 5) + blk;
+                ((float*)glu.scales)[at] = q.scale;
+                ((float*)glu.sums)[at] = q.sum;
+                ((int32_t*)glu.totals)[at] = q.total;
+            }
+        }
     }
 }
 
@@ -2787,6 +3219,16 @@ static hipError_t launch_few_kind(uint32_t kind, const uint8_t* w, Activations a
     }
 }
 
+// Whether AUTO products of up to 8 rows take the kernel with weights in
+// LDS (TMH_FEW_ROWS_KERNEL=lanes keeps the lanes kernels, for comparisons).
+static bool few_rows_kernel() {
+    static const bool lanes = [] {
+        const char* env = getenv("TMH_FEW_ROWS_KERNEL");
+        return env && strcmp(env, "lanes") == 0;
+    }();
+    return !lanes;
+}
+
 hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, Activations act, float* dst,
                                const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
                                hipStream_t stream) {
@@ -2800,6 +3242,17 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
         case 1: return launch_mx<1>(fused, w, act, dst, bias, rows, n, k, stream);
         default: return launch_mx<2>(fused, w, act, dst, bias, rows, n, k, stream);
         }
+    }
+    if (mode == 0u /* AUTO */ && (rows == 1u || rows == 8u) && few_rows_kernel()) {
+        // one or 8 rows: the weights of each workgroup's tile staged into LDS
+        // at once, the products on the matrix cores (measured, Q4_1: 8 rows
+        // 9.8 / 13.4 us against 12.2 / 14.9 for the lanes kernel at 8192x2048
+        // / 2048x8192, one row 9.1 against 10.4 at 2048x8192; from 2 to 4 rows
+        // the lanes kernel is as fast or faster, 10.7 against 11.9 at 2 rows
+        // of 2048x8192)
+        const hipError_t e = launch_rows_product(kind, NB_QUANT, w, nullptr, 0, nullptr, 0.0f, act, dst, bias, 0, rows,
+                                                 n, k, compute_units, stream);
+        if (e != hipErrorInvalidValue) return e;
     }
     if (mode == 0u /* AUTO */ && few_fits(w, act, kind, rows, k))
         return launch_few_kind(kind, w, act, dst, bias, 0, rows, n, k, stream);
@@ -2986,6 +3439,206 @@ hipError_t launch_gate_up_swiglu_rms(uint32_t kind, const uint8_t* w, const floa
     case 1: return launch_glu_one<1>(w, x, norm, eps, H, k, glu, stream);
     default: return launch_glu_one<2>(w, x, norm, eps, H, k, glu, stream);
     }
+}
+
+// ----------------------------------- a few rows, weights in LDS: launchers
+
+// k a multiple of 256 (whole groups of 8 blocks a wave), weight rows of
+// whole 16-byte pieces starting 16-byte aligned (the direct loads); QUANT: rows and tables 16-byte aligned; F32/NORM: at most 2048
+// values a row (a block a lane), rows and norm weights 16-byte aligned. A
+// last single row of QUANT or NORM takes the one-row kernel, whose own
+// limits apply then.
+static bool nb_fits(uint32_t kind, uint32_t mode, const uint8_t* w, uint32_t rows, uint32_t k, const float* x,
+                    uint32_t ldx, const float* nw, const Activations& act) {
+    const uint32_t nb = k >> 5;
+    if (nb == 0 || k % 256u != 0 || (nb * block_bytes(kind)) % 16u != 0 || ((uintptr_t)w & 15u) != 0) return false;
+    if (mode != NB_F32 && rows % 2u == 1u && !one_fits(kind, w, k)) return false;
+    if (mode == NB_QUANT) {
+        const uintptr_t extra = kind == 1 ? (uintptr_t)act.totals : kind == 2 ? (uintptr_t)act.sums : 0;
+        return act.qs && act.scales && (((uintptr_t)act.qs | (uintptr_t)act.scales | extra) & 15u) == 0;
+    }
+    if (k > 2048u || !x || ((uintptr_t)x & 15u) != 0 || ldx % 4u != 0) return false;
+    return mode != NB_NORM || (nw && ((uintptr_t)nw & 15u) == 0);
+}
+
+// Weight rows a workgroup: about one workgroup a compute unit, within the
+// LDS limit; rounds of equal tiles when the rows take more than one round.
+template <int KIND, uint32_t MODE, int NB>
+static uint32_t nb_tile(uint32_t n, uint32_t k, int compute_units) {
+    const uint32_t nb = k >> 5, rb = nb * Fmt<KIND>::BB;
+    const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
+    uint32_t tr = std::max(1u, (n + cus - 1u) / cus);
+    while (tr > 1 && nb_lds(NB, KIND, k, tr, rb, MODE, false).end > ONE_LDS_LIMIT) --tr;
+    const uint64_t per_round = (uint64_t)cus * tr;
+    const uint64_t rounds = (n + per_round - 1u) / per_round;
+    return std::max(1u, (uint32_t)((n + cus * rounds - 1u) / (cus * rounds)));
+}
+
+template <int KIND, uint32_t MODE, int NB>
+static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
+                            Activations act, float* dst, const float* bias, uint32_t bias_ld, uint32_t n, uint32_t k,
+                            int compute_units, hipStream_t stream) {
+    const uint32_t nb = k >> 5;
+    const uint32_t tr = nb_tile<KIND, MODE, NB>(n, k, compute_units);
+    const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false);
+    if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NB_THREADS), L.end,
+                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, Activations{});
+    return hipGetLastError();
+}
+
+// Activation rows in groups of 8, 4 and 2 (each output depends on its own
+// row only, so the grouping changes no bits); a last single row takes the
+// one-row kernel (F32: k_matvec_nb of one row).
+template <int KIND, uint32_t MODE>
+static hipError_t launch_nb_rows(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
+                                 Activations act, float* dst, const float* bias, uint32_t bias_ld, uint32_t rows,
+                                 uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+    const uint32_t nb = k >> 5;
+    uint32_t done = 0;
+    while (done < rows) {
+        const uint32_t left = rows - done;
+        Activations a = act;
+        if (MODE == NB_QUANT) {
+            a.scales += (size_t)done * nb;
+            a.sums += (size_t)done * nb;
+            a.totals += (size_t)done * nb;
+            a.qs += (size_t)done * k;
+        }
+        const float* xr = MODE == NB_QUANT ? nullptr : x + (size_t)done * ldx;
+        float* d = dst + (size_t)done * n;
+        const float* bi = bias ? bias + (size_t)done * bias_ld : nullptr;
+        hipError_t err;
+        uint32_t take;
+        if (left >= 8) {
+            err = launch_nb<KIND, MODE, 8>(w, xr, ldx, nw, eps, a, d, bi, bias_ld, n, k, compute_units, stream), take = 8;
+        } else if (left >= 4) {
+            err = launch_nb<KIND, MODE, 4>(w, xr, ldx, nw, eps, a, d, bi, bias_ld, n, k, compute_units, stream), take = 4;
+        } else if (left >= 2) {
+            err = launch_nb<KIND, MODE, 2>(w, xr, ldx, nw, eps, a, d, bi, bias_ld, n, k, compute_units, stream), take = 2;
+        } else {
+            take = 1;
+            if constexpr (MODE == NB_F32)
+                err = launch_nb<KIND, NB_F32, 1>(w, xr, ldx, nullptr, 0.0f, a, d, bi, 0, n, k, compute_units, stream);
+            else if constexpr (MODE == NB_NORM)
+                err = bi ? hipErrorInvalidValue
+                         : launch_one<KIND, true>(w, xr, nw, eps, Activations{}, d, nullptr, n, k, compute_units, stream);
+            else
+                err = launch_one<KIND, false>(w, nullptr, nullptr, 0.0f, a, d, bi, n, k, compute_units, stream);
+        }
+        if (err != hipSuccess) return err;
+        done += take;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_rows_product(uint32_t kind, uint32_t mode, const uint8_t* w, const float* x, uint32_t ldx,
+                               const float* nw, float eps, Activations act, float* dst, const float* bias,
+                               uint32_t bias_ld, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                               hipStream_t stream) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (mode > NB_NORM || !nb_fits(kind, mode, w, rows, k, x, ldx, nw, act) || (mode == NB_NORM && bias))
+        return hipErrorInvalidValue;
+#define TMH_NB_MODES(KIND)                                                                                          \
+    switch (mode) {                                                                                                 \
+    case NB_QUANT:                                                                                                  \
+        return launch_nb_rows<KIND, NB_QUANT>(w, x, ldx, nw, eps, act, dst, bias, bias_ld, rows, n, k,              \
+                                              compute_units, stream);                                               \
+    case NB_F32:                                                                                                    \
+        return launch_nb_rows<KIND, NB_F32>(w, x, ldx, nw, eps, act, dst, bias, bias_ld, rows, n, k, compute_units, \
+                                            stream);                                                                \
+    default:                                                                                                        \
+        return launch_nb_rows<KIND, NB_NORM>(w, x, ldx, nw, eps, act, dst, bias, bias_ld, rows, n, k,               \
+                                             compute_units, stream);                                                \
+    }
+    switch (kind) {
+    case 0: TMH_NB_MODES(0)
+    case 1: TMH_NB_MODES(1)
+    default: TMH_NB_MODES(2)
+    }
+#undef TMH_NB_MODES
+}
+
+// The GLU tile of k_matvec_nb: 32 gate rows and the 32 up rows of the same
+// indices (one quantisation block of outputs).
+static constexpr uint32_t NB_GLU_HALF = 32;
+
+template <int KIND, uint32_t MODE, int NB>
+static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
+                                Activations act, uint32_t H, uint32_t k, Activations glu, hipStream_t stream) {
+    const uint32_t nb = k >> 5, h = NB_GLU_HALF;
+    const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
+    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NB_THREADS), L.end, stream, w, x, ldx, nw,
+                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, glu);
+    return hipGetLastError();
+}
+
+template <int KIND, uint32_t MODE>
+static hipError_t launch_nb_glu_rows(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
+                                     Activations act, uint32_t rows, uint32_t H, uint32_t k, Activations glu,
+                                     hipStream_t stream) {
+    const uint32_t nb = k >> 5, hb = H >> 5;
+    uint32_t done = 0;
+    while (done < rows) {
+        const uint32_t left = rows - done;
+        Activations g = glu, a = act;
+        g.scales += (size_t)done * hb;
+        g.sums += (size_t)done * hb;
+        g.totals += (size_t)done * hb;
+        g.qs += (size_t)done * H;
+        if (MODE == NB_QUANT) {
+            a.scales += (size_t)done * nb;
+            a.sums += (size_t)done * nb;
+            a.totals += (size_t)done * nb;
+            a.qs += (size_t)done * k;
+        }
+        const float* xr = MODE == NB_QUANT ? nullptr : x + (size_t)done * ldx;
+        hipError_t err;
+        uint32_t take;
+        if (left >= 8) {
+            err = launch_nb_glu<KIND, MODE, 8>(w, xr, ldx, nw, eps, a, H, k, g, stream), take = 8;
+        } else if (left >= 4) {
+            err = launch_nb_glu<KIND, MODE, 4>(w, xr, ldx, nw, eps, a, H, k, g, stream), take = 4;
+        } else if (left >= 2) {
+            err = launch_nb_glu<KIND, MODE, 2>(w, xr, ldx, nw, eps, a, H, k, g, stream), take = 2;
+        } else {
+            take = 1;
+            if constexpr (MODE == NB_NORM) err = launch_glu_one<KIND>(w, xr, nw, eps, H, k, g, stream);
+            else err = launch_glu_nb<KIND, 1>(w, a, H, k, g, stream);
+        }
+        if (err != hipSuccess) return err;
+        done += take;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_rows_gate_up(uint32_t kind, uint32_t mode, const uint8_t* w, const float* x, uint32_t ldx,
+                               const float* nw, float eps, Activations act, uint32_t rows, uint32_t H, uint32_t k,
+                               Activations glu, hipStream_t stream) {
+    if (rows == 0 || H == 0) return hipSuccess;
+    if ((mode != NB_NORM && mode != NB_QUANT) || !nb_fits(kind, mode, w, rows, k, x, ldx, nw, act) ||
+        H % NB_GLU_HALF != 0)
+        return hipErrorInvalidValue;
+    const uint32_t nb = k >> 5, np = nb / 2u;
+    // the tile in LDS at the largest group (a last single row: the one-row
+    // kernel's own limits under NORM, the lanes GLU kernel's under QUANT)
+    const uint32_t group = rows >= 8 ? 8u : rows >= 4 ? 4u : rows >= 2 ? 2u : 1u;
+    if (nb_lds(group, kind, k, 2u * NB_GLU_HALF, nb * block_bytes(kind), mode, true).end > ONE_LDS_LIMIT)
+        return hipErrorInvalidValue;
+    if (rows % 2u == 1u) {
+        const uint32_t h1 = glu_half(nb);
+        if ((np & (np - 1u)) != 0 || H % h1 != 0 || glu_lds(1, nb) > CU_LDS ||
+            (mode == NB_NORM && one_lds(k, 2u * h1, nb * block_bytes(kind), lanes_stride(nb), true, true).end >
+                                    ONE_LDS_LIMIT))
+            return hipErrorInvalidValue;
+    }
+#define TMH_NB_GLU(KIND)                                                                                                return mode == NB_QUANT ? launch_nb_glu_rows<KIND, NB_QUANT>(w, x, ldx, nw, eps, act, rows, H, k, glu, stream)                             : launch_nb_glu_rows<KIND, NB_NORM>(w, x, ldx, nw, eps, act, rows, H, k, glu, stream);
+    switch (kind) {
+    case 0: TMH_NB_GLU(0)
+    case 1: TMH_NB_GLU(1)
+    default: TMH_NB_GLU(2)
+    }
+#undef TMH_NB_GLU
 }
 
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,

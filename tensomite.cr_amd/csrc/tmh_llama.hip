@@ -9,6 +9,7 @@
 // round trip and one captured HIP graph replays any number of them.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -76,11 +77,41 @@ struct Llama {
     void* owned = nullptr;  // weights this decoder loaded itself (tmh_llama_load_gguf)
 };
 
+// Rows a forward takes through the products whose workgroups stage their
+// weight tile into LDS and run the norm and quantiser in their prologue
+// (one row: k_matvec_one; 2 to 8: k_matvec_nb), five launches a layer.
+constexpr uint32_t FEW_ROWS = 8;
+
+// How a forward of 2 to FEW_ROWS rows takes RMSNorm: in a launch of its own
+// (k_rmsnorm_quantise_wave) before the products, which then take the
+// quantised rows -- the default: every workgroup of a fused product would
+// normalise and quantise every row again, VALU work that outweighs the
+// launch at 8 rows -- or in each product's prologue (TMH_FEW_ROWS_NORM=fused,
+// for comparisons).
+bool few_rows_norm_fused() {
+    static const bool fused = [] {
+        const char* env = getenv("TMH_FEW_ROWS_NORM");
+        return env && strcmp(env, "fused") == 0;
+    }();
+    return fused;
+}
+
 // dst[rows, n] = act · wᵀ (+ bias) over quantised activations.
 hipError_t product(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
                    uint32_t n, uint32_t k, float* dst, const float* bias) {
     return tmh::launch_block_matmul(m.c.kind, TMH_MODE_AUTO, w, act, dst, bias, rows, n, k, ctx.compute_units,
                                     ctx.stream);
+}
+
+// dst[rows, n] = act · wᵀ with no bias: up to FEW_ROWS rows the product
+// with weights in LDS, else (or where its shape does not fit) product().
+hipError_t few_product(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
+                       uint32_t n, uint32_t k, float* dst) {
+    hipError_t e = rows <= FEW_ROWS ? tmh::launch_rows_product(m.c.kind, tmh::NB_QUANT, w, nullptr, 0, nullptr, 0.0f,
+                                                               act, dst, nullptr, 0, rows, n, k, ctx.compute_units,
+                                                               ctx.stream)
+                                    : hipErrorInvalidValue;
+    return e == hipErrorInvalidValue ? product(m, ctx, w, act, rows, n, k, dst, nullptr) : e;
 }
 
 // Quantises rows of f32 activations into act.
@@ -100,16 +131,20 @@ hipError_t norm_quantise(const Llama& m, const DeviceContext& ctx, const float* 
 
 // The residual update x += act · wᵀ, as the host's `x + product` (one
 // rounding per element either way round): for fewer rows than the matrix
-// cores take, the lanes product adds each row's x as its bias and writes
-// the other residual buffer; else one row is a product with x as bias, and
-// more rows a product and an add.
+// cores take, the product (weights in LDS up to FEW_ROWS rows, else the
+// lanes or few-rows kernel) adds each row's x as its bias and writes the
+// other residual buffer; else one row is a product with x as bias, and more
+// rows a product and an add.
 hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, tmh::Activations act, uint32_t rows,
                     uint32_t k, int& cur) {
     const uint32_t W = (uint32_t)m.c.width;
-    if (rows == 1) {
-        // one row: the weights of each workgroup's tile staged into LDS at once
-        hipError_t r = tmh::launch_product_one(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], W, k, ctx.compute_units,
-                                               ctx.stream);
+    if (rows <= FEW_ROWS) {
+        // up to 8 rows: the weights of each workgroup's tile staged into LDS at once
+        hipError_t r = rows == 1 ? tmh::launch_product_one(m.c.kind, w, act, m.x[cur ^ 1], m.x[cur], W, k,
+                                                           ctx.compute_units, ctx.stream)
+                                 : tmh::launch_rows_product(m.c.kind, tmh::NB_QUANT, w, nullptr, 0, nullptr, 0.0f, act,
+                                                            m.x[cur ^ 1], m.x[cur], W, rows, W, k, ctx.compute_units,
+                                                            ctx.stream);
         if (r != hipErrorInvalidValue) {
             cur ^= 1;
             return r;
@@ -141,22 +176,28 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
     const uint32_t W = (uint32_t)c.width, H = (uint32_t)c.hidden, hw = (uint32_t)c.head_width;
     const float scale = (float)(1.0 / std::sqrt((double)hw));
     const bool quant_att = hw % 32u == 0;
-    const bool rows_fused = tokens == 1;
+    const bool rows_fused = tokens <= FEW_ROWS;
     int cur = 0;
     hipError_t e = tmh::launch_gather(c.kind, m.embed, c.vocab, W, m.ids, tokens, m.x[cur], ctx.errors, ctx.stream);
     const tmh::Activations a_in = tmh::carve_scratch(m.scratch[0], tokens, W);
     for (int32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
         float* keys = m.keys + (size_t)l * m.layer_cache;
         float* values = m.values + (size_t)l * m.layer_cache;
-        // one row: the norm and quantiser in the product's prologue (one
-        // launch); else RMSNorm+quantise, then the product
-        hipError_t f = rows_fused ? tmh::launch_product_rms(c.kind, m.qkv[l], m.x[cur], W, m.attn_norm[l], c.eps,
-                                                            m.qkv_out, tokens, m.nqkv, W, ctx.compute_units,
-                                                            ctx.stream)
-                                  : hipErrorInvalidValue;
+        // one row (or up to FEW_ROWS with the fused norm): the norm and
+        // quantiser in the product's prologue (one launch); else
+        // RMSNorm+quantise, then the product
+        hipError_t f = !rows_fused ? hipErrorInvalidValue
+                       : tokens == 1
+                           ? tmh::launch_product_rms(c.kind, m.qkv[l], m.x[cur], W, m.attn_norm[l], c.eps, m.qkv_out,
+                                                     tokens, m.nqkv, W, ctx.compute_units, ctx.stream)
+                       : few_rows_norm_fused()
+                           ? tmh::launch_rows_product(c.kind, tmh::NB_NORM, m.qkv[l], m.x[cur], W, m.attn_norm[l],
+                                                      c.eps, tmh::Activations{}, m.qkv_out, nullptr, 0, tokens,
+                                                      m.nqkv, W, ctx.compute_units, ctx.stream)
+                           : hipErrorInvalidValue;
         if (f == hipErrorInvalidValue) {
             e = norm_quantise(m, ctx, m.x[cur], m.attn_norm[l], tokens, a_in);
-            if (e == hipSuccess) e = product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out, nullptr);
+            if (e == hipSuccess) e = few_product(m, ctx, m.qkv[l], a_in, tokens, m.nqkv, W, m.qkv_out);
         } else {
             e = f;
         }
@@ -177,11 +218,14 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
         if (e == hipSuccess && !quant_att) e = quantise(ctx, m.att, tokens, m.qn, a_att);
         if (e == hipSuccess) e = residual(m, ctx, m.o[l], a_att, tokens, m.qn, cur);
         const tmh::Activations a_hid = tmh::carve_scratch(m.scratch[1], tokens, H);
-        // one row: RMSNorm in gate_up's prologue, SwiGLU and the quantiser in
-        // its epilogue (one launch)
-        hipError_t fg = (e == hipSuccess && rows_fused)
-                            ? tmh::launch_gate_up_swiglu_rms(c.kind, m.gate_up[l], m.x[cur], W, m.ffn_norm[l], c.eps,
-                                                             tokens, H, W, a_hid, ctx.stream)
+        // up to FEW_ROWS rows: RMSNorm in gate_up's prologue, SwiGLU and the
+        // quantiser in its epilogue (one launch)
+        hipError_t fg = !(e == hipSuccess && rows_fused) ? hipErrorInvalidValue
+                        : tokens == 1 ? tmh::launch_gate_up_swiglu_rms(c.kind, m.gate_up[l], m.x[cur], W, m.ffn_norm[l],
+                                                                       c.eps, tokens, H, W, a_hid, ctx.stream)
+                        : few_rows_norm_fused()
+                            ? tmh::launch_rows_gate_up(c.kind, tmh::NB_NORM, m.gate_up[l], m.x[cur], W, m.ffn_norm[l],
+                                                       c.eps, tmh::Activations{}, tokens, H, W, a_hid, ctx.stream)
                             : hipErrorInvalidValue;
         if (fg != hipErrorInvalidValue) {
             e = fg;
@@ -190,8 +234,14 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
         }
         if (e == hipSuccess && fg == hipErrorInvalidValue) {
             // gate_up with SwiGLU and the quantiser in its epilogue where the
-            // shape allows, else the product then SwiGLU+quantise
-            hipError_t g = tmh::launch_gate_up_swiglu(c.kind, m.gate_up[l], a_in, tokens, H, W, a_hid, ctx.stream);
+            // shape allows (weights in LDS up to FEW_ROWS rows, else the
+            // lanes kernel), else the product then SwiGLU+quantise
+            hipError_t g = tokens <= FEW_ROWS
+                               ? tmh::launch_rows_gate_up(c.kind, tmh::NB_QUANT, m.gate_up[l], nullptr, 0, nullptr,
+                                                          0.0f, a_in, tokens, H, W, a_hid, ctx.stream)
+                               : hipErrorInvalidValue;
+            if (g == hipErrorInvalidValue)
+                g = tmh::launch_gate_up_swiglu(c.kind, m.gate_up[l], a_in, tokens, H, W, a_hid, ctx.stream);
             if (g == hipErrorInvalidValue) {
                 e = product(m, ctx, m.gate_up[l], a_in, tokens, 2u * H, W, m.gu, nullptr);
                 if (e == hipSuccess)
@@ -204,14 +254,19 @@ hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tok
     }
     const tmh::Activations a_fin = tmh::carve_scratch(m.scratch[0], final_rows, W);
     float* logits = m.logits + (size_t)logits_row * c.vocab;
-    hipError_t fh = (e == hipSuccess && final_rows == 1)
-                        ? tmh::launch_product_rms(c.kind, m.head, m.x[cur] + (size_t)final_from * W, W, m.norm, c.eps,
-                                                  logits, final_rows, (uint32_t)c.vocab, W, ctx.compute_units,
-                                                  ctx.stream)
+    const float* x_fin = m.x[cur] + (size_t)final_from * W;
+    hipError_t fh = !(e == hipSuccess && final_rows <= FEW_ROWS) ? hipErrorInvalidValue
+                    : final_rows == 1
+                        ? tmh::launch_product_rms(c.kind, m.head, x_fin, W, m.norm, c.eps, logits, final_rows,
+                                                  (uint32_t)c.vocab, W, ctx.compute_units, ctx.stream)
+                    : few_rows_norm_fused()
+                        ? tmh::launch_rows_product(c.kind, tmh::NB_NORM, m.head, x_fin, W, m.norm, c.eps,
+                                                   tmh::Activations{}, logits, nullptr, 0, final_rows,
+                                                   (uint32_t)c.vocab, W, ctx.compute_units, ctx.stream)
                         : hipErrorInvalidValue;
     if (fh != hipErrorInvalidValue) return fh;
-    if (e == hipSuccess) e = norm_quantise(m, ctx, m.x[cur] + (size_t)final_from * W, m.norm, final_rows, a_fin);
-    if (e == hipSuccess) e = product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, logits, nullptr);
+    if (e == hipSuccess) e = norm_quantise(m, ctx, x_fin, m.norm, final_rows, a_fin);
+    if (e == hipSuccess) e = few_product(m, ctx, m.head, a_fin, final_rows, (uint32_t)c.vocab, W, logits);
     return e;
 }
 

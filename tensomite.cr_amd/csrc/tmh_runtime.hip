@@ -728,6 +728,35 @@ int check_product(uint32_t kind, uint32_t rows, uint32_t n, uint32_t k, uint32_t
     return TMH_SUCCESS;
 }
 
+// The one-row kernel (which quantises x itself) takes one-row AUTO products
+// of at most this many weight bytes; larger ones stream better through the
+// few-rows kernel or the quantise pass and the lanes product (measured: Q4_1
+// 8192x2048 one row 11.7 us against about 7; 2048x8192 21 against about 10).
+constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
+
+// AUTO products of 2 rows, and of one row above ROW_KERNEL_MAX_BYTES: the
+// few-rows kernel with weights in LDS, which quantises x in every
+// workgroup's prologue (k at most 2048), one launch and no scratch. From 3
+// rows the quantisation of every row by every workgroup costs more than the
+// quantise pass (measured, Q4_1 8192x2048: 6.1 / 7.7 / 9.9 / 12.6 us at 1 /
+// 2 / 4 / 8 rows, against 7.7 / 8.2 / 9.8 / 12.2 for the quantise pass and
+// the lanes product), so those take the quantise pass and the product.
+// hipErrorInvalidValue, nothing launched, when the call is not for it.
+// TMH_FEW_ROWS_KERNEL=lanes keeps the quantise pass and the lanes product,
+// for comparisons.
+hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, float* dst,
+                        const float* bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
+    static const bool lanes = [] {
+        const char* env = getenv("TMH_FEW_ROWS_KERNEL");
+        return env && strcmp(env, "lanes") == 0;
+    }();
+    const uint64_t bytes = (uint64_t)n * (k / 32u) * tmh::block_bytes(kind);
+    if (lanes || mode != TMH_MODE_AUTO || rows > 2u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
+        return hipErrorInvalidValue;
+    return tmh::launch_rows_product(kind, tmh::NB_F32, w, x, ldx, nullptr, 0.0f, tmh::Activations{}, dst, bias, 0u,
+                                    rows, n, k, d.compute_units, d.stream);
+}
+
 }  // namespace
 
 int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
@@ -741,17 +770,19 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     if (rows == 0 || n == 0) return TMH_SUCCESS;
     if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
     const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
-    // One row of a product of at most 4 MB of weights: the one-row kernel,
-    // which quantises x itself (one launch). Larger ones stream better as
-    // the quantise pass and the lanes product (measured: Q4_1 8192x2048 one
-    // row 11.7 us against about 7; 2048x8192 21 against about 10).
-    constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
+    // One row of a product of at most ROW_KERNEL_MAX_BYTES of weights: the
+    // one-row kernel, which quantises x itself (one launch).
     if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
         tmh::row_kernel_fits(mode, wrow, k)) {
         hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
                                        d->compute_units, d->stream);
         if (e == hipSuccess) d->gpu_ops.fetch_add(1);
         return code(e);
+    }
+    hipError_t few = few_rows_f32(*d, kind, wrow, (const float*)x, ldx, (float*)dst, (const float*)bias, rows, n, k, mode);
+    if (few != hipErrorInvalidValue) {
+        if (few == hipSuccess) d->gpu_ops.fetch_add(1);
+        return code(few);
     }
     std::lock_guard<std::mutex> guard(d->launch);
     if ((err = ensure_scratch(*d, scratch_need(rows, k))) != TMH_SUCCESS) return err;
@@ -785,15 +816,19 @@ int tmh_block_matmul_fixed(uint32_t kind, uint64_t w, uint64_t w_byte_offset, ui
     if (rows == 0 || n == 0) return TMH_SUCCESS;
     if (!w || !x || !dst) return TMH_ERROR_INVALID_VALUE;
     const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
-    // The same choice of kernels as tmh_block_matmul: a one-row product that
-    // the one-row kernel takes needs no scratch at all.
-    constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
+    // The same choice of kernels as tmh_block_matmul: a product that the
+    // one-row or the few-rows kernel takes needs no scratch at all.
     if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
         tmh::row_kernel_fits(mode, wrow, k)) {
         hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
                                        d->compute_units, d->stream);
         if (e == hipSuccess) d->gpu_ops.fetch_add(1);
         return code(e);
+    }
+    hipError_t few = few_rows_f32(*d, kind, wrow, (const float*)x, ldx, (float*)dst, (const float*)bias, rows, n, k, mode);
+    if (few != hipErrorInvalidValue) {
+        if (few == hipSuccess) d->gpu_ops.fetch_add(1);
+        return code(few);
     }
     if (scratch_need(rows, k) > TMH_FIXED_SCRATCH_BYTES) return TMH_ERROR_SCRATCH_LIMIT;
     // Calls share this device's array; the lock keeps each call's quantise

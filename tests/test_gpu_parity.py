@@ -217,6 +217,33 @@ def test_one_row_over_4mb_with_bias(dev, fmt, n, k):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("k", [64, 512, 2048])
+def test_few_rows_weights_in_lds(dev, fmt, k):
+    # 1-8 rows (groups of 8, 4 and 2; one row above 4 MB) through the kernel
+    # that quantises the rows in each workgroup's prologue: rows ldx apart,
+    # a ragged last tile, a bias, and rows of zeros (scale 0), a spike and
+    # exact halves (rounding ties) beside Gaussian ones.
+    n = 1000 if k < 2048 else 4100
+    wq = weights(fmt, n, k, k + 1)
+    x = acts(8, k, k + 2)
+    x[k:2 * k] = 0.0
+    x[2 * k + 5] = 1e4
+    x[3 * k:4 * k] = (np.arange(k) % 255 - 127).astype(np.float32) * np.float32(0.5)
+    ldx = k + 32
+    strided = np.zeros(8 * ldx, np.float32)
+    for r in range(8):
+        strided[r * ldx:r * ldx + k] = x[r * k:(r + 1) * k]
+    bias = acts(1, n, 4)
+    want = oracle.add_bias(oracle.matmul(fmt, x, wq, 8, n, k), bias)
+    wbuf, xbuf, bbuf = dev.from_array(wq), dev.from_array(strided), dev.from_array(bias)
+    for rows in range(1, 9):
+        say("few rows", fmt, k, rows)
+        out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k, bias=bbuf, ldx=ldx)
+        got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
+        assert np.array_equal(bits(got), bits(want[:rows])), rows
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
 def test_special_rows(dev, fmt):
     # quant_spec.cr:30-48 on the device: zero first block, a spike of 50, a
     # zero activation block, the [127, j - 15.5] row, at {3, 5, 1280} and
