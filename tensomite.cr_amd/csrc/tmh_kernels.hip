@@ -2308,6 +2308,23 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     return l;
 }
 
+// Direct loads of one f32 row of nb blocks of 32 values at src into LDS at
+// `to` (the region holds whole kilobytes), by wave `by` only, swizzled for
+// reading a block a lane: the 16-byte piece i of block c lands in slot
+// 8 c + ((i + c) & 7), so that lanes c reading their piece i together fall
+// on 16 different 4-bank groups. Returns this wave's loads.
+__device__ __forceinline__ uint32_t stage_blocks_swizzled(const float* src, uint32_t nb, uint32_t to, uint32_t wave,
+                                                          uint32_t by) {
+    if (wave != by) return 0;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t slots = 8u * nb, loads = (slots + 63u) >> 6;
+    for (uint32_t n = 0; n < loads; ++n) {
+        const uint32_t slot = min(n * 64u + lane, slots - 1u), c = slot >> 3, i = (slot - c) & 7u;
+        lds_load16(src + 32u * c + 4u * i, to + n * 1024u);
+    }
+    return loads;
+}
+
 // Direct loads of `rows` rows of `bytes` bytes (a multiple of 16) at src,
 // src_stride apart, into LDS rows `dst_stride` bytes apart from `to` (a
 // byte address; the region holds whole kilobytes), 1 KB a load, load i by
@@ -2341,17 +2358,57 @@ __device__ __forceinline__ uint32_t stage_rows(const uint8_t* src, uint32_t byte
     return mine;
 }
 
+// One block of 32 activations (v) quantised by one lane, as
+// quantize_activations does it (quant.cr:428-442): d = amax/127, id = 1/d
+// (0 when d is 0), q = round-half-away(v·id) as int8; scale F16(d), sum
+// F16(float(Σq)·d). amax is the host's largest |v| taken in index order,
+// which skips a NaN unless it is v[0]: here a tree of the same comparison
+// that takes the right operand when the left is NaN (any order gives the
+// largest of the non-NaN values), then v[0]'s NaN if it is one.
+__device__ __forceinline__ void quantize_block32(const float (&v)[32], uint32_t (&packed)[8], float& scale,
+                                                 float& sum, int& total) {
+    float m[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m[i] = fabsf(v[i]);
+#pragma unroll
+    for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) {
+            const float a = m[i], b = m[i + w];
+            m[i] = (b > a || a != a) ? b : a;
+        }
+    const float first = fabsf(v[0]);
+    const float amax = first != first ? first : m[0];
+    const float d = amax / 127.0f;
+    const float id = d == 0.0f ? 0.0f : 1.0f / d;
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q0 = (int8_t)(int)roundf(v[4 * i] * id);
+        const int q1 = (int8_t)(int)roundf(v[4 * i + 1] * id);
+        const int q2 = (int8_t)(int)roundf(v[4 * i + 2] * id);
+        const int q3 = (int8_t)(int)roundf(v[4 * i + 3] * id);
+        packed[i] = (uint32_t)(q0 & 0xff) | (uint32_t)(q1 & 0xff) << 8 | (uint32_t)(q2 & 0xff) << 16 |
+                    (uint32_t)(q3 & 0xff) << 24;
+        tot += q0 + q1 + q2 + q3;
+    }
+    total = tot;
+    scale = round_to_half(d);
+    sum = round_to_half((float)tot * d);
+}
+
 // NB (at most 16) activation rows times a tile of `tr` weight rows per
 // workgroup, the tile's weights direct-loaded into LDS at the start (as
 // k_matvec_one does for one row). Every wave issues its share of the
 // activations first, then of the weights, so that its wait for the
 // activations never waits for weights.
-//   F32/NORM (k <= 2048, NB <= 8): NORM first takes each row through
-//     Op::RMSNorm (host.cr:374-386): Σx² in index order by speculation
-//     across one wave a row (ordered_sum_wave), root = sqrtf(Σ/k + eps),
-//     v = x / root · nw; then the quantiser (quantize_quad, 8 lanes a
-//     block) into LDS, spread over the workgroup, while the weights are in
-//     flight;
+//   F32/NORM (k <= 2048, NB <= 8): wave b takes row b into registers, lane
+//     c its block c (32 values; stage_blocks_swizzled; one f32 row is
+//     quantised by the whole workgroup, 8 lanes a block); NORM first takes
+//     the row through Op::RMSNorm (host.cr:374-386): Σx² in index order by
+//     speculation across the wave (ordered_sum_wave), root = sqrtf(Σ/k +
+//     eps), v = x / root · nw; then the lane quantises its block
+//     (quantize_block32) into LDS, while the weights are in flight;
 //   QUANT: the rows arrive quantised.
 // Products on the int8 matrix cores: per tile of 16 weight rows and block,
 // one v_mfma_i32_16x16x32_i8 of the activation rows (A; rows past NB zero)
@@ -2398,12 +2455,14 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
             stage_rows<false>(reinterpret_cast<const uint8_t*>(act.totals), 4u * nb, 4u * nb, NB, lbase + L.totals,
                               L.trow, wave, 0u, NB_WAVES);
     } else {
+        if constexpr (MODE == NB_F32 && NB == 1) {
+            stage_bytes<false>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u, 1u);
+        } else {
 #pragma unroll
-        for (uint32_t b = 0; b < (uint32_t)NB; ++b)
-            stage_bytes<false>(reinterpret_cast<const uint8_t*>(x + (size_t)b * ldx), 4u * k,
-                               lbase + L.x + b * L.xrow, wave, b % NB_WAVES, 1u);
-        if constexpr (MODE == NB_NORM)
-            stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, NB % NB_WAVES, 1u);
+            for (uint32_t b = 0; b < (uint32_t)NB; ++b)
+                stage_blocks_swizzled(x + (size_t)b * ldx, nb, lbase + L.x + b * L.xrow, wave, b % NB_WAVES);
+            if constexpr (MODE == NB_NORM) stage_blocks_swizzled(nw, nb, lbase + L.nw, wave, NB % NB_WAVES);
+        }
     }
     uint32_t mine;
     if constexpr (GLU) {
@@ -2422,63 +2481,68 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
     float* asc = reinterpret_cast<float*>(base + L.scales);
     float* asm_ = reinterpret_cast<float*>(base + L.sums);
     int32_t* atot = reinterpret_cast<int32_t*>(base + L.totals);
-    if constexpr (MODE != NB_QUANT) {
-        // NORM: wave b takes Σx² of row b, lane c its chunk of 32 values
-        // (lanes past the row hold zeros); every thread takes the 4-value
-        // quarters j = t, t + 512, ... of the rows' blocks (row j / (8 nb),
-        // block j / 8 % nb, quarter j % 8), read before the quantised rows
-        // overwrite them.
-        __shared__ float roots[8];
-        constexpr uint32_t JOBS = NB * 64u * 8u / NB_THREADS;  // quarters a thread at k = 2048
-        const uint32_t jobs = NB * nb * 8u;
-        float4 xv[JOBS], wv[JOBS];
-#pragma unroll
-        for (uint32_t i = 0; i < JOBS; ++i) {
-            const uint32_t j = t + NB_THREADS * i;
-            if (j < jobs) {
-                const uint32_t b = j / (8u * nb), c = (j - b * 8u * nb) * 4u;
-                xv[i] = *reinterpret_cast<const float4*>(base + L.x + b * L.xrow + 4u * c);
-                if constexpr (MODE == NB_NORM) wv[i] = *reinterpret_cast<const float4*>(base + L.nw + 4u * c);
+    if constexpr (MODE == NB_F32 && NB == 1) {
+        // One row: the quantiser spread over the workgroup, 8 lanes a block
+        // (one wave a row would take every block's arithmetic alone), the
+        // quarters read before the quantised row overwrites them.
+        const uint32_t jobs = nb * 8u;
+        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (t < jobs) xv = *reinterpret_cast<const float4*>(base + L.x + 16u * t);
+        lds_sync();
+        if (t < jobs) {  // the same for the 8 lanes of a block (jobs a multiple of 8)
+            const Q8Quad q = quantize_quad(xv.x, xv.y, xv.z, xv.w);
+            *reinterpret_cast<uint32_t*>(aq + 4u * t) = q.packed;
+            if ((t & 7u) == 0) {
+                asc[t >> 3] = q.scale;
+                if constexpr (KIND == 2) asm_[t >> 3] = q.sum;
+                if constexpr (KIND == 1) atot[t >> 3] = q.total;
             }
         }
-        if constexpr (MODE == NB_NORM) {
-            if (wave < (uint32_t)NB) {
-                const float* xs = reinterpret_cast<const float*>(base + L.x + wave * L.xrow) + lane * 32u;
-                const bool live = lane < nb;
+    } else if constexpr (MODE != NB_QUANT) {
+        // wave b: row b, lane c its block c (lanes past the row hold zeros),
+        // its pieces read where the swizzled staging put them
+        const bool live = lane < nb;
+        float v[32], nv[32];
+        if (wave < (uint32_t)NB) {
+            const float4* xs = reinterpret_cast<const float4*>(base + L.x + wave * L.xrow) + 8u * lane;
+            const float4* ws = reinterpret_cast<const float4*>(base + L.nw) + 8u * lane;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                const uint32_t slot = (i + lane) & 7u;
+                const float4 q = live ? xs[slot] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+                if constexpr (MODE == NB_NORM) {
+                    const float4 g = live ? ws[slot] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    nv[4 * i] = g.x, nv[4 * i + 1] = g.y, nv[4 * i + 2] = g.z, nv[4 * i + 3] = g.w;
+                }
+            }
+        }
+        lds_sync();  // every row is in registers: the quantised rows may overwrite them
+        if (wave < (uint32_t)NB) {
+            if constexpr (MODE == NB_NORM) {
                 float sq[32];
 #pragma unroll
-                for (int i = 0; i < 32; i += 4) {
-                    const float4 q = live ? *reinterpret_cast<const float4*>(xs + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    sq[i] = q.x * q.x, sq[i + 1] = q.y * q.y, sq[i + 2] = q.z * q.z, sq[i + 3] = q.w * q.w;
-                }
+                for (int i = 0; i < 32; ++i) sq[i] = v[i] * v[i];
                 const float total = ordered_sum_wave<32>(sq);
-                if (lane == 0) roots[wave] = __builtin_sqrtf(total / (float)k + eps);
+                const float root = __builtin_sqrtf(total / (float)k + eps);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const float q = v[i] / root;
+                    v[i] = q * nv[i];
+                }
             }
-        }
-        lds_sync();  // the roots are in, and every value has been read
-#pragma unroll
-        for (uint32_t i = 0; i < JOBS; ++i) {
-            const uint32_t j = t + NB_THREADS * i;
-            if (j < jobs) {  // the same for the 8 lanes of a block (jobs a multiple of 8)
-                const uint32_t b = j / (8u * nb), c = (j - b * 8u * nb) * 4u, blk = c >> 5;
-                float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-                if constexpr (MODE == NB_NORM) {
-                    const float root = roots[b];
-                    const float g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float q = v[e] / root;
-                        v[e] = q * g[e];
-                    }
-                }
-                const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
-                *reinterpret_cast<uint32_t*>(aq + (size_t)b * L.arow + c) = q.packed;
-                if ((t & 7u) == 0) {
-                    const uint32_t at = b * (L.trow >> 2) + blk;
-                    asc[at] = q.scale;
-                    if constexpr (KIND == 2) asm_[at] = q.sum;
-                    if constexpr (KIND == 1) atot[at] = q.total;
-                }
+            if (live) {
+                uint32_t packed[8];
+                float scale, sum;
+                int total;
+                quantize_block32(v, packed, scale, sum, total);
+                uint4* to = reinterpret_cast<uint4*>(aq + (size_t)wave * L.arow + lane * 32u);
+                to[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                to[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+                const uint32_t at = wave * (L.trow >> 2) + lane;
+                asc[at] = scale;
+                if constexpr (KIND == 2) asm_[at] = sum;
+                if constexpr (KIND == 1) atot[at] = total;
             }
         }
     }

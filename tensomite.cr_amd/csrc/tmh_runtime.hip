@@ -734,13 +734,11 @@ int check_product(uint32_t kind, uint32_t rows, uint32_t n, uint32_t k, uint32_t
 // 8192x2048 one row 11.7 us against about 7; 2048x8192 21 against about 10).
 constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
 
-// AUTO products of 2 rows, and of one row above ROW_KERNEL_MAX_BYTES: the
-// few-rows kernel with weights in LDS, which quantises x in every
-// workgroup's prologue (k at most 2048), one launch and no scratch. From 3
-// rows the quantisation of every row by every workgroup costs more than the
-// quantise pass (measured, Q4_1 8192x2048: 6.1 / 7.7 / 9.9 / 12.6 us at 1 /
-// 2 / 4 / 8 rows, against 7.7 / 8.2 / 9.8 / 12.2 for the quantise pass and
-// the lanes product), so those take the quantise pass and the product.
+// AUTO products of 2 to 8 rows, and of one row above ROW_KERNEL_MAX_BYTES:
+// the few-rows kernel with weights in LDS, which quantises x in every
+// workgroup's prologue (k at most 2048), one launch and no scratch
+// (measured, Q4_1 8192x2048: 6.2 / 7.4 / 8.1 / 9.0 us a call at 1 / 2 / 4 / 8
+// rows, against 7.7 / 8.2 / 9.8 / 9.8 for the quantise pass and the product).
 // hipErrorInvalidValue, nothing launched, when the call is not for it.
 // TMH_FEW_ROWS_KERNEL=lanes keeps the quantise pass and the lanes product,
 // for comparisons.
@@ -751,7 +749,7 @@ hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const 
         return env && strcmp(env, "lanes") == 0;
     }();
     const uint64_t bytes = (uint64_t)n * (k / 32u) * tmh::block_bytes(kind);
-    if (lanes || mode != TMH_MODE_AUTO || rows > 2u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
+    if (lanes || mode != TMH_MODE_AUTO || rows > 8u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
         return hipErrorInvalidValue;
     return tmh::launch_rows_product(kind, tmh::NB_F32, w, x, ldx, nullptr, 0.0f, tmh::Activations{}, dst, bias, 0u,
                                     rows, n, k, d.compute_units, d.stream);
