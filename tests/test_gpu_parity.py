@@ -243,6 +243,37 @@ def test_few_rows_weights_in_lds(dev, fmt, k):
         assert np.array_equal(bits(got), bits(want[:rows])), rows
 
 
+def same_or_both_nan(got, want):
+    g, w = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan = np.isnan(w)
+    return np.array_equal(np.isnan(g), nan) and np.array_equal(bits(g[~nan]), bits(w[~nan]))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_few_rows_nan_and_inf_blocks(dev, fmt):
+    # The host's amax is taken in index order and skips a NaN unless it is the
+    # block's first value (quant.cr:428-442); the few-rows kernel's lane-a-
+    # block quantiser takes it as a tree. Blocks with a NaN first, a NaN in
+    # the middle, and an inf, in every row count of the one-launch form.
+    n, k = 700, 512
+    wq = weights(fmt, n, k, 41)
+    x = acts(8, k, 42)
+    for r in range(8):
+        x[r * k + 32 * 9 + 5 + r] = np.nan  # inside a block: skipped by amax, quantised to 0
+        x[r * k + 32 * 3 + 31 - r] = np.nan
+    x[4 * k + 32 * 6] = np.nan  # first in its block: the block's scale is NaN
+    x[5 * k + 32 * 2] = np.nan
+    x[6 * k + 32 * 12 + 6] = np.inf
+    x[7 * k + 32 * 1] = -np.inf
+    want = oracle.matmul(fmt, x, wq, 8, n, k)
+    wbuf, xbuf = dev.from_array(wq), dev.from_array(x)
+    for rows in range(1, 9):
+        say("nan rows", fmt, rows)
+        out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k)
+        got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
+        assert same_or_both_nan(got, want[:rows]), rows
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_special_rows(dev, fmt):
     # quant_spec.cr:30-48 on the device: zero first block, a spike of 50, a
