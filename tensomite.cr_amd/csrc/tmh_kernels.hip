@@ -2397,6 +2397,46 @@ __device__ __forceinline__ void quantize_block32(const float (&v)[32], uint32_t 
     sum = round_to_half((float)tot * d);
 }
 
+// 8 bytes at byte address p in LDS, p any alignment (three dword reads
+// and two byte funnels; the dword after them must lie in LDS).
+__device__ __forceinline__ void lds_read8(const uint8_t* p, uint32_t& lo, uint32_t& hi) {
+    const uint32_t s = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - s);
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+    lo = funnel(d1, d0, s), hi = funnel(d2, d1, s);
+}
+
+// The 16 values of half h of block b of a weight row (LDS) as one lane's
+// v_mfma_i32_16x16x64_i8 operand: values 8h .. 8h + 7 and 16 + 8h .. 16 +
+// 8h + 7 (Q4: bytes 8h .. 8h + 7 of the nibbles, low then high; Q8_0 the
+// two runs of bytes), in that order; pair_acts takes the activations alike.
+template <int KIND>
+__device__ __forceinline__ v4i pair_weights(const uint8_t* row, uint32_t b, uint32_t h) {
+    uint32_t x0, x1;
+    if constexpr (KIND == 0) {
+        const uint8_t* q = row + 34u * b + 2u + 8u * h;
+        uint32_t y0, y1;
+        lds_read8(q, x0, x1);
+        lds_read8(q + 16, y0, y1);
+        return v4i{(int)x0, (int)x1, (int)y0, (int)y1};
+    } else {
+        if constexpr (KIND == 1) {
+            lds_read8(row + 18u * b + 2u + 8u * h, x0, x1);
+        } else {
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(row + 20u * b + 4u + 8u * h);
+            x0 = q[0], x1 = q[1];
+        }
+        return v4i{(int)(x0 & 0x0f0f0f0fu), (int)(x1 & 0x0f0f0f0fu), (int)((x0 >> 4) & 0x0f0f0f0fu),
+                   (int)((x1 >> 4) & 0x0f0f0f0fu)};
+    }
+}
+
+__device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_t h) {
+    const uint2 lo = *reinterpret_cast<const uint2*>(row + 32u * b + 8u * h);
+    const uint2 hi = *reinterpret_cast<const uint2*>(row + 32u * b + 16u + 8u * h);
+    return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+}
+
 // NB (at most 16) activation rows times a tile of `tr` weight rows per
 // workgroup, the tile's weights direct-loaded into LDS at the start (as
 // k_matvec_one does for one row). Every wave issues its share of the
@@ -2570,6 +2610,74 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
             const uint32_t cl = min(chunk, nb - q0);  // blocks of this chunk, a multiple of 8
             const uint32_t u0 = NB_PER * wave;        // this wave's first block of the chunk
             if (u0 < cl) {
+              if constexpr (NB <= 8) {
+                // Pairs of blocks on v_mfma_i32_16x16x64_i8: A is the tile's 16
+                // weight rows (lane (m, g): row m, half g % 2 of block g / 2 of
+                // the pair), B's 16 columns n = b + 8 j are activation row b in
+                // block j of the pair (lane (n, g): zero unless g / 2 == j), so
+                // D[m][n] is weight row m's dot product with row b over block j
+                // alone. A lane's outputs: weight rows 4 g + i of column n.
+                const uint32_t jj = lq >> 1, hh = lq & 1u, ab = lr & 7u, aj = lr >> 3;
+                const bool breal = ab < (uint32_t)NB && aj == jj;
+                const uint8_t* brow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(ab, (uint32_t)NB - 1u) * L.arow;
+                v4i av[4], bv[4];
+                uint32_t dm[4][4];
+                float sx[4], ex[4];
+#pragma unroll
+                for (uint32_t p = 0; p < 4; ++p) {
+                    const uint32_t b = q0 + u0 + 2u * p;  // the pair's first block
+                    av[p] = pair_weights<KIND>(wrow, b + jj, hh);
+                    const v4i x = pair_acts(brow, b + aj, hh);  // brow clamped: a valid row
+                    bv[p] = breal ? x : v4i{0, 0, 0, 0};
+                    const uint32_t at = min(ab, (uint32_t)NB - 1u) * tstride + b + aj;
+                    sx[p] = asc[at];
+                    ex[p] = 0.0f;
+                    if constexpr (KIND == 2) ex[p] = asm_[at];
+                    if constexpr (KIND == 1) ex[p] = __int_as_float(-8 * atot[at]);
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; ++i) {
+                        const uint32_t r = min(16u * c + 4u * lq + i, rows - 1u);
+                        const uint8_t* rp = GLU ? (r < h ? base + L.w + r * wstride : base + L.w2 + (r - h) * wstride)
+                                                : base + L.w + r * wstride;
+                        if constexpr (KIND == 2) dm[p][i] = *reinterpret_cast<const uint32_t*>(rp + 20u * (b + aj));
+                        else dm[p][i] = *reinterpret_cast<const uint16_t*>(rp + BB * (b + aj));
+                    }
+                }
+                v4i tv[4];
+#pragma unroll
+                for (uint32_t p = 0; p < 4; ++p) {
+                    v4i cin = {0, 0, 0, 0};
+                    if constexpr (KIND == 1) {
+                        const int neg8 = __float_as_int(ex[p]);
+                        cin = v4i{neg8, neg8, neg8, neg8};
+                    }
+                    tv[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[p], bv[p], cin, 0, 0, 0);
+                }
+                if (ab < (uint32_t)NB) {
+#pragma unroll
+                    for (uint32_t p = 0; p < 4; ++p) {
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; ++i) {
+                            const float ft = (float)tv[p][i], d = half_value(dm[p][i] & 0xffffu);
+                            float cv;
+                            if constexpr (KIND == 0) {
+                                const float sc = d * sx[p];
+                                cv = ft * sc;
+                            } else if constexpr (KIND == 1) {
+                                const float pr = ft * d;
+                                cv = pr * sx[p];
+                            } else {
+                                const float sc = d * sx[p];
+                                const float f = sc * ft;
+                                const float g = half_value(dm[p][i] >> 16) * ex[p];
+                                cv = f + g;
+                            }
+                            if (16u * c + 4u * lq + i < rows)
+                                part[(ab * 17u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
+                        }
+                    }
+                }
+              } else {
                 // Every operand read of the wave's 8 blocks first, then the
                 // MFMAs, then the contributions.
                 typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
@@ -2652,6 +2760,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                         }
                     }
                 }
+                          }
             }
             lds_sync();
             if (fb < (uint32_t)NB && 16u * c + fr < rows) {
