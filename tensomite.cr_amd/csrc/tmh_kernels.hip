@@ -2673,7 +2673,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                                 cv = f + g;
                             }
                             if (16u * c + 4u * lq + i < rows)
-                                part[(ab * 17u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
+                                part[(ab * 16u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
                         }
                     }
                 }
