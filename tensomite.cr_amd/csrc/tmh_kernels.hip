@@ -2261,8 +2261,8 @@ static_assert(NB_PER == 8, "a wave's blocks of a chunk: two 16-byte table reads 
 //            the prologue reads them; then (and for QUANT from the start)
 //            the quantised rows qs [NB][k] and their tables [NB][nb]
 //            (scales; Q4_1 sums; Q4_0 totals), the contributions part
-//            [NB][16][pstride] of one tile of 16 weight rows and one chunk
-//            of blocks, and the GLU outputs;
+//            [tpp][NB][16][pstride] of the tpp tiles of 16 weight rows of a
+//            phase and one chunk of blocks, and the GLU outputs;
 //   [w, end) the weight tile, direct-loaded (GLU: its gate rows at w, its
 //            up rows at w2).
 struct NbLds {
@@ -2280,7 +2280,7 @@ __host__ __device__ inline uint32_t nb_row_stride(uint32_t bytes) {
 }
 
 __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint32_t row_bytes,
-                                        uint32_t mode, bool glu) {
+                                        uint32_t mode, bool glu, uint32_t tpp = 1u) {
     const uint32_t nb = k >> 5;
     auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
     NbLds l;
@@ -2294,7 +2294,7 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     const uint32_t act_end = l.totals + (kind == 1 ? tab : 0u);
     l.pstride = ((nb < NB_CHUNK ? nb : NB_CHUNK) + 3u) / 4u * 4u + 4u;  // 16-byte rows, apart by 4 banks
     l.part = act_end;
-    l.outs = l.part + 4u * nbatch * 16u * l.pstride;
+    l.outs = l.part + 4u * tpp * nbatch * 16u * l.pstride;
     const uint32_t outs_end = l.outs + (glu ? 4u * nbatch * (tr + tr / 2u) : 0u);
     l.x = 0;
     l.xrow = kb(4u * k);  // whole kilobytes: a row's last direct load may write past its end
@@ -2468,7 +2468,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                                                           uint32_t ldx, const float* __restrict__ nw, float eps,
                                                           Activations act, float* __restrict__ dst,
                                                           const float* __restrict__ bias, uint32_t bias_ld, uint32_t n,
-                                                          uint32_t k, uint32_t tr, Activations glu) {
+                                                          uint32_t k, uint32_t tr, uint32_t tpp, Activations glu) {
     static_assert(NB >= 1 && NB <= 16 && (MODE == NB_QUANT || NB <= 8), "activation rows of a launch");
     extern __shared__ float4 lds4[];
     uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
@@ -2477,7 +2477,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
     const uint32_t nb = k >> 5, row_bytes = nb * BB;
     const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
     const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
-    const NbLds L = nb_lds(NB, KIND, k, tr, row_bytes, MODE, GLU);
+    const NbLds L = nb_lds(NB, KIND, k, tr, row_bytes, MODE, GLU, tpp);
     const uint32_t lbase = lds_address(base);
 
     // Activations first, every wave its share, then the weights.
@@ -2599,12 +2599,18 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
     const uint8_t* arow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(lr, (uint32_t)NB - 1u) * L.arow;
     const uint32_t tstride = L.trow >> 2, wstride = L.wrow;
     const bool alive = lr < (uint32_t)NB;
-    const uint32_t fb = t >> 4, fr = t & 15u;  // the output this thread adds up: row fb, weight row 16·c + fr
-    for (uint32_t c = 0; c * 16u < rows; ++c) {
+    // A phase takes tpp tiles of 16 weight rows (2 only up to 8 rows): the
+    // output this thread adds up is row fb, weight row 16·(c + ft) + fr.
+    const uint32_t ft = tpp > 1u ? t >> 7 : 0u;
+    const uint32_t fb = tpp > 1u ? (t >> 4) & 7u : t >> 4, fr = t & 15u;
+    const uint32_t tile_floats = (uint32_t)NB * 16u * pstride;
+    for (uint32_t c = 0; c * 16u < rows; c += tpp) {
         const uint32_t wr = min(16u * c + lr, rows - 1u);  // a clamped row's contributions are not written
         const uint8_t* wrow = GLU ? (wr < h ? base + L.w + wr * wstride : base + L.w2 + (wr - h) * wstride)
                                   : base + L.w + wr * wstride;
         const bool wlive = 16u * c + lr < rows;
+        const uint32_t fc = c + ft;  // the tile of this thread's output
+        const bool folds = ft < tpp && fb < (uint32_t)NB && 16u * fc + fr < rows;
         float acc = 0.0f;
         for (uint32_t q0 = 0; q0 < nb; q0 += chunk) {
             const uint32_t cl = min(chunk, nb - q0);  // blocks of this chunk, a multiple of 8
@@ -2620,13 +2626,21 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                 const uint32_t jj = lq >> 1, hh = lq & 1u, ab = lr & 7u, aj = lr >> 3;
                 const bool breal = ab < (uint32_t)NB && aj == jj;
                 const uint8_t* brow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(ab, (uint32_t)NB - 1u) * L.arow;
+#pragma unroll
+                for (uint32_t tt = 0; tt < 2u; ++tt) {
+                const uint32_t ct = c + tt;
+                if (tt >= tpp || ct * 16u >= rows) break;
+                const uint32_t wrt = min(16u * ct + lr, rows - 1u);
+                const uint8_t* trow = GLU ? (wrt < h ? base + L.w + wrt * wstride : base + L.w2 + (wrt - h) * wstride)
+                                          : base + L.w + wrt * wstride;
+                float* tpart = part + tt * tile_floats;
                 v4i av[4], bv[4];
                 uint32_t dm[4][4];
                 float sx[4], ex[4];
 #pragma unroll
                 for (uint32_t p = 0; p < 4; ++p) {
                     const uint32_t b = q0 + u0 + 2u * p;  // the pair's first block
-                    av[p] = pair_weights<KIND>(wrow, b + jj, hh);
+                    av[p] = pair_weights<KIND>(trow, b + jj, hh);
                     const v4i x = pair_acts(brow, b + aj, hh);  // brow clamped: a valid row
                     bv[p] = breal ? x : v4i{0, 0, 0, 0};
                     const uint32_t at = min(ab, (uint32_t)NB - 1u) * tstride + b + aj;
@@ -2636,7 +2650,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                     if constexpr (KIND == 1) ex[p] = __int_as_float(-8 * atot[at]);
 #pragma unroll
                     for (uint32_t i = 0; i < 4; ++i) {
-                        const uint32_t r = min(16u * c + 4u * lq + i, rows - 1u);
+                        const uint32_t r = min(16u * ct + 4u * lq + i, rows - 1u);
                         const uint8_t* rp = GLU ? (r < h ? base + L.w + r * wstride : base + L.w2 + (r - h) * wstride)
                                                 : base + L.w + r * wstride;
                         if constexpr (KIND == 2) dm[p][i] = *reinterpret_cast<const uint32_t*>(rp + 20u * (b + aj));
@@ -2672,10 +2686,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                                 const float g = half_value(dm[p][i] >> 16) * ex[p];
                                 cv = f + g;
                             }
-                            if (16u * c + 4u * lq + i < rows)
-                                part[(ab * 16u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
+                            if (16u * ct + 4u * lq + i < rows)
+                                tpart[(ab * 16u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
                         }
                     }
+                }
                 }
               } else {
                 // Every operand read of the wave's 8 blocks first, then the
@@ -2763,10 +2778,10 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                           }
             }
             lds_sync();
-            if (fb < (uint32_t)NB && 16u * c + fr < rows) {
+            if (folds) {
                 // the chunk's contributions in block order, read 32 at a
                 // time into registers before they are added
-                const float* cp = part + (fb * 16u + fr) * pstride;
+                const float* cp = part + ft * tile_floats + (fb * 16u + fr) * pstride;
                 uint32_t i = 0;
                 for (; i + 32u <= cl; i += 32u) {
                     float2 vv[16];
@@ -2782,8 +2797,8 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
             }
             lds_sync();
         }
-        if (fb < (uint32_t)NB && 16u * c + fr < rows) {
-            const uint32_t r = 16u * c + fr;
+        if (folds) {
+            const uint32_t r = 16u * fc + fr;
             if constexpr (GLU) {
                 outs[fb * tr + r] = acc;
             } else {
@@ -3647,16 +3662,32 @@ static uint32_t nb_tile(uint32_t n, uint32_t k, int compute_units) {
     return std::max(1u, (uint32_t)((n + cus * rounds - 1u) / (cus * rounds)));
 }
 
+// Tiles of 16 weight rows a phase of k_matvec_nb: two (every wave's pairs
+// of both, one barrier pair and one fold pass for both) up to 8 rows where
+// the tile has more than 16 rows and the second contributions region fits
+// the LDS limit, else one. TMH_NB_TPP=1 keeps one, for measurement.
+static uint32_t nb_tpp(int nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint32_t row_bytes, uint32_t mode,
+                       bool glu) {
+    static const bool on = [] {
+        const char* env = getenv("TMH_NB_TPP");
+        return !(env && strcmp(env, "1") == 0);
+    }();
+    return on && nbatch <= 8 && tr > 16u && nb_lds(nbatch, kind, k, tr, row_bytes, mode, glu, 2u).end <= ONE_LDS_LIMIT
+               ? 2u
+               : 1u;
+}
+
 template <int KIND, uint32_t MODE, int NB>
 static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
                             Activations act, float* dst, const float* bias, uint32_t bias_ld, uint32_t n, uint32_t k,
                             int compute_units, hipStream_t stream) {
     const uint32_t nb = k >> 5;
     const uint32_t tr = nb_tile<KIND, MODE, NB>(n, k, compute_units);
-    const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false);
+    const uint32_t tpp = nb_tpp(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false);
+    const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NB_THREADS), L.end,
-                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, Activations{});
+                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, Activations{});
     return hipGetLastError();
 }
 
@@ -3740,9 +3771,10 @@ template <int KIND, uint32_t MODE, int NB>
 static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
                                 Activations act, uint32_t H, uint32_t k, Activations glu, hipStream_t stream) {
     const uint32_t nb = k >> 5, h = NB_GLU_HALF;
-    const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
+    const uint32_t tpp = nb_tpp(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
+    const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
     hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NB_THREADS), L.end, stream, w, x, ldx, nw,
-                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, glu);
+                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, glu);
     return hipGetLastError();
 }
 
