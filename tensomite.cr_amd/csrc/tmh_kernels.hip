@@ -2255,6 +2255,18 @@ constexpr uint32_t NB_WAVES = NB_THREADS / 64u;
 constexpr uint32_t NB_CHUNK = 64;
 constexpr uint32_t NB_PER = NB_CHUNK / NB_WAVES;
 static_assert(NB_PER == 8, "a wave's blocks of a chunk: two 16-byte table reads and writes");
+// One or two rows: 16 waves a workgroup, four a SIMD, each with 4 blocks
+// (2 pairs) of a chunk, so that a SIMD has more waves to hide each one's LDS
+// reads and MFMA results (measured, config 3 8192x2048: B = 1 and 2 0.25 us
+// faster a call, B = 4 the same, B = 8 0.15 us slower); else 8 waves of 8
+// blocks.
+template <int NB>
+struct NbShape {
+    static constexpr uint32_t THREADS = NB <= 2 ? 1024u : NB_THREADS;
+    static constexpr uint32_t WAVES = THREADS / 64u;
+    static constexpr uint32_t PER = NB_CHUNK / WAVES;  // blocks of a chunk a wave
+    static_assert(PER % 2u == 0 && PER <= 8u, "whole pairs, at most 4 a wave");
+};
 
 // LDS of k_matvec_nb in bytes from the start of its dynamic LDS:
 //   [0, w)   F32/NORM: the f32 rows [NB][xrow] and the norm's weights while
@@ -2456,20 +2468,21 @@ __device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_
 // (few_acts, few_weights; Q4_0's -8·Σq as C); each (row, output, block)
 // contribution is formed in the host's expression (Q8_0 float(t)·(d·sx);
 // Q4_0 (float(t)·d)·sx; Q4_1 (d·sx)·float(t) + m·mx) and written to LDS, a
-// chunk of NB_CHUNK blocks at a time, wave v taking blocks v, v + 8, ...;
-// then thread b·16 + r adds output (b, r)'s contributions of the chunk in
-// block order to its running sum (quant.cr:447-455). dst[b][row] = Σ (+
-// bias[b · bias_ld + row], one rounding); GLU: SwiGLU and the quantiser on
-// the tile's gate/up outputs into glu, as k_matvec_one. Each output depends
-// on its own activation row only, so the bits are those of one row at a
-// time.
+// chunk of NB_CHUNK blocks at a time, each wave a run of consecutive blocks
+// of the chunk; then one thread an output adds the output's contributions of
+// the chunk in block order to its running sum (quant.cr:447-455).
+// dst[b][row] = Σ (+ bias[b · bias_ld + row], one rounding); GLU: SwiGLU and
+// the quantiser on the tile's gate/up outputs into glu, as k_matvec_one. Each
+// output depends on its own activation row only, so the bits are those of one
+// row at a time.
 template <int KIND, uint32_t MODE, bool GLU, int NB>
-__global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                          uint32_t ldx, const float* __restrict__ nw, float eps,
-                                                          Activations act, float* __restrict__ dst,
-                                                          const float* __restrict__ bias, uint32_t bias_ld, uint32_t n,
-                                                          uint32_t k, uint32_t tr, uint32_t tpp, Activations glu) {
+__global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
+    const uint8_t* __restrict__ w, const float* __restrict__ x, uint32_t ldx, const float* __restrict__ nw, float eps,
+    Activations act, float* __restrict__ dst, const float* __restrict__ bias, uint32_t bias_ld, uint32_t n, uint32_t k,
+    uint32_t tr, uint32_t tpp, Activations glu) {
     static_assert(NB >= 1 && NB <= 16 && (MODE == NB_QUANT || NB <= 8), "activation rows of a launch");
+    constexpr uint32_t WAVES = NbShape<NB>::WAVES, THREADS = NbShape<NB>::THREADS, PER = NbShape<NB>::PER;
+    constexpr uint32_t PP = PER / 2u;  // pairs of a chunk a wave (up to 8 rows)
     extern __shared__ float4 lds4[];
     uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
     constexpr uint32_t BB = Fmt<KIND>::BB;
@@ -2485,34 +2498,34 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
         // rows and tables contiguous (the quantise pass's layout); NB·nb a
         // multiple of 4 and the tables 16-byte aligned
         stage_rows<false>(reinterpret_cast<const uint8_t*>(act.qs), k, k, NB, lbase + L.qs, L.arow, wave, 0u,
-                          NB_WAVES);
+                          WAVES);
         stage_rows<false>(reinterpret_cast<const uint8_t*>(act.scales), 4u * nb, 4u * nb, NB, lbase + L.scales, L.trow,
-                          wave, 0u, NB_WAVES);
+                          wave, 0u, WAVES);
         if constexpr (KIND == 2)
             stage_rows<false>(reinterpret_cast<const uint8_t*>(act.sums), 4u * nb, 4u * nb, NB, lbase + L.sums, L.trow,
-                              wave, 0u, NB_WAVES);
+                              wave, 0u, WAVES);
         if constexpr (KIND == 1)
             stage_rows<false>(reinterpret_cast<const uint8_t*>(act.totals), 4u * nb, 4u * nb, NB, lbase + L.totals,
-                              L.trow, wave, 0u, NB_WAVES);
+                              L.trow, wave, 0u, WAVES);
     } else {
         if constexpr (MODE == NB_F32 && NB == 1) {
             stage_bytes<false>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u, 1u);
         } else {
 #pragma unroll
             for (uint32_t b = 0; b < (uint32_t)NB; ++b)
-                stage_blocks_swizzled(x + (size_t)b * ldx, nb, lbase + L.x + b * L.xrow, wave, b % NB_WAVES);
-            if constexpr (MODE == NB_NORM) stage_blocks_swizzled(nw, nb, lbase + L.nw, wave, NB % NB_WAVES);
+                stage_blocks_swizzled(x + (size_t)b * ldx, nb, lbase + L.x + b * L.xrow, wave, b % WAVES);
+            if constexpr (MODE == NB_NORM) stage_blocks_swizzled(nw, nb, lbase + L.nw, wave, NB % WAVES);
         }
     }
     uint32_t mine;
     if constexpr (GLU) {
         mine = stage_rows<true>(w + (size_t)g0 * row_bytes, row_bytes, row_bytes, h, lbase + L.w, L.wrow, wave, 0u,
-                                NB_WAVES);
+                                WAVES);
         mine += stage_rows<true>(w + (size_t)(H + g0) * row_bytes, row_bytes, row_bytes, h, lbase + L.w2, L.wrow, wave,
-                                 0u, NB_WAVES);
+                                 0u, WAVES);
     } else {
         mine = stage_rows<true>(w + (size_t)row0 * row_bytes, row_bytes, row_bytes, rows, lbase + L.w, L.wrow, wave,
-                                0u, NB_WAVES);
+                                0u, WAVES);
     }
     wait_vm_lds_upto(mine);  // this wave's activation loads (issued before its weights) have landed
     lds_sync();
@@ -2614,7 +2627,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
         float acc = 0.0f;
         for (uint32_t q0 = 0; q0 < nb; q0 += chunk) {
             const uint32_t cl = min(chunk, nb - q0);  // blocks of this chunk, a multiple of 8
-            const uint32_t u0 = NB_PER * wave;        // this wave's first block of the chunk
+            const uint32_t u0 = PER * wave;           // this wave's first block of the chunk
             if (u0 < cl) {
               if constexpr (NB <= 8) {
                 // Pairs of blocks on v_mfma_i32_16x16x64_i8: A is the tile's 16
@@ -2634,11 +2647,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                 const uint8_t* trow = GLU ? (wrt < h ? base + L.w + wrt * wstride : base + L.w2 + (wrt - h) * wstride)
                                           : base + L.w + wrt * wstride;
                 float* tpart = part + tt * tile_floats;
-                v4i av[4], bv[4];
-                uint32_t dm[4][4];
-                float sx[4], ex[4];
+                v4i av[PP], bv[PP];
+                uint32_t dm[PP][4];
+                float sx[PP], ex[PP];
 #pragma unroll
-                for (uint32_t p = 0; p < 4; ++p) {
+                for (uint32_t p = 0; p < PP; ++p) {
                     const uint32_t b = q0 + u0 + 2u * p;  // the pair's first block
                     av[p] = pair_weights<KIND>(trow, b + jj, hh);
                     const v4i x = pair_acts(brow, b + aj, hh);  // brow clamped: a valid row
@@ -2657,9 +2670,9 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                         else dm[p][i] = *reinterpret_cast<const uint16_t*>(rp + BB * (b + aj));
                     }
                 }
-                v4i tv[4];
+                v4i tv[PP];
 #pragma unroll
-                for (uint32_t p = 0; p < 4; ++p) {
+                for (uint32_t p = 0; p < PP; ++p) {
                     v4i cin = {0, 0, 0, 0};
                     if constexpr (KIND == 1) {
                         const int neg8 = __float_as_int(ex[p]);
@@ -2669,7 +2682,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                 }
                 if (ab < (uint32_t)NB) {
 #pragma unroll
-                    for (uint32_t p = 0; p < 4; ++p) {
+                    for (uint32_t p = 0; p < PP; ++p) {
 #pragma unroll
                         for (uint32_t i = 0; i < 4; ++i) {
                             const float ft = (float)tv[p][i], d = half_value(dm[p][i] & 0xffffu);
@@ -2697,11 +2710,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                 // MFMAs, then the contributions.
                 typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
                 typedef int i4a __attribute__((ext_vector_type(4), aligned(16)));
-                long av[NB_PER], bv[NB_PER];
-                uint32_t dm[NB_PER];
-                float sx[4][NB_PER], ex[4][NB_PER];
+                long av[PER], bv[PER];
+                uint32_t dm[PER];
+                float sx[4][PER], ex[4][PER];
 #pragma unroll
-                for (uint32_t p = 0; p < NB_PER; ++p) {
+                for (uint32_t p = 0; p < PER; ++p) {
                     const uint32_t b = q0 + u0 + p;  // of p's parity (q0, u0 even)
                     const long a = few_acts<KIND>(arow, b, lq);  // arow clamped: a valid row
                     av[p] = alive ? a : 0l;
@@ -2731,9 +2744,9 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                             ex[i][e] = __int_as_float(-8 * e0[e]), ex[i][4 + e] = __int_as_float(-8 * e1[e]);
                     }
                 }
-                v4i tv[NB_PER];
+                v4i tv[PER];
 #pragma unroll
-                for (uint32_t p = 0; p < NB_PER; ++p) {
+                for (uint32_t p = 0; p < PER; ++p) {
                     v4i cin = {0, 0, 0, 0};
                     if constexpr (KIND == 1) {
 #pragma unroll
@@ -2741,9 +2754,9 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
                     }
                     tv[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[p], bv[p], cin, 0, 0, 0);
                 }
-                float cv[4][NB_PER];
+                float cv[4][PER];
 #pragma unroll
-                for (uint32_t p = 0; p < NB_PER; ++p) {
+                for (uint32_t p = 0; p < PER; ++p) {
                     const float d = half_value(dm[p] & 0xffffu);
                     const float m = KIND == 2 ? half_value(dm[p] >> 16) : 0.0f;
 #pragma unroll
@@ -2811,13 +2824,13 @@ __global__ __launch_bounds__(NB_THREADS) void k_matvec_nb(const uint8_t* __restr
         // SwiGLU one output a thread, then the quantiser, 8 lanes a block
         lds_sync();
         float* act_out = outs + NB * tr;
-        for (uint32_t o = t; o < (uint32_t)NB * h; o += NB_THREADS) {
+        for (uint32_t o = t; o < (uint32_t)NB * h; o += THREADS) {
             const uint32_t b = o / h, i = o - b * h;
             act_out[o] = swiglu_value(outs[b * tr + i], outs[b * tr + h + i]);
         }
         lds_sync();
         const uint32_t hb = h >> 5, Hb = H >> 5, sub = t & 7u;
-        for (uint32_t g = t >> 3; g < (uint32_t)NB * hb; g += NB_THREADS / 8u) {  // uniform across each 8-lane group
+        for (uint32_t g = t >> 3; g < (uint32_t)NB * hb; g += THREADS / 8u) {  // uniform across each 8-lane group
             const uint32_t b = g / hb, blk = g - b * hb;
             const float4 v4 = *reinterpret_cast<const float4*>(act_out + b * h + blk * 32u + sub * 4u);
             const Q8Quad q = quantize_quad(v4.x, v4.y, v4.z, v4.w);
@@ -3686,7 +3699,7 @@ static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, cons
     const uint32_t tpp = nb_tpp(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false);
     const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NB_THREADS), L.end,
+    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS), L.end,
                        stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, Activations{});
     return hipGetLastError();
 }
@@ -3773,7 +3786,8 @@ static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, 
     const uint32_t nb = k >> 5, h = NB_GLU_HALF;
     const uint32_t tpp = nb_tpp(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
     const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
-    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NB_THREADS), L.end, stream, w, x, ldx, nw,
+    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream, w, x,
+                       ldx, nw,
                        eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, glu);
     return hipGetLastError();
 }
