@@ -2273,12 +2273,13 @@ struct NbShape {
 //            the prologue reads them; then (and for QUANT from the start)
 //            the quantised rows qs [NB][k] and their tables [NB][nb]
 //            (scales; Q4_1 sums; Q4_0 totals), the contributions part
-//            [tpp][NB][16][pstride] of the tpp tiles of 16 weight rows of a
-//            phase and one chunk of blocks, and the GLU outputs;
+//            [tpp][NB][prow] ([rt][pstride] and a skew) of the tpp tiles of
+//            16 weight rows of a phase and one chunk of blocks, and the GLU
+//            outputs;
 //   [w, end) the weight tile, direct-loaded (GLU: its gate rows at w, its
 //            up rows at w2).
 struct NbLds {
-    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, outs, w, w2, wrow, end;
+    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, rt, prow, outs, w, w2, wrow, end;
 };
 
 // The LDS stride of rows of `bytes` bytes (a multiple of 16) read 16 rows at
@@ -2305,14 +2306,25 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     l.totals = l.sums + (kind == 2 ? tab : 0u);
     const uint32_t act_end = l.totals + (kind == 1 ? tab : 0u);
     l.pstride = ((nb < NB_CHUNK ? nb : NB_CHUNK) + 3u) / 4u * 4u + 4u;  // 16-byte rows, apart by 4 banks
+    // An activation row's contribution rows (16; 8 for a tile of at most 8
+    // weight rows), then a skew: 16·pstride is a multiple of the 64 banks,
+    // so without it the pair MFMAs' writes of 8 activation rows (a lane's
+    // row b, weight row 4 g + i, block j: bank 16 g + j + b·(prow mod 64))
+    // would meet on 8 banks; 2 floats spread them over all 64 (8 rows:
+    // b·34 + 16 g + j, 32 lanes on distinct banks). From 9 rows the writes
+    // are 16-byte vectors: a skew of 4 floats.
+    l.rt = tr <= 8u ? 8u : 16u;
+    l.prow = l.rt * l.pstride + (nbatch <= 8u ? 2u : 4u);
     l.part = act_end;
-    l.outs = l.part + 4u * tpp * nbatch * 16u * l.pstride;
+    l.outs = l.part + 4u * tpp * nbatch * l.prow;
     const uint32_t outs_end = l.outs + (glu ? 4u * nbatch * (tr + tr / 2u) : 0u);
     l.x = 0;
     l.xrow = kb(4u * k);  // whole kilobytes: a row's last direct load may write past its end
     l.nw = nbatch * l.xrow;
     const uint32_t x_end = mode == NB_QUANT ? 0u : l.nw + (mode == NB_NORM ? kb(4u * k) : 0u);
-    l.w = kb(x_end > outs_end ? x_end : outs_end);
+    // the weight tile's direct loads fill whole kilobytes from its start,
+    // which needs 16-byte alignment only (x_end is whole kilobytes)
+    l.w = ((x_end > outs_end ? x_end : outs_end) + 255u) & ~255u;
     l.wrow = nb_row_stride(row_bytes);
     const uint32_t half = kb((tr / 2u) * l.wrow);
     l.w2 = glu ? l.w + half : l.w;
@@ -2616,7 +2628,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     // output this thread adds up is row fb, weight row 16·(c + ft) + fr.
     const uint32_t ft = tpp > 1u ? t >> 7 : 0u;
     const uint32_t fb = tpp > 1u ? (t >> 4) & 7u : t >> 4, fr = t & 15u;
-    const uint32_t tile_floats = (uint32_t)NB * 16u * pstride;
+    const uint32_t prow = L.prow, tile_floats = (uint32_t)NB * prow;
     for (uint32_t c = 0; c * 16u < rows; c += tpp) {
         const uint32_t wr = min(16u * c + lr, rows - 1u);  // a clamped row's contributions are not written
         const uint8_t* wrow = GLU ? (wr < h ? base + L.w + wr * wstride : base + L.w2 + (wr - h) * wstride)
@@ -2700,7 +2712,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                                 cv = f + g;
                             }
                             if (16u * ct + 4u * lq + i < rows)
-                                tpart[(ab * 16u + 4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
+                                tpart[ab * prow + (4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
                         }
                     }
                 }
@@ -2780,7 +2792,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         if (4u * lq + i < (uint32_t)NB) {
-                            f4a* to = reinterpret_cast<f4a*>(part + ((4u * lq + i) * 16u + lr) * pstride + u0);
+                            f4a* to = reinterpret_cast<f4a*>(part + (4u * lq + i) * prow + lr * pstride + u0);
                             const f4a c0 = {cv[i][0], cv[i][1], cv[i][2], cv[i][3]};
                             const f4a c1 = {cv[i][4], cv[i][5], cv[i][6], cv[i][7]};
                             to[0] = c0;
@@ -2794,7 +2806,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
             if (folds) {
                 // the chunk's contributions in block order, read 32 at a
                 // time into registers before they are added
-                const float* cp = part + ft * tile_floats + (fb * 16u + fr) * pstride;
+                const float* cp = part + ft * tile_floats + fb * prow + fr * pstride;
                 uint32_t i = 0;
                 for (; i + 32u <= cl; i += 32u) {
                     float2 vv[16];
