@@ -704,7 +704,14 @@ __device__ void attend_staged(const AttDecodeLds& l, const float* __restrict__ k
             for (uint32_t c = tid; c < width; c += 256u) l.kt[att_key_at((uint32_t)(cur - (int32_t)p0) * width + c)] = l.kcur[c];
             lds_sync();
         }
-        for (uint32_t pl = tid; pl < cnt; pl += 256u) {
+        // Thread -> position: lane l of a wave takes position 4 (l % 16) +
+        // l / 16 of the wave's 64, so the 16 lanes an LDS pass serves read
+        // 16 different 1 KB pieces (1040 bytes apart: distinct 4-bank
+        // groups); lane l -> position l would put a piece's four rows, 256
+        // bytes apart and so on the same banks, in one pass. Any order of
+        // the positions gives the same scores.
+        const uint32_t mine = (tid & ~63u) + 4u * (tid & 15u) + ((tid >> 4) & 3u);
+        for (uint32_t pl = mine; pl < cnt; pl += 256u) {
             const uint32_t p = p0 + pl;
             float dot = 0.0f;
             if (width == 64u) {
