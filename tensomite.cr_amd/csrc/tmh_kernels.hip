@@ -2273,13 +2273,15 @@ struct NbShape {
 //            the prologue reads them; then (and for QUANT from the start)
 //            the quantised rows qs [NB][k] and their tables [NB][nb]
 //            (scales; Q4_1 sums; Q4_0 totals), the contributions part
-//            [tpp][NB][prow] ([rt][pstride] and a skew) of the tpp tiles of
-//            16 weight rows of a phase and one chunk of blocks, and the GLU
-//            outputs;
+//            [bufs][tpp][NB][prow] ([rt][pstride] and a skew) of the tpp
+//            tiles of 16 weight rows of a phase and one chunk of blocks (two
+//            buffers: a phase's fold runs while the next one's contributions
+//            are formed), and the GLU outputs;
 //   [w, end) the weight tile, direct-loaded (GLU: its gate rows at w, its
 //            up rows at w2).
 struct NbLds {
-    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, rt, prow, outs, w, w2, wrow, end;
+    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, rt, prow, region, bufs, outs, w, w2,
+        wrow, end;
 };
 
 // The LDS stride of rows of `bytes` bytes (a multiple of 16) read 16 rows at
@@ -2293,7 +2295,7 @@ __host__ __device__ inline uint32_t nb_row_stride(uint32_t bytes) {
 }
 
 __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint32_t row_bytes,
-                                        uint32_t mode, bool glu, uint32_t tpp = 1u) {
+                                        uint32_t mode, bool glu, uint32_t tpp = 1u, uint32_t bufs = 1u) {
     const uint32_t nb = k >> 5;
     auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
     NbLds l;
@@ -2316,7 +2318,9 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     l.rt = tr <= 8u ? 8u : 16u;
     l.prow = l.rt * l.pstride + (nbatch <= 8u ? 2u : 4u);
     l.part = act_end;
-    l.outs = l.part + 4u * tpp * nbatch * l.prow;
+    l.region = tpp * nbatch * l.prow;  // floats of one phase's contributions
+    l.bufs = bufs;
+    l.outs = l.part + 4u * bufs * l.region;
     const uint32_t outs_end = l.outs + (glu ? 4u * nbatch * (tr + tr / 2u) : 0u);
     l.x = 0;
     l.xrow = kb(4u * k);  // whole kilobytes: a row's last direct load may write past its end
@@ -2491,7 +2495,7 @@ template <int KIND, uint32_t MODE, bool GLU, int NB>
 __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     const uint8_t* __restrict__ w, const float* __restrict__ x, uint32_t ldx, const float* __restrict__ nw, float eps,
     Activations act, float* __restrict__ dst, const float* __restrict__ bias, uint32_t bias_ld, uint32_t n, uint32_t k,
-    uint32_t tr, uint32_t tpp, Activations glu) {
+    uint32_t tr, uint32_t tpp, uint32_t bufs, Activations glu) {
     static_assert(NB >= 1 && NB <= 16 && (MODE == NB_QUANT || NB <= 8), "activation rows of a launch");
     constexpr uint32_t WAVES = NbShape<NB>::WAVES, THREADS = NbShape<NB>::THREADS, PER = NbShape<NB>::PER;
     constexpr uint32_t PP = PER / 2u;  // pairs of a chunk a wave (up to 8 rows)
@@ -2502,7 +2506,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     const uint32_t nb = k >> 5, row_bytes = nb * BB;
     const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
     const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
-    const NbLds L = nb_lds(NB, KIND, k, tr, row_bytes, MODE, GLU, tpp);
+    const NbLds L = nb_lds(NB, KIND, k, tr, row_bytes, MODE, GLU, tpp, bufs);
     const uint32_t lbase = lds_address(base);
 
     // Activations first, every wave its share, then the weights.
@@ -2619,7 +2623,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     // 4·lq + i of weight row 16·c + lr.
     const uint32_t lr = lane & 15u, lq = lane >> 4;
     const uint32_t chunk = min(nb, NB_CHUNK), pstride = L.pstride;
-    float* part = reinterpret_cast<float*>(base + L.part);
+    float* parts = reinterpret_cast<float*>(base + L.part);
     float* outs = reinterpret_cast<float*>(base + L.outs);
     const uint8_t* arow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(lr, (uint32_t)NB - 1u) * L.arow;
     const uint32_t tstride = L.trow >> 2, wstride = L.wrow;
@@ -2629,6 +2633,41 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     const uint32_t ft = tpp > 1u ? t >> 7 : 0u;
     const uint32_t fb = tpp > 1u ? (t >> 4) & 7u : t >> 4, fr = t & 15u;
     const uint32_t prow = L.prow, tile_floats = (uint32_t)NB * prow;
+    // The fold of one phase: this thread adds its output's contributions of
+    // the chunk (cl blocks, in `from`) in block order to its running sum,
+    // and after a tile's last chunk stores the output (tile oc).
+    float acc = 0.0f;
+    auto fold = [&](const float* from, uint32_t cl, bool live, uint32_t oc, bool last) {
+        if (!live) return;
+        // read 32 at a time into registers before they are added
+        const float* cp = from + ft * tile_floats + fb * prow + fr * pstride;
+        uint32_t i = 0;
+        for (; i + 32u <= cl; i += 32u) {
+            float2 vv[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc += vv[e].x;
+                acc += vv[e].y;
+            }
+        }
+        for (; i < cl; ++i) acc += cp[i];
+        if (last) {
+            const uint32_t r = 16u * oc + fr;
+            if constexpr (GLU) {
+                outs[fb * tr + r] = acc;
+            } else {
+                const uint32_t row = row0 + r;
+                dst[(size_t)fb * n + row] = bias ? acc + bias[(size_t)fb * bias_ld + row] : acc;
+            }
+            acc = 0.0f;
+        }
+    };
+    // Two buffers: the previous phase's fold, held here, runs after this
+    // phase's contributions are written (one barrier a phase).
+    uint32_t buf = 0, held_cl = 0, held_oc = 0;
+    bool held = false, held_live = false, held_last = false;
     for (uint32_t c = 0; c * 16u < rows; c += tpp) {
         const uint32_t wr = min(16u * c + lr, rows - 1u);  // a clamped row's contributions are not written
         const uint8_t* wrow = GLU ? (wr < h ? base + L.w + wr * wstride : base + L.w2 + (wr - h) * wstride)
@@ -2636,10 +2675,10 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
         const bool wlive = 16u * c + lr < rows;
         const uint32_t fc = c + ft;  // the tile of this thread's output
         const bool folds = ft < tpp && fb < (uint32_t)NB && 16u * fc + fr < rows;
-        float acc = 0.0f;
         for (uint32_t q0 = 0; q0 < nb; q0 += chunk) {
             const uint32_t cl = min(chunk, nb - q0);  // blocks of this chunk, a multiple of 8
             const uint32_t u0 = PER * wave;           // this wave's first block of the chunk
+            float* part = parts + buf * L.region;     // this phase's contributions
             if (u0 < cl) {
               if constexpr (NB <= 8) {
                 // Pairs of blocks on v_mfma_i32_16x16x64_i8: A is the tile's 16
@@ -2802,36 +2841,20 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                 }
                           }
             }
-            lds_sync();
-            if (folds) {
-                // the chunk's contributions in block order, read 32 at a
-                // time into registers before they are added
-                const float* cp = part + ft * tile_floats + fb * prow + fr * pstride;
-                uint32_t i = 0;
-                for (; i + 32u <= cl; i += 32u) {
-                    float2 vv[16];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        acc += vv[e].x;
-                        acc += vv[e].y;
-                    }
-                }
-                for (; i < cl; ++i) acc += cp[i];
-            }
-            lds_sync();
-        }
-        if (folds) {
-            const uint32_t r = 16u * fc + fr;
-            if constexpr (GLU) {
-                outs[fb * tr + r] = acc;
+            const bool last = q0 + chunk >= nb;
+            if (bufs > 1u) {
+                if (held) fold(parts + (buf ^ 1u) * L.region, held_cl, held_live, held_oc, held_last);
+                lds_sync();  // this phase's contributions written; the held fold done with the other buffer
+                held = true, held_cl = cl, held_live = folds, held_oc = fc, held_last = last;
+                buf ^= 1u;
             } else {
-                const uint32_t row = row0 + r;
-                dst[(size_t)fb * n + row] = bias ? acc + bias[(size_t)fb * bias_ld + row] : acc;
+                lds_sync();
+                fold(part, cl, folds, fc, last);
+                lds_sync();
             }
         }
     }
+    if (held) fold(parts + (buf ^ 1u) * L.region, held_cl, held_live, held_oc, held_last);
     if constexpr (GLU) {
         // SwiGLU one output a thread, then the quantiser, 8 lanes a block
         lds_sync();
@@ -3702,6 +3725,21 @@ static uint32_t nb_tpp(int nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint3
                : 1u;
 }
 
+// Contributions buffers of k_matvec_nb: two (each phase's fold behind the
+// next phase's contributions, one barrier a phase) where a launch has two
+// phases or more and the second buffer fits the LDS limit, else one.
+// TMH_NB_BUFS=1 keeps one, for measurement.
+static uint32_t nb_bufs(int nbatch, uint32_t kind, uint32_t k, uint32_t tr, uint32_t row_bytes, uint32_t mode,
+                        bool glu, uint32_t tpp) {
+    static const bool on = [] {
+        const char* env = getenv("TMH_NB_BUFS");
+        return !(env && strcmp(env, "1") == 0);
+    }();
+    const uint32_t tiles = (tr + 15u) / 16u, phases = (tiles + tpp - 1u) / tpp * ((k / 32u + NB_CHUNK - 1u) / NB_CHUNK);
+    return on && phases >= 2u && nb_lds(nbatch, kind, k, tr, row_bytes, mode, glu, tpp, 2u).end <= ONE_LDS_LIMIT ? 2u
+                                                                                                            : 1u;
+}
+
 template <int KIND, uint32_t MODE, int NB>
 static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, const float* nw, float eps,
                             Activations act, float* dst, const float* bias, uint32_t bias_ld, uint32_t n, uint32_t k,
@@ -3709,10 +3747,11 @@ static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, cons
     const uint32_t nb = k >> 5;
     const uint32_t tr = nb_tile<KIND, MODE, NB>(n, k, compute_units);
     const uint32_t tpp = nb_tpp(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false);
-    const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
+    const uint32_t bufs = nb_bufs(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
+    const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp, bufs);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS), L.end,
-                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, Activations{});
+                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, bufs, Activations{});
     return hipGetLastError();
 }
 
@@ -3797,10 +3836,11 @@ static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, 
                                 Activations act, uint32_t H, uint32_t k, Activations glu, hipStream_t stream) {
     const uint32_t nb = k >> 5, h = NB_GLU_HALF;
     const uint32_t tpp = nb_tpp(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
-    const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
+    const uint32_t bufs = nb_bufs(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
+    const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp, bufs);
     hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream, w, x,
                        ldx, nw,
-                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, glu);
+                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, bufs, glu);
     return hipGetLastError();
 }
 
