@@ -2276,12 +2276,13 @@ struct NbShape {
 //            [bufs][tpp][NB][prow] ([rt][pstride] and a skew) of the tpp
 //            tiles of 16 weight rows of a phase and one chunk of blocks (two
 //            buffers: a phase's fold runs while the next one's contributions
-//            are formed), and the GLU outputs;
+//            are formed), the GLU outputs, a zero piece and a dummy slot
+//            per lane (below);
 //   [w, end) the weight tile, direct-loaded (GLU: its gate rows at w, its
 //            up rows at w2).
 struct NbLds {
-    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, rt, prow, region, bufs, outs, w, w2,
-        wrow, end;
+    uint32_t x, xrow, nw, qs, arow, scales, sums, totals, trow, part, pstride, rt, prow, region, bufs, outs, zeros,
+        dummy, w, w2, wrow, end;
 };
 
 // The LDS stride of rows of `bytes` bytes (a multiple of 16) read 16 rows at
@@ -2328,7 +2329,12 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     const uint32_t x_end = mode == NB_QUANT ? 0u : l.nw + (mode == NB_NORM ? kb(4u * k) : 0u);
     // the weight tile's direct loads fill whole kilobytes from its start,
     // which needs 16-byte alignment only (x_end is whole kilobytes)
-    l.w = ((x_end > outs_end ? x_end : outs_end) + 255u) & ~255u;
+    // 512 bytes of zeros, read as the B operand by the lanes whose values
+    // must be zero, and 512 bytes the lanes with no contribution slot write
+    l.zeros = (outs_end + 15u) & ~15u;
+    l.dummy = l.zeros + 512u;
+    const uint32_t extra_end = l.dummy + 512u;
+    l.w = ((x_end > extra_end ? x_end : extra_end) + 255u) & ~255u;
     l.wrow = nb_row_stride(row_bytes);
     const uint32_t half = kb((tr / 2u) * l.wrow);
     l.w2 = glu ? l.w + half : l.w;
@@ -2457,6 +2463,34 @@ __device__ __forceinline__ v4i pair_weights(const uint8_t* row, uint32_t b, uint
         return v4i{(int)(x0 & 0x0f0f0f0fu), (int)(x1 & 0x0f0f0f0fu), (int)((x0 >> 4) & 0x0f0f0f0fu),
                    (int)((x1 >> 4) & 0x0f0f0f0fu)};
     }
+}
+
+// pair_weights with q at half h of block b already: row + BB·b + (Q4_1: 4,
+// else 2) + 8h; pair_acts with q at row + 32·b + 8h.
+template <int KIND>
+__device__ __forceinline__ v4i pair_weights_at(const uint8_t* q) {
+    uint32_t x0, x1;
+    if constexpr (KIND == 0) {
+        uint32_t y0, y1;
+        lds_read8(q, x0, x1);
+        lds_read8(q + 16, y0, y1);
+        return v4i{(int)x0, (int)x1, (int)y0, (int)y1};
+    } else {
+        if constexpr (KIND == 1) {
+            lds_read8(q, x0, x1);
+        } else {
+            const uint32_t* d = reinterpret_cast<const uint32_t*>(q);
+            x0 = d[0], x1 = d[1];
+        }
+        return v4i{(int)(x0 & 0x0f0f0f0fu), (int)(x1 & 0x0f0f0f0fu), (int)((x0 >> 4) & 0x0f0f0f0fu),
+                   (int)((x1 >> 4) & 0x0f0f0f0fu)};
+    }
+}
+
+__device__ __forceinline__ v4i pair_acts_at(const uint8_t* q) {
+    const uint2 lo = *reinterpret_cast<const uint2*>(q);
+    const uint2 hi = *reinterpret_cast<const uint2*>(q + 16);
+    return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
 }
 
 __device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_t h) {
@@ -2615,6 +2649,9 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
             }
         }
     }
+    // the zero piece (below the weights; any staged f32 rows are in
+    // registers or quantised by now)
+    for (uint32_t z = t; z < 128u; z += THREADS) reinterpret_cast<float*>(base + L.zeros)[z] = 0.0f;
     wait_vm_lds<0>();  // this wave's weights
     lds_sync();
 
@@ -2687,9 +2724,32 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                 // block j of the pair (lane (n, g): zero unless g / 2 == j), so
                 // D[m][n] is weight row m's dot product with row b over block j
                 // alone. A lane's outputs: weight rows 4 g + i of column n.
+                // Every pair's operands at constant offsets from one base a
+                // phase (pairs 2·BB bytes apart in a weight row, 64 in an
+                // activation row, 2 entries in a table).
                 const uint32_t jj = lq >> 1, hh = lq & 1u, ab = lr & 7u, aj = lr >> 3;
                 const bool breal = ab < (uint32_t)NB && aj == jj;
-                const uint8_t* brow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(ab, (uint32_t)NB - 1u) * L.arow;
+                const uint32_t b0 = q0 + u0;  // the wave's first block of the chunk (even)
+                // B: row ab's half hh of block b0 + 2p + aj, or the zero piece
+                // for a lane whose values must be zero
+                const uint8_t* bq = breal ? reinterpret_cast<const uint8_t*>(aq) + (size_t)ab * L.arow + 32u * (b0 + aj) + 8u * hh
+                                          : base + L.zeros + 8u * hh;
+                const uint32_t sat = min(ab, (uint32_t)NB - 1u) * tstride + b0 + aj;
+                v4i bv[PP];
+                float sx[PP], ex[PP];
+#pragma unroll
+                for (uint32_t p = 0; p < PP; ++p) {
+                    bv[p] = pair_acts_at(bq + 64u * p);
+                    sx[p] = asc[sat + 2u * p];
+                    ex[p] = 0.0f;
+                    if constexpr (KIND == 2) ex[p] = asm_[sat + 2u * p];
+                    if constexpr (KIND == 1) ex[p] = __int_as_float(-8 * atot[sat + 2u * p]);
+                }
+                // the lane's output i goes to its slot (weight row 4 lq + i of
+                // row ab), or to the lane's own dummy slot when the region has
+                // no such slot (ab past NB; a row past 8 in a tile of 8 rows);
+                // a slot of a weight row past the tile's rows is never folded
+                float* dummy = reinterpret_cast<float*>(base + L.dummy) + lane;
 #pragma unroll
                 for (uint32_t tt = 0; tt < 2u; ++tt) {
                 const uint32_t ct = c + tt;
@@ -2697,28 +2757,27 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                 const uint32_t wrt = min(16u * ct + lr, rows - 1u);
                 const uint8_t* trow = GLU ? (wrt < h ? base + L.w + wrt * wstride : base + L.w2 + (wrt - h) * wstride)
                                           : base + L.w + wrt * wstride;
-                float* tpart = part + tt * tile_floats;
-                v4i av[PP], bv[PP];
+                const uint8_t* wq = trow + BB * (b0 + jj) + (KIND == 2 ? 4u : 2u) + 8u * hh;
+                const uint8_t* dq[4];
+                float* wp[4];
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) {
+                    const uint32_t r = min(16u * ct + 4u * lq + i, rows - 1u);
+                    const uint8_t* rp = GLU ? (r < h ? base + L.w + r * wstride : base + L.w2 + (r - h) * wstride)
+                                            : base + L.w + r * wstride;
+                    dq[i] = rp + BB * (b0 + aj);
+                    const bool slot = ab < (uint32_t)NB && 4u * lq + i < L.rt;
+                    wp[i] = slot ? part + tt * tile_floats + ab * prow + (4u * lq + i) * pstride + u0 + aj : dummy;
+                }
+                v4i av[PP];
                 uint32_t dm[PP][4];
-                float sx[PP], ex[PP];
 #pragma unroll
                 for (uint32_t p = 0; p < PP; ++p) {
-                    const uint32_t b = q0 + u0 + 2u * p;  // the pair's first block
-                    av[p] = pair_weights<KIND>(trow, b + jj, hh);
-                    const v4i x = pair_acts(brow, b + aj, hh);  // brow clamped: a valid row
-                    bv[p] = breal ? x : v4i{0, 0, 0, 0};
-                    const uint32_t at = min(ab, (uint32_t)NB - 1u) * tstride + b + aj;
-                    sx[p] = asc[at];
-                    ex[p] = 0.0f;
-                    if constexpr (KIND == 2) ex[p] = asm_[at];
-                    if constexpr (KIND == 1) ex[p] = __int_as_float(-8 * atot[at]);
+                    av[p] = pair_weights_at<KIND>(wq + 2u * BB * p);
 #pragma unroll
                     for (uint32_t i = 0; i < 4; ++i) {
-                        const uint32_t r = min(16u * ct + 4u * lq + i, rows - 1u);
-                        const uint8_t* rp = GLU ? (r < h ? base + L.w + r * wstride : base + L.w2 + (r - h) * wstride)
-                                                : base + L.w + r * wstride;
-                        if constexpr (KIND == 2) dm[p][i] = *reinterpret_cast<const uint32_t*>(rp + 20u * (b + aj));
-                        else dm[p][i] = *reinterpret_cast<const uint16_t*>(rp + BB * (b + aj));
+                        if constexpr (KIND == 2) dm[p][i] = *reinterpret_cast<const uint32_t*>(dq[i] + 2u * BB * p);
+                        else dm[p][i] = *reinterpret_cast<const uint16_t*>(dq[i] + 2u * BB * p);
                     }
                 }
                 v4i tv[PP];
@@ -2731,28 +2790,25 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                     }
                     tv[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[p], bv[p], cin, 0, 0, 0);
                 }
-                if (ab < (uint32_t)NB) {
 #pragma unroll
-                    for (uint32_t p = 0; p < PP; ++p) {
+                for (uint32_t p = 0; p < PP; ++p) {
 #pragma unroll
-                        for (uint32_t i = 0; i < 4; ++i) {
-                            const float ft = (float)tv[p][i], d = half_value(dm[p][i] & 0xffffu);
-                            float cv;
-                            if constexpr (KIND == 0) {
-                                const float sc = d * sx[p];
-                                cv = ft * sc;
-                            } else if constexpr (KIND == 1) {
-                                const float pr = ft * d;
-                                cv = pr * sx[p];
-                            } else {
-                                const float sc = d * sx[p];
-                                const float f = sc * ft;
-                                const float g = half_value(dm[p][i] >> 16) * ex[p];
-                                cv = f + g;
-                            }
-                            if (16u * ct + 4u * lq + i < rows)
-                                tpart[ab * prow + (4u * lq + i) * pstride + u0 + 2u * p + aj] = cv;
+                    for (uint32_t i = 0; i < 4; ++i) {
+                        const float ft = (float)tv[p][i], d = half_value(dm[p][i] & 0xffffu);
+                        float cv;
+                        if constexpr (KIND == 0) {
+                            const float sc = d * sx[p];
+                            cv = ft * sc;
+                        } else if constexpr (KIND == 1) {
+                            const float pr = ft * d;
+                            cv = pr * sx[p];
+                        } else {
+                            const float sc = d * sx[p];
+                            const float f = sc * ft;
+                            const float g = half_value(dm[p][i] >> 16) * ex[p];
+                            cv = f + g;
                         }
+                        wp[i][2u * p] = cv;
                     }
                 }
                 }
