@@ -1987,34 +1987,6 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 template <int KIND>
 __device__ __forceinline__ long few_weights(const uint8_t* row, uint32_t b, uint32_t q);
 
-// few_weights for a block b whose parity is known where it is called (the
-// two layouts of a pair's blocks, without a branch between them).
-template <int KIND, bool ODD>
-__device__ __forceinline__ long few_weights_at(const uint8_t* row, uint32_t b, uint32_t q) {
-    if constexpr (KIND == 0) {
-        if constexpr (!ODD) {
-            const uint32_t* p = (const uint32_t*)(row + 34u * b + 8u * q);
-            const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-            return (long)funnel(d1, d0, 2) | ((long)funnel(d2, d1, 2) << 32);
-        }
-        const uint32_t* p = (const uint32_t*)(row + 34u * b + 2u + 8u * q);
-        return (long)p[0] | ((long)p[1] << 32);
-    } else {
-        uint32_t v;
-        if constexpr (KIND == 1) {
-            if constexpr (!ODD) {
-                const uint32_t* p = (const uint32_t*)(row + 18u * b + 4u * q);
-                v = funnel(p[1], p[0], 2);
-            } else {
-                v = *(const uint32_t*)(row + 18u * b + 2u + 4u * q);
-            }
-        } else {
-            v = *(const uint32_t*)(row + 20u * b + 4u + 4u * q);
-        }
-        return (long)(v & 0x0f0f0f0fu) | ((long)((v >> 4) & 0x0f0f0f0fu) << 32);
-    }
-}
-
 template <int KIND>
 __device__ __forceinline__ long few_weights(const uint8_t* row, uint32_t b, uint32_t q) {
     if constexpr (KIND == 0) {
@@ -2249,17 +2221,14 @@ __global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __res
 
 // Threads of a k_matvec_nb workgroup: 8 waves, two a SIMD.
 constexpr uint32_t NB_THREADS = 512;
-constexpr uint32_t NB_WAVES = NB_THREADS / 64u;
 // Blocks of a fold chunk: the contributions of NB_CHUNK blocks are held in
-// LDS at a time, NB_PER consecutive blocks a wave.
+// LDS at a time, a run of consecutive blocks a wave.
 constexpr uint32_t NB_CHUNK = 64;
-constexpr uint32_t NB_PER = NB_CHUNK / NB_WAVES;
-static_assert(NB_PER == 8, "a wave's blocks of a chunk: two 16-byte table reads and writes");
 // One or two rows: 16 waves a workgroup, four a SIMD, each with 4 blocks
 // (2 pairs) of a chunk, so that a SIMD has more waves to hide each one's LDS
 // reads and MFMA results (measured, config 3 8192x2048: B = 1 and 2 0.25 us
 // faster a call, B = 4 the same, B = 8 0.15 us slower); else 8 waves of 8
-// blocks.
+// blocks (4 pairs).
 template <int NB>
 struct NbShape {
     static constexpr uint32_t THREADS = NB <= 2 ? 1024u : NB_THREADS;
@@ -2314,10 +2283,9 @@ __host__ __device__ inline NbLds nb_lds(uint32_t nbatch, uint32_t kind, uint32_t
     // so without it the pair MFMAs' writes of 8 activation rows (a lane's
     // row b, weight row 4 g + i, block j: bank 16 g + j + b·(prow mod 64))
     // would meet on 8 banks; 2 floats spread them over all 64 (8 rows:
-    // b·34 + 16 g + j, 32 lanes on distinct banks). From 9 rows the writes
-    // are 16-byte vectors: a skew of 4 floats.
+    // b·34 + 16 g + j, 32 lanes on distinct banks).
     l.rt = tr <= 8u ? 8u : 16u;
-    l.prow = l.rt * l.pstride + (nbatch <= 8u ? 2u : 4u);
+    l.prow = l.rt * l.pstride + 2u;
     l.part = act_end;
     l.region = tpp * nbatch * l.prow;  // floats of one phase's contributions
     l.bufs = bufs;
@@ -2499,7 +2467,7 @@ __device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_
     return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
 }
 
-// NB (at most 16) activation rows times a tile of `tr` weight rows per
+// NB (at most 8) activation rows times a tile of `tr` weight rows per
 // workgroup, the tile's weights direct-loaded into LDS at the start (as
 // k_matvec_one does for one row). Every wave issues its share of the
 // activations first, then of the weights, so that its wait for the
@@ -2512,10 +2480,10 @@ __device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_
 //     eps), v = x / root · nw; then the lane quantises its block
 //     (quantize_block32) into LDS, while the weights are in flight;
 //   QUANT: the rows arrive quantised.
-// Products on the int8 matrix cores: per tile of 16 weight rows and block,
-// one v_mfma_i32_16x16x32_i8 of the activation rows (A; rows past NB zero)
-// against the weight rows (B), operands taken where the blocks lie
-// (few_acts, few_weights; Q4_0's -8·Σq as C); each (row, output, block)
+// Products on the int8 matrix cores: per tile of 16 weight rows and pair of
+// blocks, one v_mfma_i32_16x16x64_i8 of the weight rows (A) against columns
+// (activation row, block of the pair) (B), operands taken where the blocks
+// lie (Q4_0's -8·Σq as C; below); each (row, output, block)
 // contribution is formed in the host's expression (Q8_0 float(t)·(d·sx);
 // Q4_0 (float(t)·d)·sx; Q4_1 (d·sx)·float(t) + m·mx) and written to LDS, a
 // chunk of NB_CHUNK blocks at a time, each wave a run of consecutive blocks
@@ -2530,7 +2498,7 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     const uint8_t* __restrict__ w, const float* __restrict__ x, uint32_t ldx, const float* __restrict__ nw, float eps,
     Activations act, float* __restrict__ dst, const float* __restrict__ bias, uint32_t bias_ld, uint32_t n, uint32_t k,
     uint32_t tr, uint32_t tpp, uint32_t bufs, Activations glu) {
-    static_assert(NB >= 1 && NB <= 16 && (MODE == NB_QUANT || NB <= 8), "activation rows of a launch");
+    static_assert(NB >= 1 && NB <= 8, "activation rows of a launch");
     constexpr uint32_t WAVES = NbShape<NB>::WAVES, THREADS = NbShape<NB>::THREADS, PER = NbShape<NB>::PER;
     constexpr uint32_t PP = PER / 2u;  // pairs of a chunk a wave (up to 8 rows)
     extern __shared__ float4 lds4[];
@@ -2655,16 +2623,13 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     wait_vm_lds<0>();  // this wave's weights
     lds_sync();
 
-    // The lane's MFMA operands: activation row lr (A; zero past NB), k
-    // quarter lq; weight row 16·c + lr of tile c (B); its outputs are rows
-    // 4·lq + i of weight row 16·c + lr.
+    // The lane's place in the MFMA operands: lr = lane % 16 (a weight row of
+    // A, a (row, block) column of B), lq = lane / 16 (its k group).
     const uint32_t lr = lane & 15u, lq = lane >> 4;
     const uint32_t chunk = min(nb, NB_CHUNK), pstride = L.pstride;
     float* parts = reinterpret_cast<float*>(base + L.part);
     float* outs = reinterpret_cast<float*>(base + L.outs);
-    const uint8_t* arow = reinterpret_cast<const uint8_t*>(aq) + (size_t)min(lr, (uint32_t)NB - 1u) * L.arow;
     const uint32_t tstride = L.trow >> 2, wstride = L.wrow;
-    const bool alive = lr < (uint32_t)NB;
     // A phase takes tpp tiles of 16 weight rows (2 only up to 8 rows): the
     // output this thread adds up is row fb, weight row 16·(c + ft) + fr.
     const uint32_t ft = tpp > 1u ? t >> 7 : 0u;
@@ -2706,10 +2671,6 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     uint32_t buf = 0, held_cl = 0, held_oc = 0;
     bool held = false, held_live = false, held_last = false;
     for (uint32_t c = 0; c * 16u < rows; c += tpp) {
-        const uint32_t wr = min(16u * c + lr, rows - 1u);  // a clamped row's contributions are not written
-        const uint8_t* wrow = GLU ? (wr < h ? base + L.w + wr * wstride : base + L.w2 + (wr - h) * wstride)
-                                  : base + L.w + wr * wstride;
-        const bool wlive = 16u * c + lr < rows;
         const uint32_t fc = c + ft;  // the tile of this thread's output
         const bool folds = ft < tpp && fb < (uint32_t)NB && 16u * fc + fr < rows;
         for (uint32_t q0 = 0; q0 < nb; q0 += chunk) {
@@ -2717,7 +2678,6 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
             const uint32_t u0 = PER * wave;           // this wave's first block of the chunk
             float* part = parts + buf * L.region;     // this phase's contributions
             if (u0 < cl) {
-              if constexpr (NB <= 8) {
                 // Pairs of blocks on v_mfma_i32_16x16x64_i8: A is the tile's 16
                 // weight rows (lane (m, g): row m, half g % 2 of block g / 2 of
                 // the pair), B's 16 columns n = b + 8 j are activation row b in
@@ -2812,90 +2772,6 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                     }
                 }
                 }
-              } else {
-                // Every operand read of the wave's 8 blocks first, then the
-                // MFMAs, then the contributions.
-                typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
-                typedef int i4a __attribute__((ext_vector_type(4), aligned(16)));
-                long av[PER], bv[PER];
-                uint32_t dm[PER];
-                float sx[4][PER], ex[4][PER];
-#pragma unroll
-                for (uint32_t p = 0; p < PER; ++p) {
-                    const uint32_t b = q0 + u0 + p;  // of p's parity (q0, u0 even)
-                    const long a = few_acts<KIND>(arow, b, lq);  // arow clamped: a valid row
-                    av[p] = alive ? a : 0l;
-                    bv[p] = p % 2u ? few_weights_at<KIND, true>(wrow, b, lq) : few_weights_at<KIND, false>(wrow, b, lq);
-                    if constexpr (KIND == 2) dm[p] = *reinterpret_cast<const uint32_t*>(wrow + 20u * b);
-                    else dm[p] = *reinterpret_cast<const uint16_t*>(wrow + BB * b);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // 16-byte aligned: table rows of whole 16-byte pieces, chunks of 64, 8 blocks a wave
-                    const uint32_t at = min(4u * lq + i, (uint32_t)NB - 1u) * tstride + q0 + u0;
-                    const f4a s0 = *reinterpret_cast<const f4a*>(asc + at);
-                    const f4a s1 = *reinterpret_cast<const f4a*>(asc + at + 4u);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) sx[i][e] = s0[e], sx[i][4 + e] = s1[e], ex[i][e] = ex[i][4 + e] = 0.0f;
-                    if constexpr (KIND == 2) {
-                        const f4a e0 = *reinterpret_cast<const f4a*>(asm_ + at);
-                        const f4a e1 = *reinterpret_cast<const f4a*>(asm_ + at + 4u);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) ex[i][e] = e0[e], ex[i][4 + e] = e1[e];
-                    }
-                    if constexpr (KIND == 1) {
-                        const i4a e0 = *reinterpret_cast<const i4a*>(atot + at);
-                        const i4a e1 = *reinterpret_cast<const i4a*>(atot + at + 4u);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            ex[i][e] = __int_as_float(-8 * e0[e]), ex[i][4 + e] = __int_as_float(-8 * e1[e]);
-                    }
-                }
-                v4i tv[PER];
-#pragma unroll
-                for (uint32_t p = 0; p < PER; ++p) {
-                    v4i cin = {0, 0, 0, 0};
-                    if constexpr (KIND == 1) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) cin[i] = __float_as_int(ex[i][p]);
-                    }
-                    tv[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[p], bv[p], cin, 0, 0, 0);
-                }
-                float cv[4][PER];
-#pragma unroll
-                for (uint32_t p = 0; p < PER; ++p) {
-                    const float d = half_value(dm[p] & 0xffffu);
-                    const float m = KIND == 2 ? half_value(dm[p] >> 16) : 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float ft = (float)tv[p][i];
-                        if constexpr (KIND == 0) {
-                            const float sc = d * sx[i][p];
-                            cv[i][p] = ft * sc;
-                        } else if constexpr (KIND == 1) {
-                            const float pr = ft * d;
-                            cv[i][p] = pr * sx[i][p];
-                        } else {
-                            const float sc = d * sx[i][p];
-                            const float f = sc * ft;
-                            const float g = m * ex[i][p];
-                            cv[i][p] = f + g;
-                        }
-                    }
-                }
-                if (wlive) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (4u * lq + i < (uint32_t)NB) {
-                            f4a* to = reinterpret_cast<f4a*>(part + (4u * lq + i) * prow + lr * pstride + u0);
-                            const f4a c0 = {cv[i][0], cv[i][1], cv[i][2], cv[i][3]};
-                            const f4a c1 = {cv[i][4], cv[i][5], cv[i][6], cv[i][7]};
-                            to[0] = c0;
-                            to[1] = c1;
-                        }
-                    }
-                }
-                          }
             }
             const bool last = q0 + chunk >= nb;
             if (bufs > 1u) {
