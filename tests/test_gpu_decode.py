@@ -343,7 +343,7 @@ def test_decoder_limits(dev):
     assert tokens.shape == (1, 13) and gpu.length() == 20
 
 
-@pytest.mark.parametrize("layers,rows", [(2, 1), (2, 8), (24, 1)])
+@pytest.mark.parametrize("layers,rows", [(2, 1), (2, 7), (2, 8), (24, 1)])
 def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
     # BASELINE config 5's shape (width 2048, 32 heads of 64, hidden 8192,
     # vocab 49152, tied head): greedy tokens from the GPU, through a captured
@@ -359,8 +359,9 @@ def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
         gpu.forward(p, row=r, last_only=True)
     got = gpu.generate(steps, graph=True)
     cpu = oracle.Llama(config, weights)
-    # every row against the CPU at 2 layers (rows in each of the lanes
-    # product's row groups); the first two at 24
+    # every row against the CPU at 2 layers (rows in each of the few-rows
+    # product's row groups: 7 rows are groups of 4, 2 and 1); the first two
+    # at 24
     checked = prompts if layers <= 2 else prompts[:2]
     for r, p in enumerate(checked):
         assert list(got[r]) == cpu.generate(p, steps), r
@@ -374,13 +375,13 @@ def test_smollm2_1p7b_shape_greedy_identity(dev, layers, rows):
 
 
 
-@pytest.mark.parametrize("kind,rows", [("Q8_0", 1), ("Q8_0", 3), ("Q4_1", 1), ("Q4_1", 3)])
+@pytest.mark.parametrize("kind,rows", [("Q8_0", 1), ("Q8_0", 3), ("Q4_1", 1), ("Q4_1", 3), ("Q4_1", 5)])
 def test_1p7b_shape_other_formats(dev, kind, rows):
     # The 1.7B shape in Q8_0 (17-dword pairs) and Q4_1 (sums): the last
     # prefill logits bit for bit, then greedy tokens from a graph, against
     # the CPU -- the residual lanes product, gate_up with SwiGLU in its
-    # epilogue and the head at k = 2048 in both formats, and at 3 rows the
-    # row groups of the 16-token prefills.
+    # epilogue and the head at k = 2048 in both formats, and at 3 and 5 rows
+    # the few-rows product's groups of 2 and 4 (and 1) in decode.
     say("1.7B shape", kind, rows, "rows")
     config = dict(SMOLLM2_1P7B, layers=2, context=128, kind=kind)
     weights = random_block_llama(config, seed=40 + rows)
