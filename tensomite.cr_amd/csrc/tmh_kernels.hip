@@ -2692,8 +2692,9 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
                 const uint32_t b0 = q0 + u0;  // the wave's first block of the chunk (even)
                 // B: row ab's half hh of block b0 + 2p + aj, or the zero piece
                 // for a lane whose values must be zero
-                const uint8_t* bq = breal ? reinterpret_cast<const uint8_t*>(aq) + (size_t)ab * L.arow + 32u * (b0 + aj) + 8u * hh
-                                          : base + L.zeros + 8u * hh;
+                const uint8_t* bq =
+                    breal ? reinterpret_cast<const uint8_t*>(aq) + (size_t)ab * L.arow + 32u * (b0 + aj) + 8u * hh
+                          : base + L.zeros + 8u * hh;
                 const uint32_t sat = min(ab, (uint32_t)NB - 1u) * tstride + b0 + aj;
                 v4i bv[PP];
                 float sx[PP], ex[PP];
