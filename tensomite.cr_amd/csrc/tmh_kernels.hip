@@ -425,6 +425,26 @@ __device__ __forceinline__ uint32_t stage_bytes(const uint8_t* src, uint32_t byt
     return mine;
 }
 
+// Direct loads of `bytes` (a multiple of 16·G) at src into LDS at `to` (the
+// region holds whole kilobytes) by wave `by` only, the 16-byte pieces of
+// each group g of G rotated: piece i lands in slot G g + ((i + (g >> S)) %
+// G), so that lanes reading piece i of consecutive groups together meet
+// distinct bank groups (a group of G pieces spans G·4 banks of the 64). Lane
+// l of load n fills slot 64 n + l with the piece that belongs there.
+template <uint32_t G, uint32_t S>
+__device__ __forceinline__ void stage_rotated(const uint8_t* src, uint32_t bytes, uint32_t to, uint32_t wave,
+                                              uint32_t by) {
+    static_assert((G & (G - 1u)) == 0, "whole groups of a power of two");
+    if (wave != by) return;
+    const uint32_t lane = threadIdx.x & 63u, pieces = bytes >> 4, loads = (pieces + 63u) >> 6;
+    for (uint32_t n = 0; n < loads; ++n) {
+        // a slot past the last piece takes a copy of the last slot's piece
+        const uint32_t slot = min(n * 64u + lane, pieces - 1u), g = slot / G;
+        const uint32_t i = ((slot & (G - 1u)) - (g >> S)) & (G - 1u);
+        lds_load16(src + 16u * (G * g + i), to + n * 1024u);
+    }
+}
+
 // Direct loads of `count` 4-byte values at src into LDS at `to`, 256 bytes
 // a load, by wave `by` only; returns this wave's loads.
 __device__ __forceinline__ uint32_t stage_words(const void* src, uint32_t count, uint32_t to, uint32_t wave,
@@ -501,11 +521,14 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     // any weight load (the compute unit's loads queue in order, so the
     // weights would delay them). The other waves: the weights.
     constexpr uint32_t WFIRST = NORM ? 2u : 1u;  // the first wave of the weights
+    // x in groups of 8 pieces (a lane's 32 values of Σx²) rotated by group / 2,
+    // the quantised row in groups of 4 (a pair of blocks) rotated by group /
+    // 4 (stage_rotated), so that the lanes' reads below meet distinct banks
     if constexpr (NORM) {
-        stage_bytes<false>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u, 1u);
+        stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u);
         stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, 1u, 1u);
     } else {
-        stage_bytes<false>(reinterpret_cast<const uint8_t*>(act.qs), k, lbase + L.qs, wave, 0u, 1u);
+        stage_rotated<4, 2>(reinterpret_cast<const uint8_t*>(act.qs), k, lbase + L.qs, wave, 0u);
         stage_words(act.scales, nb, lbase + L.scales, wave, 0u);
         if constexpr (KIND == 2) stage_words(act.sums, nb, lbase + L.sums, wave, 0u);
         if constexpr (KIND == 1) stage_words(act.totals, nb, lbase + L.totals, wave, 0u);
@@ -526,12 +549,12 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     if (wave == 0) {
         wait_vm_lds<0>();  // wave 0 issued only the activations
         if constexpr (NORM) {
-            const float* xs = reinterpret_cast<const float*>(base + L.x);
+            const float4* xs4 = reinterpret_cast<const float4*>(base + L.x);
             float sq[32];
 #pragma unroll
             for (uint32_t i = 0; i < 32u; i += 4u) {
-                const uint32_t c = t * 32u + i;
-                const float4 v = c < k ? *reinterpret_cast<const float4*>(xs + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const uint32_t c = t * 32u + i;  // piece i / 4 of group t
+                const float4 v = c < k ? xs4[8u * t + ((i / 4u + (t >> 1)) & 7u)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 sq[i] = v.x * v.x;
                 sq[i + 1] = v.y * v.y;
                 sq[i + 2] = v.z * v.z;
@@ -544,12 +567,12 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     if (NORM && wave == 1) wait_vm_lds<0>();  // wave 1 issued only the norm's weights
     lds_sync();  // the activations (and the root) are in
     if constexpr (NORM) {
-        const float* xs = reinterpret_cast<const float*>(base + L.x);
+        const float4* xs4 = reinterpret_cast<const float4*>(base + L.x);
         const float* ws = reinterpret_cast<const float*>(base + L.nw);
         const float root = root_slot;
         for (uint32_t blk = t >> 3; blk < nb; blk += ONE_THREADS / 8u) {  // uniform across each 8-lane group
             const uint32_t c = blk * 32u + (t & 7u) * 4u;
-            const float4 xq = *reinterpret_cast<const float4*>(xs + c);
+            const float4 xq = xs4[8u * blk + (((t & 7u) + (blk >> 1)) & 7u)];  // piece t % 8 of group blk
             const float4 wq = *reinterpret_cast<const float4*>(ws + c);
             const float xj[4] = {xq.x, xq.y, xq.z, xq.w};
             const float wj[4] = {wq.x, wq.y, wq.z, wq.w};
@@ -560,7 +583,9 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
                 v[i] = q * wj[i];
             }
             const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
-            *reinterpret_cast<uint32_t*>(aq + c) = q.packed;
+            // byte o of pair blk / 2, in the rotated layout of the staged rows
+            const uint32_t pj = blk >> 1, o = (blk & 1u) * 32u + (t & 7u) * 4u;
+            *reinterpret_cast<uint32_t*>(aq + 16u * (4u * pj + (((o >> 4) + (pj >> 2)) & 3u)) + (o & 15u)) = q.packed;
             if ((t & 7u) == 0) {
                 asc[blk] = q.scale;
                 asm_[blk] = q.sum;
@@ -575,10 +600,10 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     const uint32_t j = t % np, rpass = ONE_THREADS / np;
     uint32_t a[16];
     {
-        const uint4* q4 = reinterpret_cast<const uint4*>(aq + (size_t)j * 64u);
+        const uint4* q4 = reinterpret_cast<const uint4*>(aq) + 4u * j;  // the pair's pieces, rotated by j / 4
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 v = q4[i];
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint4 v = q4[(i + (j >> 2)) & 3u];
             a[4 * i] = v.x, a[4 * i + 1] = v.y, a[4 * i + 2] = v.z, a[4 * i + 3] = v.w;
         }
     }
