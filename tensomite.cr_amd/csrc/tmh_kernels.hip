@@ -463,13 +463,13 @@ struct OneLds {
 };
 
 __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_bytes, uint32_t stride, bool norm,
-                                          bool glu) {
+                                          bool glu, bool plain = false) {
     const uint32_t nb = k >> 5;
     auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
     OneLds l;
     l.x = 0;
     l.nw = norm ? kb(4u * k) : 0u;
-    l.qs = norm ? 2u * kb(4u * k) : 0u;
+    l.qs = norm ? (plain ? 1u : 2u) * kb(4u * k) : 0u;  // plain: no norm weights
     l.scales = l.qs + kb(k);
     l.sums = l.scales + ((4u * nb + 255u) & ~255u);
     l.totals = l.sums + ((4u * nb + 255u) & ~255u);
@@ -492,13 +492,15 @@ __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_
 //     index order by speculation across wave 0, root = sqrtf(Σ/k + eps),
 //     v = x / root · nw, quantize_quad: the bits of k_rmsnorm_quantise_wave
 //     -- while the weights are in flight;
+//   NORM and PLAIN: x is the f32 row, quantised as it is (no norm; waves 0
+//     and 1 stage it, half each when its bytes are whole kilobytes);
 //   else the row arrives quantised (act, as the quantise pass lays it out).
 // Then matvec_tile's per-pair contributions and ordered fold, from LDS:
 // dst[row] = Σ (+ bias[row], one rounding), or, GLU, SwiGLU and the
 // quantiser on the tile's gate/up outputs into glu. k a multiple of 64 with
 // ONE_THREADS % (k / 64) == 0 (whole rows of pairs per pass), rows whole
 // 16-byte pieces starting 16-byte aligned.
-template <int KIND, bool NORM, bool GLU>
+template <int KIND, bool NORM, bool GLU, bool PLAIN = false>
 __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ nw, float eps, Activations act,
@@ -513,7 +515,8 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     const uint32_t nb = k >> 5, np = nb >> 1, row_bytes = nb * BB;
     const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
     const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
-    const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU);
+    static_assert(!PLAIN || (NORM && !GLU), "plain rows take the f32 path");
+    const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU, PLAIN);
     const uint32_t lbase = lds_address(base);
 
     // Wave 0: the activations (NORM: x, while wave 1 brings the norm's
@@ -524,7 +527,14 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     // x in groups of 8 pieces (a lane's 32 values of Σx²) rotated by group / 2,
     // the quantised row in groups of 4 (a pair of blocks) rotated by group /
     // 4 (stage_rotated), so that the lanes' reads below meet distinct banks
-    if constexpr (NORM) {
+    if constexpr (PLAIN) {
+        // halves of whole kilobytes (a group's rotation depends on the
+        // group's index mod 16, and each half holds a multiple of 16 groups)
+        const uint32_t half = (k % 512u) == 0 ? 2u * k : 4u * k;
+        stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), half, lbase + L.x, wave, 0u);
+        if (half < 4u * k)
+            stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x) + half, half, lbase + L.x + half, wave, 1u);
+    } else if constexpr (NORM) {
         stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u);
         stage_bytes<false>(reinterpret_cast<const uint8_t*>(nw), 4u * k, lbase + L.nw, wave, 1u, 1u);
     } else {
@@ -548,7 +558,7 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     int32_t* atot = reinterpret_cast<int32_t*>(base + L.totals);
     if (wave == 0) {
         wait_vm_lds<0>();  // wave 0 issued only the activations
-        if constexpr (NORM) {
+        if constexpr (NORM && !PLAIN) {
             const float4* xs4 = reinterpret_cast<const float4*>(base + L.x);
             float sq[32];
 #pragma unroll
@@ -564,23 +574,24 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
             if (t == 0) root_slot = __builtin_sqrtf(total / (float)k + eps);
         }
     }
-    if (NORM && wave == 1) wait_vm_lds<0>();  // wave 1 issued only the norm's weights
+    if (NORM && wave == 1) wait_vm_lds<0>();  // wave 1 issued only the norm's weights (PLAIN: x's second half)
     lds_sync();  // the activations (and the root) are in
     if constexpr (NORM) {
         const float4* xs4 = reinterpret_cast<const float4*>(base + L.x);
         const float* ws = reinterpret_cast<const float*>(base + L.nw);
-        const float root = root_slot;
+        const float root = PLAIN ? 1.0f : root_slot;  // PLAIN: unused
         for (uint32_t blk = t >> 3; blk < nb; blk += ONE_THREADS / 8u) {  // uniform across each 8-lane group
             const uint32_t c = blk * 32u + (t & 7u) * 4u;
             const float4 xq = xs4[8u * blk + (((t & 7u) + (blk >> 1)) & 7u)];  // piece t % 8 of group blk
-            const float4 wq = *reinterpret_cast<const float4*>(ws + c);
-            const float xj[4] = {xq.x, xq.y, xq.z, xq.w};
-            const float wj[4] = {wq.x, wq.y, wq.z, wq.w};
-            float v[4];
+            float v[4] = {xq.x, xq.y, xq.z, xq.w};
+            if constexpr (!PLAIN) {
+                const float4 wq = *reinterpret_cast<const float4*>(ws + c);
+                const float wj[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float q = xj[i] / root;
-                v[i] = q * wj[i];
+                for (int i = 0; i < 4; ++i) {
+                    const float q = v[i] / root;
+                    v[i] = q * wj[i];
+                }
             }
             const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
             // byte o of pair blk / 2, in the rotated layout of the staged rows
@@ -3560,24 +3571,24 @@ static bool one_fits(uint32_t kind, const uint8_t* w, uint32_t k) {
 // Rows a workgroup: about one workgroup a compute unit, within the LDS limit;
 // when the rows take more than one round of workgroups, rounds of equal
 // tiles (a last round of a few workgroups would take as long as a full one).
-static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units) {
+static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units, bool plain = false) {
     const uint32_t nb = k >> 5, rb = nb * block_bytes(kind), stride = lanes_stride(nb);
     const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
     uint32_t tr = std::max(1u, (n + cus - 1u) / cus);
-    while (tr > 1 && one_lds(k, tr, rb, stride, norm, false).end > ONE_LDS_LIMIT) --tr;
+    while (tr > 1 && one_lds(k, tr, rb, stride, norm, false, plain).end > ONE_LDS_LIMIT) --tr;
     const uint64_t per_round = (uint64_t)cus * tr;
     const uint64_t rounds = (n + per_round - 1u) / per_round;
     return std::max(1u, (uint32_t)((n + cus * rounds - 1u) / (cus * rounds)));
 }
 
-template <int KIND, bool NORM>
+template <int KIND, bool NORM, bool PLAIN = false>
 static hipError_t launch_one(const uint8_t* w, const float* x, const float* nw, float eps, Activations act, float* dst,
                              const float* bias, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
     const uint32_t nb = k >> 5, stride = lanes_stride(nb);
-    const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units);
-    const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false);
+    const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units, PLAIN);
+    const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false, PLAIN);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end, stream, w, x, nw,
+    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false, PLAIN>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end, stream, w, x, nw,
                        eps, act, dst, bias, n, k, tr, stride, Activations{});
     return hipGetLastError();
 }
@@ -3607,6 +3618,20 @@ hipError_t launch_product_one(uint32_t kind, const uint8_t* w, Activations act, 
     case 0: return launch_one<0, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
     case 1: return launch_one<1, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
     default: return launch_one<2, false>(w, nullptr, nullptr, 0.0f, act, dst, bias, n, k, compute_units, stream);
+    }
+}
+
+// One f32 row x, quantised by every workgroup in its prologue (no norm):
+// one launch, no scratch. k at most 8192 (the staged row and the tile in
+// LDS), x 16-byte aligned; hipErrorInvalidValue, nothing launched, else.
+hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* x, float* dst, const float* bias,
+                                  uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    if (k > 8192u || !one_fits(kind, w, k) || ((uintptr_t)x & 15u) != 0) return hipErrorInvalidValue;
+    switch (kind) {
+    case 0: return launch_one<0, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
+    case 1: return launch_one<1, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
+    default: return launch_one<2, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
     }
 }
 

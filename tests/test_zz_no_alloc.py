@@ -35,10 +35,12 @@ def fixed(dev, kind, w, x, dst, bias, rows, n, k, ldx=None, mode="auto"):
                                           th.MODES[mode])
 
 
-# (rows, n, k): the matrix cores (config 4's 512 x 2048 -> 2048), then the
-# lanes kernel over fewer rows, then one row over 4 MB (quantise pass +
-# lanes), then one row the one-row kernel takes (no scratch)
-CALLS = [(512, 2048, 2048), (8, 1000, 1024), (1, 4096, 2048), (1, 960, 576)]
+# (rows, n, k): the matrix cores (config 4's 512 x 2048 -> 2048), then 12
+# rows (the quantise pass and the 9-16-row kernel): both through the static
+# scratch, the second with a smaller input; then products that need no
+# scratch: 8 rows (the few-rows kernel), one row over 4 MB (the one-row
+# kernel with weights in LDS), one row the tiled one-row kernel takes
+CALLS = [(512, 2048, 2048), (12, 1000, 4096), (8, 1000, 1024), (1, 4096, 2048), (1, 960, 576)]
 
 
 @pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0", "Q4_1"])
