@@ -206,9 +206,11 @@ hipError_t launch_rows_gate_up(uint32_t kind, uint32_t mode, const uint8_t* w, c
 // hipErrorInvalidValue when the shape is not for it.
 hipError_t launch_product_one(uint32_t kind, const uint8_t* w, Activations act, float* dst, const float* bias,
                               uint32_t n, uint32_t k, int compute_units, hipStream_t stream);
-// One f32 row quantised in each workgroup's prologue (no norm), k <= 8192.
-hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* x, float* dst, const float* bias,
-                                  uint32_t n, uint32_t k, int compute_units, hipStream_t stream);
+// One or two f32 rows (ldx apart) quantised in each workgroup's prologue
+// (no norm), k <= 8192.
+hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, float* dst,
+                                  const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                                  hipStream_t stream);
 
 // dst[i] = the F16 bits of the float with word first + i, i < count.
 hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream);

@@ -459,25 +459,26 @@ __device__ __forceinline__ uint32_t stage_words(const void* src, uint32_t count,
 
 // LDS layout of k_matvec_one, in bytes from the start of its dynamic LDS.
 struct OneLds {
-    uint32_t x, nw, qs, scales, sums, totals, w, w2, part, outs, end;
+    uint32_t x, nw, qs, scales, sums, totals, arow, w, w2, part, outs, end;
 };
 
 __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_bytes, uint32_t stride, bool norm,
-                                          bool glu, bool plain = false) {
+                                          bool glu, bool plain = false, uint32_t xr = 1u) {
     const uint32_t nb = k >> 5;
     auto kb = [](uint32_t b) { return (b + 1023u) & ~1023u; };
     OneLds l;
-    l.x = 0;
-    l.nw = norm ? kb(4u * k) : 0u;
-    l.qs = norm ? (plain ? 1u : 2u) * kb(4u * k) : 0u;  // plain: no norm weights
+    l.x = 0;  // xr rows of kb(4k) bytes
+    l.nw = norm ? xr * kb(4u * k) : 0u;
+    l.qs = norm ? (plain ? xr : 2u) * kb(4u * k) : 0u;  // plain: no norm weights
     l.scales = l.qs + kb(k);
     l.sums = l.scales + ((4u * nb + 255u) & ~255u);
     l.totals = l.sums + ((4u * nb + 255u) & ~255u);
-    l.w = l.totals + kb(4u * nb);
+    l.arow = l.totals + kb(4u * nb) - l.qs;  // one quantised row and its tables; row b at + b·arow
+    l.w = l.qs + xr * l.arow;
     const uint32_t wbytes = glu ? (tr / 2u) * row_bytes : tr * row_bytes;
     l.w2 = l.w + kb(wbytes);
     l.part = glu ? l.w2 + kb(wbytes) : l.w2;
-    l.outs = l.part + 4u * tr * stride;
+    l.outs = l.part + 4u * xr * tr * stride;  // activation row b's contributions at part + b·tr rows
     l.end = l.outs + (glu ? 4u * (tr + tr / 2u) : 0u);
     return l;
 }
@@ -493,20 +494,22 @@ __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_
 //     v = x / root · nw, quantize_quad: the bits of k_rmsnorm_quantise_wave
 //     -- while the weights are in flight;
 //   NORM and PLAIN: x is the f32 row, quantised as it is (no norm; waves 0
-//     and 1 stage it, half each when its bytes are whole kilobytes);
+//     and 1 stage it, half each when its bytes are whole kilobytes); XR = 2:
+//     two rows (x and x + ldx, one a wave), each weight pair read once for
+//     both, outputs dst[b·n + row];
 //   else the row arrives quantised (act, as the quantise pass lays it out).
 // Then matvec_tile's per-pair contributions and ordered fold, from LDS:
 // dst[row] = Σ (+ bias[row], one rounding), or, GLU, SwiGLU and the
 // quantiser on the tile's gate/up outputs into glu. k a multiple of 64 with
 // ONE_THREADS % (k / 64) == 0 (whole rows of pairs per pass), rows whole
 // 16-byte pieces starting 16-byte aligned.
-template <int KIND, bool NORM, bool GLU, bool PLAIN = false>
+template <int KIND, bool NORM, bool GLU, bool PLAIN = false, uint32_t XR = 1>
 __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ nw, float eps, Activations act,
                                                             float* __restrict__ dst, const float* __restrict__ bias,
                                                             uint32_t n, uint32_t k, uint32_t tr, uint32_t stride,
-                                                            Activations glu) {
+                                                            Activations glu, uint32_t ldx) {
     extern __shared__ float4 lds4[];
     uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
     __shared__ float root_slot;
@@ -516,7 +519,9 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     const uint32_t tile = blockIdx.x, h = tr >> 1, H = n >> 1, g0 = tile * h;
     const uint32_t row0 = tile * tr, rows = GLU ? tr : min(tr, n - row0);
     static_assert(!PLAIN || (NORM && !GLU), "plain rows take the f32 path");
-    const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU, PLAIN);
+    static_assert(XR == 1 || (PLAIN && XR == 2), "two rows: plain f32 rows only");
+    const OneLds L = one_lds(k, tr, row_bytes, stride, NORM, GLU, PLAIN, XR);
+    const uint32_t xrow = (4u * k + 1023u) & ~1023u;
     const uint32_t lbase = lds_address(base);
 
     // Wave 0: the activations (NORM: x, while wave 1 brings the norm's
@@ -527,7 +532,10 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
     // x in groups of 8 pieces (a lane's 32 values of Σx²) rotated by group / 2,
     // the quantised row in groups of 4 (a pair of blocks) rotated by group /
     // 4 (stage_rotated), so that the lanes' reads below meet distinct banks
-    if constexpr (PLAIN) {
+    if constexpr (PLAIN && XR == 2) {
+        stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u);
+        stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x + ldx), 4u * k, lbase + L.x + xrow, wave, 1u);
+    } else if constexpr (PLAIN) {
         // halves of whole kilobytes (a group's rotation depends on the
         // group's index mod 16, and each half holds a multiple of 16 groups)
         const uint32_t half = (k % 512u) == 0 ? 2u * k : 4u * k;
@@ -580,9 +588,11 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
         const float4* xs4 = reinterpret_cast<const float4*>(base + L.x);
         const float* ws = reinterpret_cast<const float*>(base + L.nw);
         const float root = PLAIN ? 1.0f : root_slot;  // PLAIN: unused
+#pragma unroll
+        for (uint32_t b = 0; b < XR; ++b)
         for (uint32_t blk = t >> 3; blk < nb; blk += ONE_THREADS / 8u) {  // uniform across each 8-lane group
             const uint32_t c = blk * 32u + (t & 7u) * 4u;
-            const float4 xq = xs4[8u * blk + (((t & 7u) + (blk >> 1)) & 7u)];  // piece t % 8 of group blk
+            const float4 xq = xs4[b * (xrow / 16u) + 8u * blk + (((t & 7u) + (blk >> 1)) & 7u)];  // piece t % 8 of group blk
             float v[4] = {xq.x, xq.y, xq.z, xq.w};
             if constexpr (!PLAIN) {
                 const float4 wq = *reinterpret_cast<const float4*>(ws + c);
@@ -596,11 +606,13 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
             const Q8Quad q = quantize_quad(v[0], v[1], v[2], v[3]);
             // byte o of pair blk / 2, in the rotated layout of the staged rows
             const uint32_t pj = blk >> 1, o = (blk & 1u) * 32u + (t & 7u) * 4u;
-            *reinterpret_cast<uint32_t*>(aq + 16u * (4u * pj + (((o >> 4) + (pj >> 2)) & 3u)) + (o & 15u)) = q.packed;
+            const uint32_t ob = b * L.arow;  // row b's block of quantised values and tables
+            *reinterpret_cast<uint32_t*>(aq + ob + 16u * (4u * pj + (((o >> 4) + (pj >> 2)) & 3u)) + (o & 15u)) =
+                q.packed;
             if ((t & 7u) == 0) {
-                asc[blk] = q.scale;
-                asm_[blk] = q.sum;
-                atot[blk] = q.total;
+                reinterpret_cast<float*>(base + L.scales + ob)[blk] = q.scale;
+                reinterpret_cast<float*>(base + L.sums + ob)[blk] = q.sum;
+                reinterpret_cast<int32_t*>(base + L.totals + ob)[blk] = q.total;
             }
         }
     }
@@ -609,20 +621,30 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
 
     // This thread's pair of the row (j = t % np: whole rows of pairs per pass).
     const uint32_t j = t % np, rpass = ONE_THREADS / np;
-    uint32_t a[16];
-    {
-        const uint4* q4 = reinterpret_cast<const uint4*>(aq) + 4u * j;  // the pair's pieces, rotated by j / 4
+    uint32_t a[XR][16];
+    float sx0[XR], sx1[XR], mx0[XR], mx1[XR];
+    int e0[XR], e1[XR];
+#pragma unroll
+    for (uint32_t b = 0; b < XR; ++b) {
+        const uint32_t ob = b * L.arow;
+        const uint4* q4 = reinterpret_cast<const uint4*>(aq + ob) + 4u * j;  // the pair's pieces, rotated by j / 4
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint4 v = q4[(i + (j >> 2)) & 3u];
-            a[4 * i] = v.x, a[4 * i + 1] = v.y, a[4 * i + 2] = v.z, a[4 * i + 3] = v.w;
+            a[b][4 * i] = v.x, a[b][4 * i + 1] = v.y, a[b][4 * i + 2] = v.z, a[b][4 * i + 3] = v.w;
+        }
+        const float* bsc = reinterpret_cast<const float*>(base + L.scales + ob);
+        sx0[b] = bsc[2u * j], sx1[b] = bsc[2u * j + 1u];
+        e0[b] = 0, e1[b] = 0, mx0[b] = 0.0f, mx1[b] = 0.0f;
+        if constexpr (KIND == 1) {
+            const int32_t* bt = reinterpret_cast<const int32_t*>(base + L.totals + ob);
+            e0[b] = -8 * bt[2u * j], e1[b] = -8 * bt[2u * j + 1u];
+        }
+        if constexpr (KIND == 2) {
+            const float* bs = reinterpret_cast<const float*>(base + L.sums + ob);
+            mx0[b] = bs[2u * j], mx1[b] = bs[2u * j + 1u];
         }
     }
-    const float sx0 = asc[2u * j], sx1 = asc[2u * j + 1u];
-    int e0 = 0, e1 = 0;
-    float mx0 = 0.0f, mx1 = 0.0f;
-    if constexpr (KIND == 1) e0 = -8 * atot[2u * j], e1 = -8 * atot[2u * j + 1u];
-    if constexpr (KIND == 2) mx0 = asm_[2u * j], mx1 = asm_[2u * j + 1u];
     float* part = reinterpret_cast<float*>(base + L.part);
     // up to UNITS rows' pairs read from LDS together, then their
     // contributions (one LDS latency a batch rather than a row)
@@ -642,18 +664,23 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
         for (uint32_t q = 0; q < UNITS; ++q) {
             const uint32_t r = r0 + q * rpass;
             if (r < rows) {
-                float c0, c1;
-                Pair<KIND>::contribute(u[q], a, sx0, sx1, e0, e1, mx0, mx1, c0, c1);
-                *(float2*)(part + (size_t)r * stride + 2u * j) = make_float2(c0, c1);
+#pragma unroll
+                for (uint32_t b = 0; b < XR; ++b) {
+                    float c0, c1;
+                    Pair<KIND>::contribute(u[q], a[b], sx0[b], sx1[b], e0[b], e1[b], mx0[b], mx1[b], c0, c1);
+                    *(float2*)(part + (size_t)(b * tr + r) * stride + 2u * j) = make_float2(c0, c1);
+                }
             }
         }
     }
     lds_sync();
     float* outs = reinterpret_cast<float*>(base + L.outs);
-    for (uint32_t o = t; o < rows; o += ONE_THREADS) {
-        // the row's contributions in block order, read 64 at a time into
-        // registers before they are added (an LDS read's latency once a batch)
-        const float* c = part + (size_t)o * stride;
+    for (uint32_t ob = t; ob < XR * rows; ob += ONE_THREADS) {
+        // output o of activation row b: its contributions in block order,
+        // read 64 at a time into registers before they are added (an LDS
+        // read's latency once a batch)
+        const uint32_t b = XR == 2 && ob >= rows ? 1u : 0u, o = ob - b * rows;
+        const float* c = part + (size_t)(b * tr + o) * stride;
         float sum = 0.0f;
         uint32_t i = 0;
         for (; i + 64u <= nb; i += 64u) {
@@ -680,7 +707,7 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
             outs[o] = sum;
         } else {
             const uint32_t row = row0 + o;
-            dst[row] = bias ? sum + bias[row] : sum;
+            dst[(size_t)b * n + row] = bias ? sum + bias[row] : sum;
         }
     }
     if constexpr (GLU) {
@@ -3571,25 +3598,27 @@ static bool one_fits(uint32_t kind, const uint8_t* w, uint32_t k) {
 // Rows a workgroup: about one workgroup a compute unit, within the LDS limit;
 // when the rows take more than one round of workgroups, rounds of equal
 // tiles (a last round of a few workgroups would take as long as a full one).
-static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units, bool plain = false) {
+static uint32_t one_tile(uint32_t kind, uint32_t n, uint32_t k, bool norm, int compute_units, bool plain = false,
+                         uint32_t xr = 1u) {
     const uint32_t nb = k >> 5, rb = nb * block_bytes(kind), stride = lanes_stride(nb);
     const uint32_t cus = (uint32_t)(compute_units > 0 ? compute_units : 256);
     uint32_t tr = std::max(1u, (n + cus - 1u) / cus);
-    while (tr > 1 && one_lds(k, tr, rb, stride, norm, false, plain).end > ONE_LDS_LIMIT) --tr;
+    while (tr > 1 && one_lds(k, tr, rb, stride, norm, false, plain, xr).end > ONE_LDS_LIMIT) --tr;
     const uint64_t per_round = (uint64_t)cus * tr;
     const uint64_t rounds = (n + per_round - 1u) / per_round;
     return std::max(1u, (uint32_t)((n + cus * rounds - 1u) / (cus * rounds)));
 }
 
-template <int KIND, bool NORM, bool PLAIN = false>
+template <int KIND, bool NORM, bool PLAIN = false, uint32_t XR = 1>
 static hipError_t launch_one(const uint8_t* w, const float* x, const float* nw, float eps, Activations act, float* dst,
-                             const float* bias, uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+                             const float* bias, uint32_t n, uint32_t k, int compute_units, hipStream_t stream,
+                             uint32_t ldx = 0) {
     const uint32_t nb = k >> 5, stride = lanes_stride(nb);
-    const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units, PLAIN);
-    const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false, PLAIN);
+    const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units, PLAIN, XR);
+    const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false, PLAIN, XR);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false, PLAIN>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end, stream, w, x, nw,
-                       eps, act, dst, bias, n, k, tr, stride, Activations{});
+    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false, PLAIN, XR>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end,
+                       stream, w, x, nw, eps, act, dst, bias, n, k, tr, stride, Activations{}, ldx);
     return hipGetLastError();
 }
 
@@ -3621,18 +3650,28 @@ hipError_t launch_product_one(uint32_t kind, const uint8_t* w, Activations act, 
     }
 }
 
-// One f32 row x, quantised by every workgroup in its prologue (no norm):
-// one launch, no scratch. k at most 8192 (the staged row and the tile in
-// LDS), x 16-byte aligned; hipErrorInvalidValue, nothing launched, else.
-hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* x, float* dst, const float* bias,
-                                  uint32_t n, uint32_t k, int compute_units, hipStream_t stream) {
+// One or two f32 rows x (ldx apart), quantised by every workgroup in its
+// prologue (no norm): one launch, no scratch. k at most 8192 (the staged
+// rows and the tile in LDS), rows 16-byte aligned; hipErrorInvalidValue,
+// nothing launched, else.
+hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, float* dst,
+                                  const float* bias, uint32_t rows, uint32_t n, uint32_t k, int compute_units,
+                                  hipStream_t stream) {
     if (n == 0) return hipSuccess;
-    if (k > 8192u || !one_fits(kind, w, k) || ((uintptr_t)x & 15u) != 0) return hipErrorInvalidValue;
+    if (rows < 1u || rows > 2u || k > 8192u || !one_fits(kind, w, k) || ((uintptr_t)x & 15u) != 0 ||
+        (rows == 2u && ldx % 4u != 0))
+        return hipErrorInvalidValue;
+#define TMH_F32_ONE(KIND)                                                                                          \
+    return rows == 1u ? launch_one<KIND, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k,          \
+                                                     compute_units, stream)                                       \
+                      : launch_one<KIND, true, true, 2>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k,       \
+                                                        compute_units, stream, ldx);
     switch (kind) {
-    case 0: return launch_one<0, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
-    case 1: return launch_one<1, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
-    default: return launch_one<2, true, true>(w, x, nullptr, 0.0f, Activations{}, dst, bias, n, k, compute_units, stream);
+    case 0: TMH_F32_ONE(0)
+    case 1: TMH_F32_ONE(1)
+    default: TMH_F32_ONE(2)
     }
+#undef TMH_F32_ONE
 }
 
 template <int KIND>
@@ -3642,7 +3681,7 @@ static hipError_t launch_glu_one(const uint8_t* w, const float* x, const float* 
     const OneLds L = one_lds(k, 2u * h, nb * Fmt<KIND>::BB, stride, true, true);
     if (L.end > ONE_LDS_LIMIT || H % h != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_matvec_one<KIND, true, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w, x, norm, eps,
-                       Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu);
+                       Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu, 0u);
     return hipGetLastError();
 }
 

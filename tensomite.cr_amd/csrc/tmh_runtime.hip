@@ -735,12 +735,13 @@ int check_product(uint32_t kind, uint32_t rows, uint32_t n, uint32_t k, uint32_t
 // about 10).
 constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
 
-// AUTO products of one row above ROW_KERNEL_MAX_BYTES: the one-row kernel
-// with weights in LDS, which quantises x in every workgroup's prologue;
-// where it does not fit, and for 2 to 8 rows: the few-rows kernel with
-// weights in LDS, which does the same (k at most 2048), one launch and no
-// scratch (measured, Q4_1 8192x2048: 7.4 / 8.1 / 9.0 us a call at 2 / 4 / 8
-// rows, against 8.2 / 9.8 / 9.8 for the quantise pass and the product).
+// AUTO products of one row above ROW_KERNEL_MAX_BYTES, and of two rows of
+// k up to 2048: the one-row kernel with weights in LDS, which quantises x in
+// every workgroup's prologue; where it does not fit, and for 2 to 8 rows:
+// the few-rows kernel with weights in LDS, which does the same (k at most
+// 2048), one launch and no scratch (measured, Q4_1 8192x2048: 7.4 / 8.1 /
+// 9.0 us a call at 2 / 4 / 8 rows, against 8.2 / 9.8 / 9.8 for the quantise
+// pass and the product).
 // hipErrorInvalidValue, nothing launched, when the call is not for it.
 // TMH_FEW_ROWS_KERNEL=lanes keeps the quantise pass and the lanes product,
 // for comparisons.
@@ -753,16 +754,20 @@ hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const 
     const uint64_t bytes = (uint64_t)n * (k / 32u) * tmh::block_bytes(kind);
     if (lanes || mode != TMH_MODE_AUTO || rows > 8u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
         return hipErrorInvalidValue;
-    // One row: the one-row kernel quantising x in its prologue, k up to 8192
-    // (measured, Q4_1, one box: 8192x2048 5.35 us a call against 6.38 for
-    // the few-rows kernel, 2048x8192 7.46 against 8.98 for the quantise pass
-    // and the one-row kernel). TMH_ONE_F32=0 keeps those, for comparisons.
+    // One row (k up to 8192), or two of k up to 2048: the one-row kernel
+    // quantising x in its prologue (measured, Q4_1, one box: 8192x2048 one
+    // row 5.35 us a call against 6.38 for the few-rows kernel, two rows 6.00
+    // against 7.35; 2048x8192 one row 7.46 against 8.98 for the quantise pass
+    // and the one-row kernel, two rows 10.85 against 10.66 for the quantise
+    // pass and the lanes kernel, so not taken). TMH_ONE_F32=0 keeps the other
+    // kernels, for comparisons.
     static const bool one_f32 = [] {
         const char* env = getenv("TMH_ONE_F32");
         return !(env && strcmp(env, "0") == 0);
     }();
-    if (rows == 1u && one_f32) {
-        const hipError_t e = tmh::launch_product_f32_one(kind, w, x, dst, bias, n, k, d.compute_units, d.stream);
+    if (one_f32 && (rows == 1u || (rows == 2u && k <= 2048u))) {
+        const hipError_t e =
+            tmh::launch_product_f32_one(kind, w, x, ldx, dst, bias, rows, n, k, d.compute_units, d.stream);
         if (e != hipErrorInvalidValue) return e;
     }
     return tmh::launch_rows_product(kind, tmh::NB_F32, w, x, ldx, nullptr, 0.0f, tmh::Activations{}, dst, bias, 0u,

@@ -217,23 +217,29 @@ def test_one_row_over_4mb_with_bias(dev, fmt, n, k):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("n,k", [(1000, 4096), (1200, 8192), (2049, 8192)])
-def test_one_long_row_quantised_in_kernel(dev, fmt, n, k):
-    # One row of more than 2048 values over 4 MB of weights: the one-row
-    # kernel quantises x in its prologue (no norm). Whole blocks of zeros
-    # (scale 0), a spike, exact halves (rounding ties), a ragged last tile.
+@pytest.mark.parametrize("n,k", [(1000, 4096), (1200, 8192), (2049, 8192), (8192, 2048)])
+@pytest.mark.parametrize("rows", [1, 2])
+def test_one_long_row_quantised_in_kernel(dev, fmt, n, k, rows):
+    # One row over 4 MB of weights (and two rows, rows ldx apart): the
+    # one-row kernel quantises x in its prologue (no norm). Whole blocks of
+    # zeros (scale 0), a spike, exact halves (rounding ties), a ragged last
+    # tile; the second row Gaussian.
     wq = weights(fmt, n, k, n * 7 + k)
     if wq.nbytes <= 4 << 20:
         wq = np.concatenate([wq] * 2)
         n *= 2
-    say("one long row", fmt, n, k)
-    x = acts(1, k, k + 9)
+    say("long rows", fmt, rows, n, k)
+    x = acts(rows, k, k + 9)
     x[:256] = 0.0
     x[300] = 1e4
     x[1024:1536] = (np.arange(512) % 255 - 127).astype(np.float32) * np.float32(0.5)
+    ldx = k + 32
+    strided = np.zeros(rows * ldx, np.float32)
+    for r in range(rows):
+        strided[r * ldx:r * ldx + k] = x[r * k:(r + 1) * k]
     bias = acts(1, n, 8)
-    want = oracle.add_bias(oracle.matmul(fmt, x, wq, 1, n, k), bias)
-    got = run_product(dev, fmt, wq, x, 1, n, k, bias=bias)
+    want = oracle.add_bias(oracle.matmul(fmt, x, wq, rows, n, k), bias)
+    got = run_product(dev, fmt, wq, strided, rows, n, k, bias=bias, ldx=ldx)
     assert np.array_equal(bits(got), bits(want))
 
 
