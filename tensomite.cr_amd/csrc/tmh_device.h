@@ -68,7 +68,12 @@ struct Q8Quad {
 };
 
 __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, float v3) {
+    // The host's amax starts at the block's first value and skips every
+    // later NaN (a comparison with NaN is false), so a lane other than the
+    // block's first (the 8 lanes of a block are threadIdx.x / 8's group, the
+    // quarter threadIdx.x % 8) skips a NaN in its own first value as well.
     float amax = fabsf(v0);
+    if ((threadIdx.x & 7u) != 0 && amax != amax) amax = 0.0f;
     amax = fabsf(v1) > amax ? fabsf(v1) : amax;
     amax = fabsf(v2) > amax ? fabsf(v2) : amax;
     amax = fabsf(v3) > amax ? fabsf(v3) : amax;

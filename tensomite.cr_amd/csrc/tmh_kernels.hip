@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256) void k_quantize_rows_q8(const float* __restric
         v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
     }
     float amax = fabsf(v0);
+    if (sub != 0 && amax != amax) amax = 0.0f;  // a NaN not first in its block is skipped, as the host's loop does
     amax = fabsf(v1) > amax ? fabsf(v1) : amax;
     amax = fabsf(v2) > amax ? fabsf(v2) : amax;
     amax = fabsf(v3) > amax ? fabsf(v3) : amax;

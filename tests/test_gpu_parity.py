@@ -282,19 +282,22 @@ def test_few_rows_nan_and_inf_blocks(dev, fmt):
     # block's first value (quant.cr:428-442); the few-rows kernel's lane-a-
     # block quantiser takes it as a tree. Blocks with a NaN first, a NaN in
     # the middle, and an inf, in every row count of the one-launch form.
+    # A NaN first in a lane's 4 values (block index 4j, j >= 1) is inside
+    # its block too: the 8-lane quantisers skip it like any other.
     n, k = 700, 512
     wq = weights(fmt, n, k, 41)
-    x = acts(8, k, 42)
-    for r in range(8):
+    x = acts(10, k, 42)
+    for r in range(10):
         x[r * k + 32 * 9 + 5 + r] = np.nan  # inside a block: skipped by amax, quantised to 0
         x[r * k + 32 * 3 + 31 - r] = np.nan
+        x[r * k + 32 * 5 + 4 * (1 + r % 7)] = np.nan  # first of lane 1 + r % 7's values
     x[4 * k + 32 * 6] = np.nan  # first in its block: the block's scale is NaN
     x[5 * k + 32 * 2] = np.nan
     x[6 * k + 32 * 12 + 6] = np.inf
     x[7 * k + 32 * 1] = -np.inf
-    want = oracle.matmul(fmt, x, wq, 8, n, k)
+    want = oracle.matmul(fmt, x, wq, 10, n, k)
     wbuf, xbuf = dev.from_array(wq), dev.from_array(x)
-    for rows in range(1, 9):
+    for rows in range(1, 11):  # 9 and 10: the quantise pass and the 9-16-row kernel
         say("nan rows", fmt, rows)
         out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k)
         got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
