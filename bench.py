@@ -29,8 +29,15 @@ Beside it, in the same line:
                after the same prompt, and its tokens against the GPU's.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-    python bench.py --batched     # config 3, its own line
-    python bench.py --gemm        # config 4, its own line
+  config3      config 3: Q4_1 batched-decode products, both shapes, B = 1..16,
+               each point with its roofline and CPU baseline.
+  config4      config 4: the Q8_0 prefill GEMM, N = 2048 and 8192, ordered
+               (AUTO) and UNORDERED, each with its MFMA roofline; CPU baseline.
+  host_memory  the host's STREAM-style copy rate (numpy, every core), beside
+               the CPU baselines.
+
+    python bench.py --batched     # config 3 alone, its own line
+    python bench.py --gemm        # config 4 alone, its own line
     python bench.py --decode-only # config 5, its own line
     python bench.py --write-gguf DIR   # the configs' weights as GGUF files
 """
@@ -522,106 +529,239 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
         model.destroy()
         log(f"decode batch {rows}: {ms * 1e3:.0f} us/step")
     if with_cpu:
+        # The same steps the GPU's batch 1 times: the 128-token prompt
+        # (untimed), then `steps` - 1 decode forwards at positions
+        # 128..126 + steps, each timed; the median and mean a token.
         from oracle import oracle
         host = host_cpu()
         variant = oracle.best_variant()
         oracle.set_threads(host["cores"], variant)
         cpu = oracle.Llama(config, weights, variant)
         logits = cpu.forward(prompts[0], last_only=True)[0]
-        cpu_tokens, start = [], time.perf_counter()
-        while True:
-            cpu_tokens.append(oracle.argmax(logits))
-            if time.perf_counter() - start >= cpu_seconds or len(cpu_tokens) >= 64:
-                break
+        cpu_tokens, per = [oracle.argmax(logits)], []
+        start = time.perf_counter()
+        while len(cpu_tokens) < steps and time.perf_counter() - start < cpu_seconds:
+            t = time.perf_counter()
             logits = cpu.forward([cpu_tokens[-1]], last_only=True)[0]
-        elapsed = time.perf_counter() - start
-        decoded = len(cpu_tokens) - 1
+            per.append(time.perf_counter() - t)
+            cpu_tokens.append(oracle.argmax(logits))
+        decoded = len(per)
+        ms = statistics.median(per) * 1e3 if per else None
         out["cpu_baseline"] = {
-            "ms_per_token": round(elapsed / max(decoded, 1) * 1e3, 1), "cores": host["cores"], "kind": "port",
-            "sample": f"{decoded} greedy decode steps at positions 128..{128 + decoded - 1}, after the GPU's "
-                      f"batch-1 128-token prompt (prefill excluded); the oracle's Llama forward ({variant} build, "
-                      f"{host['cores']} threads)",
+            "value": round(1e3 / ms, 2) if ms else None, "unit": "tokens/s", "cores": host["cores"], "kind": "port",
+            "ms_per_token": round(ms, 2) if ms else None,
+            "ms_per_token_mean": round(sum(per) / decoded * 1e3, 2) if per else None,
+            "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1) if ms else None,
+            "sample": f"{decoded} greedy decode steps at positions 128..{127 + decoded} (the GPU's batch-1 timed "
+                      f"steps are 128..{126 + steps}), after the same 128-token prompt (prefill excluded); the "
+                      f"oracle's Llama forward ({variant} build, {host['cores']} threads); median a token",
             "tokens_equal_gpu": gpu_tokens is not None and cpu_tokens == gpu_tokens[:len(cpu_tokens)],
             "tokens_compared": len(cpu_tokens)}
     return out
 
 
+def host_memory_rate(cores, mbytes=1024, seconds=1.0):
+    """The host's STREAM-style copy rate: `cores` threads each copying its
+    share of a `mbytes` MB array (numpy releases the GIL while copying);
+    GB/s counts the bytes read plus written. It bounds what a CPU baseline
+    that streams weights from DRAM can reach on this host."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    n = (mbytes << 20) // 8
+    src = np.ones(n, np.float64)
+    dst = np.empty_like(src)
+    bounds = [(i * n // cores, (i + 1) * n // cores) for i in range(cores)]
+
+    def part(i):
+        a, b = bounds[i]
+        np.copyto(dst[a:b], src[a:b])
+
+    rates = []
+    with ThreadPoolExecutor(cores) as pool:
+        list(pool.map(part, range(cores)))  # pages touched
+        start = time.perf_counter()
+        while time.perf_counter() - start < seconds or len(rates) < 3:
+            t = time.perf_counter()
+            list(pool.map(part, range(cores)))
+            rates.append(2 * src.nbytes / (time.perf_counter() - t) / 1e9)
+    return {"copy_GB_per_s": round(max(rates), 1), "copy_GB_per_s_median": round(statistics.median(rates), 1),
+            "threads": cores, "array_bytes": int(src.nbytes),
+            "method": "numpy copyto of a 1 GiB float64 array split over the threads; read + write bytes"}
+
+
 # ---------------------------------------------------------------- config 3
 
-def batched_config3(dev, steps, warmup):
+C3_SHAPES = ((8192, 2048), (2048, 8192))
+C3_ROWS = (1, 2, 4, 8, 16)
+
+
+def cpu_rate(kind, x, w, rows, n, k, seconds, variant, cores):
+    """The oracle's Quant.matmul (`variant` build, `cores` threads) repeated
+    for about `seconds` (at least twice): seconds a call, and the last output."""
+    from oracle import oracle
+
+    oracle.set_threads(cores, variant)
+    out = oracle.matmul(kind, x, w, rows, n, k, variant)  # warm: pages, pool
+    calls, start = 0, time.perf_counter()
+    while True:
+        out = oracle.matmul(kind, x, w, rows, n, k, variant)
+        calls += 1
+        elapsed = time.perf_counter() - start
+        if calls >= 2 and elapsed >= seconds:
+            break
+    return elapsed / calls, calls, out
+
+
+def config3(dev, warmup, cpu_seconds=None):
     """Config 3: Q4_1 batched-decode products, W [8192, 2048] and [2048, 8192]
-    against B = 1, 2, 4, 8, 16 activation rows. One call is tmh_block_matmul
-    over f32 x (the activation quantiser, then the lanes product); calls
-    rotate through enough weight copies (>= 512 MB) that the 256 MB Infinity
-    Cache cannot serve them; HIP events every 10 calls, the median over 100 groups.
-    Bytes a call: weights + 4·B·K of x + 4·B·N of y."""
+    (W ~ N(0, 0.02) quantised, seed 0x5EED0003 + n) against B = 1, 2, 4, 8,
+    16 f32 activation rows (x ~ N(0, 1)). One call is tmh_block_matmul in
+    AUTO mode (whatever kernels it takes: one launch below 8 rows of K =
+    2048, the quantise pass and a product otherwise). Calls rotate through
+    enough weight copies (>= 512 MB) that the 256 MB Infinity Cache cannot
+    serve them; HIP events every 10 calls, the median over 100 groups.
+    Bytes a call: weights + 4·B·K of x + 4·B·N of y (HBM-bound at every B).
+    Every point's output bits are checked against the oracle; with
+    cpu_seconds, the oracle's Quant.matmul restatement is timed on the same
+    bytes (portable and native builds, every host core)."""
     import quant_host
-    out = {"metric": "Q4_1 batched-decode product GB/s (config 3)", "unit": "GB/s", "n_gpus": 1, "steps": steps,
-           "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
-           "data": "synthetic: W ~ N(0,0.02) quantised to Q4_1, x ~ N(0,1)", "shapes": {}}
+    from oracle import oracle
+
+    host = host_cpu()
+    variants = list(dict.fromkeys(["portable", oracle.best_variant()]))
+    out = {"workload": "config 3: Q4_1 batched-decode products, [8192, 2048] and [2048, 8192] x B f32 rows",
+           "unit": "GB/s", "points": {}}
     rng = np.random.default_rng(0x5EED0003)
-    for n, k in ((8192, 2048), (2048, 8192)):
-        host = quant_host.synthetic_weights("Q4_1", n, k, seed=0x5EED0003 + n)
-        copies = max(2, math.ceil(2 * MALL_BYTES / host.nbytes))
-        first = dev.from_array(host)
-        ws = [first] + [dev.alloc(host.nbytes) for _ in range(copies - 1)]
+    for n, k in C3_SHAPES:
+        wq = quant_host.synthetic_weights("Q4_1", n, k, seed=0x5EED0003 + n)
+        copies = max(2, math.ceil(2 * MALL_BYTES / wq.nbytes))
+        first = dev.from_array(wq)
+        ws = [first] + [dev.alloc(wq.nbytes) for _ in range(copies - 1)]
         for w in ws[1:]:
-            dev.copy(w, first, host.nbytes)
-        for b in (1, 2, 4, 8, 16):
-            x = dev.from_array(rng.standard_normal((b, k), dtype=np.float32))
+            dev.copy(w, first, wq.nbytes)
+        for b in C3_ROWS:
+            xh = rng.standard_normal((b, k), dtype=np.float32)
+            x = dev.from_array(xh)
             dst = dev.alloc(4 * b * n)
             call = lambda i: dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst)
             warm_up(dev, call, warmup)
             per, _ = time_launches(dev, call, ROOFLINE_GROUPS * 10, 10)
-            nbytes = host.nbytes + 4 * b * k + 4 * b * n
+            nbytes = wq.nbytes + 4 * b * k + 4 * b * n
             st = launch_stats(per, nbytes, 10)
-            out["shapes"][f"{n}x{k} B={b}"] = {"us_per_call_median": st["median_us"], "us_per_call_mean": st["mean_us"],
-                                               "GB_per_s": st["GB_per_s_median"],
-                                               "hbm_peak_frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 3)}
+            got = dev.to_array(dst, np.float32, b * n).reshape(b, n)
+            point = {"us_per_call_median": st["median_us"], "us_per_call_mean": st["mean_us"],
+                     "algorithmic_bytes": nbytes, "weight_copies_rotated": copies,
+                     "roofline": {"bound": "hbm", "achieved": st["GB_per_s_median"], "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 4)}}
+            want = oracle.matmul("Q4_1", xh, wq, b, n, k, oracle.best_variant())
+            point["bit_exact_vs_oracle"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            if cpu_seconds:
+                builds = {}
+                for variant in variants:
+                    sec, calls, _ = cpu_rate("Q4_1", xh, wq, b, n, k, cpu_seconds, variant, host["cores"])
+                    builds[variant] = {"GB_per_s": round(nbytes / sec / 1e9, 2), "us_per_call": round(sec * 1e6, 1),
+                                       "calls": calls}
+                best = max(builds, key=lambda v: builds[v]["GB_per_s"])
+                point["cpu_baseline"] = {"value": builds[best]["GB_per_s"], "unit": "GB/s", "cores": host["cores"],
+                                         "kind": "port", "build": best, "builds": builds}
+            out["points"][f"{n}x{k} B={b}"] = point
             x.release()
             dst.release()
         for w in ws:
             w.release()
-    out["value"] = out["shapes"]["8192x2048 B=1"]["GB_per_s"]
+    pts = out["points"]
+    out["value"] = pts["8192x2048 B=1"]["roofline"]["achieved"]
+    out["roofline_frac_min"] = min(p["roofline"]["frac"] for p in pts.values())
+    out["roofline_frac_max"] = max(p["roofline"]["frac"] for p in pts.values())
+    out["bit_exact_vs_oracle"] = all(p["bit_exact_vs_oracle"] for p in pts.values())
+    if cpu_seconds:
+        head = pts["8192x2048 B=1"]["cpu_baseline"]
+        out["cpu_baseline"] = {
+            "value": head["value"], "unit": "GB/s", "cores": host["cores"], "kind": "port",
+            "sample": f"each of the 10 points (2 shapes x B = 1..16) repeated for ~{cpu_seconds:g} s per build "
+                      f"(portable and {oracle.best_variant()}), the oracle's Quant.matmul restatement with the "
+                      f"reference's span rule and spin pool, {host['cores']} threads; value: 8192x2048 B=1, "
+                      f"each point's own figure under points[].cpu_baseline (weights 10.5 MB: the host's caches "
+                      f"hold part of them between calls)",
+            "host": host}
     return out
 
 
 # ---------------------------------------------------------------- config 4
 
-def gemm_config4(dev, steps, warmup, mode="auto"):
+def config4(dev, warmup, cpu_seconds=None):
     """Config 4: the Q8_0 prefill GEMM at the Llama-1.7B shape, 512 tokens x
     K = 2048 against N = 2048 (attention projections) and N = 8192 (MLP
-    up/gate). One call is tmh_block_matmul over f32 x (the activation
-    quantiser, then the matrix-core kernel, k_matmul_mx); HIP events every
-    4 calls, the median over 100 groups. int8 work: 2 · 512 · 2048 · N ops a call.
-    mode "unordered" runs the same kernel with each block's contribution
-    added by one fused multiply-add (measurement only: it prices the
-    host-ordered, separately rounded fold)."""
+    up/gate), W ~ N(0, 0.02) quantised (seed 0x5EED0004 + N), x ~ N(0, 1).
+    One call is tmh_block_matmul over f32 x (the activation quantiser, then
+    the matrix-core kernel k_matmul_mx); HIP events every 4 calls, the median
+    over 100 groups. int8 work: 2 · 512 · 2048 · N ops a call; bytes: weights
+    + 4·512·K of x + 4·512·N of y. Each N runs in AUTO (the host's ordered,
+    separately rounded fold; its bits checked against the oracle) and in
+    UNORDERED (one fused multiply-add per output and block: measurement
+    only, the price of the host's order). With cpu_seconds, the oracle's
+    Quant.matmul restatement on the same bytes (portable and native builds,
+    every host core)."""
     import quant_host
-    import tensomite_hip as th
+    from oracle import oracle
+
+    host = host_cpu()
+    variants = list(dict.fromkeys(["portable", oracle.best_variant()]))
     rows, k = 512, 2048
     rng = np.random.default_rng(0x5EED0004)
-    x = dev.from_array(rng.standard_normal((rows, k), dtype=np.float32))
-    out = {"metric": "Q8_0 prefill GEMM int8 TOP/s (config 4, 512 tokens x K=2048)", "unit": "TOP/s",
-           "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True, "dtype": "int8 dot + f32 fold",
-           "mode": mode, "data": "synthetic: W ~ N(0,0.02) quantised to Q8_0, x ~ N(0,1)", "shapes": {}}
+    xh = rng.standard_normal((rows, k), dtype=np.float32)
+    x = dev.from_array(xh)
+    out = {"workload": "config 4: Q8_0 prefill GEMM, 512 tokens x K=2048 -> N = 2048 and 8192", "unit": "TOP/s",
+           "points": {}}
     for n in (2048, 8192):
-        w = dev.from_array(quant_host.synthetic_weights("Q8_0", n, k, seed=0x5EED0004 + n))
+        wq = quant_host.synthetic_weights("Q8_0", n, k, seed=0x5EED0004 + n)
+        w = dev.from_array(wq)
         dst = dev.alloc(4 * rows * n)
-        call = lambda i: dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst, mode=mode)
-        warm_up(dev, call, warmup)
-        per, _ = time_launches(dev, call, ROOFLINE_GROUPS * 4, 4)
-        med = statistics.median(per)
         ops = 2.0 * rows * k * n
-        tops = ops / (med * 1e-3) / 1e12
-        out["shapes"][f"N={n}"] = {"us_per_call_median": round(med * 1e3, 2),
-                                   "us_per_call_mean": round(sum(per) / len(per) * 1e3, 2),
-                                   "TOP_per_s": round(tops, 1),
-                                   "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
-                                                "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4)}}
+        nbytes = wq.nbytes + 4 * rows * k + 4 * rows * n
+        want = oracle.matmul("Q8_0", xh, wq, rows, n, k, oracle.best_variant())
+        for mode in ("auto", "unordered"):
+            call = lambda i: dev.block_matmul("Q8_0", w, x, rows, n, k, dst=dst, mode=mode)
+            warm_up(dev, call, warmup)
+            per, _ = time_launches(dev, call, ROOFLINE_GROUPS * 4, 4)
+            med = statistics.median(per)
+            tops = ops / (med * 1e-3) / 1e12
+            got = dev.to_array(dst, np.float32, rows * n).reshape(rows, n)
+            point = {"us_per_call_median": round(med * 1e3, 2), "us_per_call_mean": round(sum(per) / len(per) * 1e3, 2),
+                     "int8_ops": ops, "algorithmic_bytes": nbytes,
+                     "GB_per_s": round(nbytes / (med * 1e-3) / 1e9, 1),
+                     "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                                  "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4)}}
+            if mode == "auto":
+                point["bit_exact_vs_oracle"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            else:
+                rel = float(np.linalg.norm((got - want).astype(np.float64)) / np.linalg.norm(want.astype(np.float64)))
+                point["relative_l2_vs_oracle"] = rel
+            out["points"][f"N={n} {mode}"] = point
+        if cpu_seconds:
+            builds = {}
+            for variant in variants:
+                sec, calls, _ = cpu_rate("Q8_0", xh, wq, rows, n, k, cpu_seconds, variant, host["cores"])
+                builds[variant] = {"TOP_per_s": round(ops / sec / 1e12, 3), "ms_per_call": round(sec * 1e3, 2),
+                                   "calls": calls}
+            best = max(builds, key=lambda v: builds[v]["TOP_per_s"])
+            out["points"][f"N={n} auto"]["cpu_baseline"] = {
+                "value": builds[best]["TOP_per_s"], "unit": "TOP/s", "cores": host["cores"], "kind": "port",
+                "build": best, "builds": builds}
         w.release()
         dst.release()
-    out["value"] = out["shapes"]["N=8192"]["TOP_per_s"]
+    x.release()
+    pts = out["points"]
+    out["value"] = pts["N=8192 auto"]["roofline"]["achieved"]
+    out["bit_exact_vs_oracle"] = all(p.get("bit_exact_vs_oracle", True) for p in pts.values())
+    if cpu_seconds:
+        out["cpu_baseline"] = {
+            "value": pts["N=8192 auto"]["cpu_baseline"]["value"], "unit": "TOP/s", "cores": host["cores"],
+            "kind": "port",
+            "sample": f"each N repeated for ~{cpu_seconds:g} s (at least 2 calls) per build (portable and "
+                      f"{oracle.best_variant()}), the oracle's Quant.matmul restatement, {host['cores']} threads; "
+                      f"value: N=8192",
+            "host": host}
     return out
 
 
@@ -640,7 +780,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="CPU baseline sample for configs 1, 2 and 5 (config 5 stops at the GPU's step count)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode measurement")
     ap.add_argument("--no-config1", action="store_true", help="skip the config-1 (GPT-2 c_attn) measurement")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -648,7 +789,10 @@ def main():
                     help="config 3 instead (Q4_1 batched-decode products, B = 1..16); its own JSON line")
     ap.add_argument("--gemm", action="store_true",
                     help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
-    ap.add_argument("--gemm-mode", default="auto", help="config 4's BlockMatMulMode (auto, matrix, unordered)")
+    ap.add_argument("--no-config3", action="store_true", help="skip the config-3 (Q4_1 batched) measurement")
+    ap.add_argument("--no-config4", action="store_true", help="skip the config-4 (Q8_0 prefill GEMM) measurement")
+    ap.add_argument("--cpu-point-seconds", type=float, default=0.4,
+                    help="CPU baseline sample per config-3/4 point and build")
     ap.add_argument("--decode-only", action="store_true",
                     help="config 5 only (decode at batch 1 and 8); its own JSON line")
     ap.add_argument("--decode-eager", action="store_true",
@@ -672,20 +816,29 @@ def main():
 
     dev = th.HIPDevice(0)
     log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
+    cpu_points = None if args.no_cpu else args.cpu_point_seconds
     if args.gemm:
-        print(json.dumps(gemm_config4(dev, args.steps, args.warmup, args.gemm_mode)), flush=True)
+        print(json.dumps(config4(dev, args.warmup, cpu_points)), flush=True)
         return
     if args.batched:
-        print(json.dumps(batched_config3(dev, args.steps, args.warmup)), flush=True)
+        print(json.dumps(config3(dev, args.warmup, cpu_points)), flush=True)
         return
     if args.decode_only:
         print(json.dumps(decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
                                      graph=not args.decode_eager)), flush=True)
         return
     result = config2(dev, args)
+    if not args.no_cpu:
+        result["host_memory"] = host_memory_rate(host_cpu()["cores"])
     if not args.no_config1:
         log("config 1 ...")
         result["config1"] = config1(dev, args)
+    if not args.no_config3:
+        log("config 3 ...")
+        result["config3"] = config3(dev, args.warmup, cpu_points)
+    if not args.no_config4:
+        log("config 4 ...")
+        result["config4"] = config4(dev, args.warmup, cpu_points)
     if not args.no_decode:
         log("decode at the 1.7B shape ...")
         result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,

@@ -93,7 +93,10 @@ typedef struct tmh_device_info {
 } tmh_device_info;
 
 /* Device counters, as CUDA#uploads/#downloads/#gpu_ops/#device_bytes and
- * BufferPool#hits/#misses/#held/#limit (cuda.cr:214-230, buffer_pool.cr:14-35). */
+ * BufferPool#hits/#misses/#held/#limit (cuda.cr:214-230, buffer_pool.cr:14-35);
+ * `frees` counts device memory freed because the pool was full, `launches`
+ * the kernels queued (Context#launches, cuda.cr:463-475; a captured graph's
+ * replays are not counted again). */
 typedef struct tmh_counters {
     int64_t uploads;
     int64_t downloads;
@@ -104,6 +107,7 @@ typedef struct tmh_counters {
     int64_t pool_hits;
     int64_t pool_misses;
     int64_t frees;
+    int64_t launches;
 } tmh_counters;
 
 /* ------------------------------------------------------------ devices */

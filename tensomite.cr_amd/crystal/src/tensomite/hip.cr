@@ -93,6 +93,128 @@ module Tensomite
     getter gpu_ops = 0
     getter host_ops = 0
 
+    # Where a `HIP` device's time goes, collected while `HIP#profile` is set:
+    # the fields of `CUDA::Profile` (cuda.cr:249-303), so `ProfileReport` and
+    # the reference's profiling benches (bench/profile_decode_cuda.cr:31-49)
+    # read it as they read CUDA's.
+    #
+    # ```
+    # hip.profile = HIP::Profile.new
+    # model.forward(ids, cache)
+    # hip.profile.try(&.launch) # => seconds spent launching kernels
+    # ```
+    class Profile
+      # True when every op is timed on the GPU on its own, between two events
+      # on the library's stream, waiting for it to finish: GPU time per op, at
+      # the price of serialising the host and the GPU.
+      getter? per_kernel : Bool
+
+      # Count and GPU seconds per op; filled only when `#per_kernel?`.
+      getter kernels = Hash(String, {Int32, Float64}).new({0, 0.0})
+
+      # Count and wall seconds per op run on the host.
+      getter host_ops = Hash(String, {Int32, Float64}).new({0, 0.0})
+
+      # Seconds spent queuing kernels, allocating buffers, copying to and from
+      # the host, and waiting for the GPU at `sync`.
+      property launch = 0.0
+      property alloc = 0.0
+      property transfer = 0.0
+      property wait = 0.0
+
+      # Kernel launches (the library's count: a quantise pass and its product
+      # are two), uploads and downloads.
+      property launches = 0
+      property uploads = 0
+      property downloads = 0
+
+      # Buffers allocated, those the pool could not serve, and device memory
+      # freed because the pool was full.
+      property allocations = 0
+      property pool_misses = 0
+      property frees = 0
+
+      # True when `#kernels` keys each op by its shapes as well as its name
+      # (`ProfileReport.label`); takes effect only with `#per_kernel?`.
+      getter? shapes : Bool
+
+      def initialize(@per_kernel = false, @shapes = false)
+      end
+
+      protected def add_kernel(name : String, seconds : Float64) : Nil
+        count, total = kernels[name]
+        kernels[name] = {count + 1, total + seconds}
+      end
+
+      protected def add_host_op(name : String, seconds : Float64) : Nil
+        count, total = host_ops[name]
+        host_ops[name] = {count + 1, total + seconds}
+      end
+
+      # Prints, as Markdown tables, where *wall* seconds of *runs* runs went,
+      # per *unit*, from *normal* (taken as the workload ran) and the GPU
+      # time per op from *timed* (`per_kernel` and `shapes`), as
+      # `CUDA::Profile.report` does (cuda/report.cr:3-24).
+      def self.report(io : IO, device : String, unit : String, runs : Int32, wall : Float64,
+                      normal : Profile, timed : Profile, top : Int32 = 20) : Nil
+        parts = [
+          {"launching kernels", normal.launch},
+          {"allocating buffers", normal.alloc},
+          {"copying to and from the host", normal.transfer},
+          {"waiting for the GPU", normal.wait},
+        ]
+        counts = [
+          "launches: #{normal.launches // runs}; uploads: #{normal.uploads // runs}; downloads: #{normal.downloads // runs}",
+          "allocations: #{normal.allocations // runs}; not from the pool: #{normal.pool_misses // runs}; freed: #{normal.frees // runs}",
+        ]
+        io << ProfileReport.new(device, unit, runs, wall, parts, counts, normal.host_ops, timed.kernels, top)
+      end
+    end
+
+    # The profile being collected, or nil (the default) for none.
+    property profile : Profile? = nil
+
+    # The two events a per-kernel profile times each op between.
+    @events : {UInt64, UInt64}? = nil
+
+    # The library's pool of freed device memory (BufferPool, buffer_pool.cr:
+    # 14-35), read through its counters: the pool itself lives in the library,
+    # where finalizers on any thread give memory back without waiting.
+    struct Pool
+      def initialize(@gpu : HIP)
+      end
+
+      # Bytes the pool may hold: max(1 GiB, a quarter of the GPU's memory).
+      def limit : Int64
+        @gpu.counters.pool_limit
+      end
+
+      # Bytes of freed device memory it holds now.
+      def held : Int64
+        @gpu.counters.pool_held
+      end
+
+      # Allocations it served, and those it could not.
+      def hits : Int64
+        @gpu.counters.pool_hits
+      end
+
+      def misses : Int64
+        @gpu.counters.pool_misses
+      end
+    end
+
+    # The pool of freed device memory (CUDA#buffer_pool, cuda.cr:208-211).
+    def buffer_pool : Pool
+      Pool.new(self)
+    end
+
+    # Bytes of device memory allocated from the runtime and not yet freed: in
+    # live buffers and in `#buffer_pool` (CUDA#device_bytes, cuda.cr:217-222).
+    def device_bytes : Int64
+      counters.device_bytes
+    end
+
     # How a quantised matmul divides its work (BlockMatMulMode, quant.cr:5-57);
     # its value is the library's TMH_MODE_* number.
     property block_mode = BlockMatMulMode.from_env
@@ -104,6 +226,12 @@ module Tensomite
     def self.count : Int32
       check(LibTensomiteHIP.init(out count), "tmh_init")
       count
+    end
+
+    # True when the library starts and sees a GPU; never raises, as
+    # CUDA.available? (cuda.cr:986-988) for the specs' device list.
+    def self.available? : Bool
+      LibTensomiteHIP.init(out count) == LibTensomiteHIP::SUCCESS && count > 0
     end
 
     # Raises the reference's error for a failed call, "call: NAME (text)"
@@ -136,7 +264,15 @@ module Tensomite
     # a buffer of that size is free (CUDA#alloc, cuda.cr:339-353).
     def alloc(bytesize : Int32) : Buffer
       bind
+      profile = @profile
+      misses = profile ? counters.pool_misses : 0_i64
+      start = Time.instant
       HIP.check(LibTensomiteHIP.alloc(out pointer, bytesize.to_u64), "tmh_alloc")
+      if profile
+        profile.alloc += (Time.instant - start).total_seconds
+        profile.allocations += 1
+        profile.pool_misses += 1 if counters.pool_misses > misses
+      end
       HIPBuffer.new(self, pointer, bytesize)
     end
 
@@ -148,20 +284,30 @@ module Tensomite
     def upload(buffer : Buffer, data : Bytes) : Nil
       target = gpu_buffer(buffer)
       @uploads += 1
+      start = Time.instant
       unless data.empty?
         bind
         HIP.check(LibTensomiteHIP.upload_async(target.pointer, data.to_unsafe, data.size.to_u64), "tmh_upload_async")
       end
       target.device_written
+      @profile.try do |profile|
+        profile.uploads += 1
+        profile.transfer += (Time.instant - start).total_seconds
+      end
     end
 
     def download(buffer : Buffer, data : Bytes) : Nil
       source = gpu_buffer(buffer)
       @downloads += 1
+      start = Time.instant
       if copy = source.current_copy
         copy[0, data.size].copy_to(data)
       elsif !data.empty?
         fetch(source.pointer, data)
+      end
+      @profile.try do |profile|
+        profile.downloads += 1
+        profile.transfer += (Time.instant - start).total_seconds
       end
     end
 
@@ -175,11 +321,12 @@ module Tensomite
     # output is sent to the device (cuda.cr:395-415).
     def execute(node : Node, output : Buffer) : Nil
       target = gpu_buffer(output)
-      if launch_blocks(node, target)
+      if launch_profiled(node, target)
         target.device_written
         @gpu_ops += 1
         return
       end
+      start = Time.instant
       # A write keeps the rest of its target: its host copy must be current.
       target.bytes if node.op.try(&.in_place?)
       target.writing = true
@@ -190,6 +337,7 @@ module Tensomite
       end
       target.host_written
       @host_ops += 1
+      @profile.try(&.add_host_op("#{node.op} #{node.dtype}", (Time.instant - start).total_seconds))
     end
 
     # Waits for the GPU, moves retired memory into the pool, and raises
@@ -197,7 +345,14 @@ module Tensomite
     # (CUDA#sync and #check_errors, cuda.cr:419-428, 972-983).
     def sync : Nil
       bind
+      profile = @profile
+      frees = profile ? counters.frees : 0_i64
+      start = Time.instant
       code = LibTensomiteHIP.sync
+      if profile
+        profile.wait += (Time.instant - start).total_seconds
+        profile.frees += (counters.frees - frees).to_i32
+      end
       if code == LibTensomiteHIP::ERROR_EXECUTION
         report = StaticArray(Int32, 3).new(0)
         LibTensomiteHIP.error_report(report.to_unsafe)
@@ -229,10 +384,39 @@ module Tensomite
       HIP.check(LibTensomiteHIP.upload(pointer, data.to_unsafe, data.size.to_u64), "tmh_upload")
     end
 
-    # Never waits and never raises: finalizers call it on any thread.
+    # Never waits and never raises: finalizers call it on any thread. (The
+    # library counts memory it frees here because its retired list was busy
+    # or full; a profile picks that count up at the next `sync`.)
     protected def retire(pointer : LibTensomiteHIP::DevicePtr, bytesize : Int32) : Nil
       LibTensomiteHIP.set_device(@index)
       LibTensomiteHIP.retire(pointer, bytesize.to_u64)
+    end
+
+    # Launches *node* as `#launch_blocks` does, recording the time it takes
+    # and the kernels it queued with a profile, and, with a per-kernel
+    # profile, its GPU time between two events (CUDA#launch_profiled,
+    # cuda.cr:461-481).
+    private def launch_profiled(node : Node, output : HIPBuffer) : Bool
+      return launch_blocks(node, output) unless profile = @profile
+      bind
+      events = @events ||= {new_event, new_event}
+      HIP.check(LibTensomiteHIP.event_record(events[0]), "tmh_event_record") if profile.per_kernel?
+      launches = counters.launches
+      start = Time.instant
+      launched = launch_blocks(node, output)
+      profile.launch += (Time.instant - start).total_seconds
+      profile.launches += (counters.launches - launches).to_i32
+      if launched && profile.per_kernel?
+        HIP.check(LibTensomiteHIP.event_record(events[1]), "tmh_event_record")
+        HIP.check(LibTensomiteHIP.event_elapsed_ms(events[0], events[1], out ms), "tmh_event_elapsed_ms")
+        profile.add_kernel(ProfileReport.label(node, profile.shapes?), ms / 1000.0)
+      end
+      launched
+    end
+
+    private def new_event : UInt64
+      HIP.check(LibTensomiteHIP.event_create(out event), "tmh_event_create")
+      event
     end
 
     private def bind : Nil

@@ -55,6 +55,7 @@ module Tensomite
       pool_hits : Int64
       pool_misses : Int64
       frees : Int64
+      launches : Int64
     end
 
     struct Product

@@ -152,9 +152,9 @@ hipError_t launch_rmsnorm(const float* x, uint32_t ldx, const float* w, uint32_t
     if (rows == 0 || n == 0) return hipSuccess;
     if (n <= RMSNORM_LDS_ROW) {
         const size_t lds = (((size_t)n + 3u) & ~(size_t)3u) * sizeof(float);
-        hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), lds, stream, x, ldx, w, n, eps, dst, ld_dst);
+        TMH_LAUNCH(k_rmsnorm, dim3(rows), dim3(256), lds, stream, x, ldx, w, n, eps, dst, ld_dst);
     } else {
-        hipLaunchKernelGGL(k_rmsnorm_wide, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, dst, ld_dst);
+        TMH_LAUNCH(k_rmsnorm_wide, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, dst, ld_dst);
     }
     return hipGetLastError();
 }
@@ -167,14 +167,14 @@ hipError_t launch_rmsnorm_quantise(const float* x, uint32_t ldx, const float* w,
     if (!rmsnorm_quantise_fits(n)) return hipErrorInvalidValue;
     if (ldx % 4u == 0 && ((uintptr_t)x & 15u) == 0 && (!w || ((uintptr_t)w & 15u) == 0)) {
         if (n <= 64u * 8u)
-            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<8>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
+            TMH_LAUNCH(k_rmsnorm_quantise_wave<8>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
         else if (n <= 64u * 32u)
-            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<32>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
+            TMH_LAUNCH(k_rmsnorm_quantise_wave<32>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
         else
-            hipLaunchKernelGGL(k_rmsnorm_quantise_wave<128>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
+            TMH_LAUNCH(k_rmsnorm_quantise_wave<128>, dim3(rows), dim3(256), 0, stream, x, ldx, w, n, eps, act);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_rmsnorm_quantise, dim3(rows), dim3(256), (size_t)n * sizeof(float), stream, x, ldx, w,
+    TMH_LAUNCH(k_rmsnorm_quantise, dim3(rows), dim3(256), (size_t)n * sizeof(float), stream, x, ldx, w,
                        n, eps, act);
     return hipGetLastError();
 }
@@ -228,7 +228,7 @@ hipError_t launch_rope_write(const RopeWrite& a, uint32_t tokens, hipStream_t st
     const uint64_t total = (uint64_t)tokens * (a.heads + 2u * a.kv_heads) * a.width;
     if (total == 0) return hipSuccess;
     const uint32_t grid = (uint32_t)((total + 255u) / 256u);
-    hipLaunchKernelGGL(k_rope_write, dim3(grid), dim3(256), 0, stream, a, (uint32_t)total);
+    TMH_LAUNCH(k_rope_write, dim3(grid), dim3(256), 0, stream, a, (uint32_t)total);
     return hipGetLastError();
 }
 
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256) void k_attention(Attention a) {
 hipError_t launch_attention(const Attention& a, uint32_t tokens, hipStream_t stream) {
     if (tokens == 0 || a.heads == 0) return hipSuccess;
     const size_t lds = attention_lds(a.width, a.capacity);
-    hipLaunchKernelGGL(k_attention, dim3(tokens * a.heads), dim3(256), lds, stream, a);
+    TMH_LAUNCH(k_attention, dim3(tokens * a.heads), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
@@ -931,7 +931,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attention a, RopeWrite
 hipError_t launch_attention_decode(const Attention& a, const RopeWrite& r, uint32_t tokens, hipStream_t stream) {
     if (tokens == 0 || a.heads == 0) return hipSuccess;
     const size_t lds = attention_decode_lds(a.width, a.capacity);
-    hipLaunchKernelGGL(k_attention_decode, dim3(tokens * a.heads), dim3(256), lds, stream, a, r);
+    TMH_LAUNCH(k_attention_decode, dim3(tokens * a.heads), dim3(256), lds, stream, a, r);
     return hipGetLastError();
 }
 
@@ -975,7 +975,7 @@ hipError_t launch_swiglu_quantise(const float* gate, const float* value, uint32_
     const uint64_t blocks = (uint64_t)rows * (n >> 5);
     if (blocks == 0) return hipSuccess;
     if (n % 32u != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_swiglu_quantise, dim3((uint32_t)((blocks * 8u + 255u) / 256u)), dim3(256), 0, stream, gate,
+    TMH_LAUNCH(k_swiglu_quantise, dim3((uint32_t)((blocks * 8u + 255u) / 256u)), dim3(256), 0, stream, gate,
                        value, ld, n, (uint32_t)blocks, act);
     return hipGetLastError();
 }
@@ -984,7 +984,7 @@ hipError_t launch_swiglu(const float* gate, const float* value, uint32_t ld, uin
                          hipStream_t stream) {
     const uint64_t total = (uint64_t)rows * n;
     if (total == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, stream, gate, value, ld, n,
+    TMH_LAUNCH(k_swiglu, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, stream, gate, value, ld, n,
                        (uint32_t)total, dst);
     return hipGetLastError();
 }
@@ -997,7 +997,7 @@ __global__ __launch_bounds__(256) void k_add(const float* a, const float* b, flo
 
 hipError_t launch_add(const float* a, const float* b, float* dst, uint32_t count, hipStream_t stream) {
     if (count == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_add, dim3((count + 255u) / 256u), dim3(256), 0, stream, a, b, dst, count);
+    TMH_LAUNCH(k_add, dim3((count + 255u) / 256u), dim3(256), 0, stream, a, b, dst, count);
     return hipGetLastError();
 }
 
@@ -1057,7 +1057,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, uin
 
 hipError_t launch_argmax(const float* x, uint32_t ldx, uint32_t rows, uint32_t n, int32_t* ids, hipStream_t stream) {
     if (rows == 0 || n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(256), 0, stream, x, ldx, n, ids);
+    TMH_LAUNCH(k_argmax, dim3(rows), dim3(256), 0, stream, x, ldx, n, ids);
     return hipGetLastError();
 }
 
@@ -1129,9 +1129,9 @@ hipError_t launch_choose_advance(const float* logits, uint32_t rows, uint32_t vo
                                  int32_t* table, uint32_t capacity, hipStream_t stream) {
     if (rows == 0) return hipSuccess;
     const uint32_t chunks = argmax_chunks(vocab);
-    hipLaunchKernelGGL(k_argmax_chunks, dim3(rows * chunks), dim3(256), 0, stream, logits, vocab, vocab, chunks, values,
+    TMH_LAUNCH(k_argmax_chunks, dim3(rows * chunks), dim3(256), 0, stream, logits, vocab, vocab, chunks, values,
                        index);
-    hipLaunchKernelGGL(k_advance, dim3(rows), dim3(64), 0, stream, rows, logits, vocab, chunks, values,
+    TMH_LAUNCH(k_advance, dim3(rows), dim3(64), 0, stream, rows, logits, vocab, chunks, values,
                        index, ids, log, log_stride, steps, slots, table, capacity);
     return hipGetLastError();
 }

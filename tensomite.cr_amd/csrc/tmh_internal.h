@@ -14,6 +14,17 @@
 
 namespace tmh {
 
+// Counts one kernel launch on the calling thread's current device (the
+// counters' `launches`, as CUDA's Context#launches, cuda.cr:463-475). Every
+// launch site goes through TMH_LAUNCH; a captured graph's replays launch
+// its kernels without counting them again.
+void count_launch();
+#define TMH_LAUNCH(...)              \
+    do {                             \
+        ::tmh::count_launch();       \
+        hipLaunchKernelGGL(__VA_ARGS__); \
+    } while (0)
+
 // Bytes of one block of 32 values, by kind (dtype.cr:237-244).
 constexpr uint32_t block_bytes(uint32_t kind) { return kind == 0 ? 34u : kind == 1 ? 18u : 20u; }
 

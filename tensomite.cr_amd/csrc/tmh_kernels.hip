@@ -537,9 +537,12 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
         stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), 4u * k, lbase + L.x, wave, 0u);
         stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x + ldx), 4u * k, lbase + L.x + xrow, wave, 1u);
     } else if constexpr (PLAIN) {
-        // halves of whole kilobytes (a group's rotation depends on the
-        // group's index mod 16, and each half holds a multiple of 16 groups)
-        const uint32_t half = (k % 512u) == 0 ? 2u * k : 4u * k;
+        // halves only where each holds a multiple of 16 groups of 8 pieces
+        // (k a multiple of 1024): stage_rotated rotates a group by its index
+        // within the call, mod 16, and the readers below by its index within
+        // the row, so the second half's first group must be one whose
+        // row index is 0 mod 16
+        const uint32_t half = (k % 1024u) == 0 ? 2u * k : 4u * k;
         stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x), half, lbase + L.x, wave, 0u);
         if (half < 4u * k)
             stage_rotated<8, 1>(reinterpret_cast<const uint8_t*>(x) + half, half, lbase + L.x + half, wave, 1u);
@@ -2985,7 +2988,7 @@ __global__ __launch_bounds__(256) void k_f16_words(uint32_t first, uint32_t coun
 hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream) {
     if (count == 0) return hipSuccess;
     const uint32_t grid = std::min<uint32_t>((count + 255u) / 256u, 65536u);
-    hipLaunchKernelGGL(k_f16_words, dim3(grid), dim3(256), 0, stream, first, count, dst);
+    TMH_LAUNCH(k_f16_words, dim3(grid), dim3(256), 0, stream, first, count, dst);
     return hipGetLastError();
 }
 
@@ -2997,10 +3000,10 @@ hipError_t launch_quantize(const float* x, uint32_t ldx, uint32_t rows, uint32_t
     const uint32_t grid = (blocks * 8u + 255u) / 256u;
     const bool vec = ((uintptr_t)x % 16u == 0) && (ldx % 4u == 0);
     if (vec)
-        hipLaunchKernelGGL(k_quantize_rows_q8<true>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks, scales,
+        TMH_LAUNCH(k_quantize_rows_q8<true>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks, scales,
                            sums, totals, qs);
     else
-        hipLaunchKernelGGL(k_quantize_rows_q8<false>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks,
+        TMH_LAUNCH(k_quantize_rows_q8<false>, dim3(grid), dim3(256), 0, stream, x, ldx, nb, k, blocks,
                            scales, sums, totals, qs);
     return hipGetLastError();
 }
@@ -3057,7 +3060,7 @@ static hipError_t launch_lanes_nb(const uint8_t* w, Activations act, float* dst,
     const uint32_t stride = lanes_stride(nb);
     const size_t lds = (size_t)NB * tr * stride * sizeof(float);
     const uint32_t grid = (n + tr - 1u) / tr;
-    hipLaunchKernelGGL((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k, tr,
+    TMH_LAUNCH((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k, tr,
                        stride);
     return hipGetLastError();
 }
@@ -3102,7 +3105,7 @@ static hipError_t launch_thread(const uint8_t* w, Activations act, float* dst, c
                                 uint32_t n, uint32_t k, hipStream_t stream) {
     const uint32_t count = rows * n;
     const uint32_t grid = (count + 255u) / 256u;
-    hipLaunchKernelGGL(k_block_matmul_thread<KIND>, dim3(grid), dim3(256), 0, stream, w, act, dst, bias, n, k, count);
+    TMH_LAUNCH(k_block_matmul_thread<KIND>, dim3(grid), dim3(256), 0, stream, w, act, dst, bias, n, k, count);
     return hipGetLastError();
 }
 
@@ -3191,13 +3194,13 @@ hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* o
     const uint32_t ab = (uint32_t)align16(act_bytes);
     const size_t lds = ab + part_bytes;
     if (kind == 0)
-        hipLaunchKernelGGL((k_matvec_rows<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+        TMH_LAUNCH((k_matvec_rows<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
                            ab);
     else if (kind == 1)
-        hipLaunchKernelGGL((k_matvec_rows<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+        TMH_LAUNCH((k_matvec_rows<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
                            ab);
     else
-        hipLaunchKernelGGL((k_matvec_rows<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
+        TMH_LAUNCH((k_matvec_rows<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
                            ab);
     return hipGetLastError();
 }
@@ -3217,11 +3220,11 @@ hipError_t launch_row(uint32_t kind, const uint8_t* w, const float* x, float* ds
     const uint32_t ab = (uint32_t)row_act_bytes(p);
     const size_t lds = ab + row_part_bytes(p);
     if (kind == 0)
-        hipLaunchKernelGGL((k_matvec_row<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+        TMH_LAUNCH((k_matvec_row<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
     else if (kind == 1)
-        hipLaunchKernelGGL((k_matvec_row<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+        TMH_LAUNCH((k_matvec_row<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
     else
-        hipLaunchKernelGGL((k_matvec_row<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+        TMH_LAUNCH((k_matvec_row<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
     return hipGetLastError();
 }
 
@@ -3356,7 +3359,7 @@ template <int KIND, bool HB>
 static hipError_t launch_stream_kind(const StreamLaunch& l, hipStream_t stream) {
 #define TMH_STREAM(RING)                                                                                     \
     case RING:                                                                                               \
-        hipLaunchKernelGGL((k_matvec_stream<KIND, RING, HB>), dim3(l.grid), dim3(256), l.lds, stream, l.table, \
+        TMH_LAUNCH((k_matvec_stream<KIND, RING, HB>), dim3(l.grid), dim3(256), l.lds, stream, l.table, \
                            l.starts, l.total, l.act_bytes, l.part_floats, l.x_floats, l.act_offset);          \
         break;
     switch (l.ring) {
@@ -3384,7 +3387,7 @@ template <int KIND>
 static hipError_t launch_mfma(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t rows,
                               uint32_t n, uint32_t k, hipStream_t stream) {
     const dim3 grid((n + MM_TILE - 1u) / MM_TILE, (rows + MM_TILE - 1u) / MM_TILE);
-    hipLaunchKernelGGL(k_matmul_mfma<KIND>, grid, dim3(256), 0, stream, w, act, dst, bias, rows, n, k);
+    TMH_LAUNCH(k_matmul_mfma<KIND>, grid, dim3(256), 0, stream, w, act, dst, bias, rows, n, k);
     return hipGetLastError();
 }
 
@@ -3403,10 +3406,10 @@ static hipError_t launch_mx(bool fused, const uint8_t* w, Activations act, float
                             uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
     const uint32_t tiles_m = (rows + MX_TILE - 1u) / MX_TILE, tiles = tiles_m * ((n + MX_TILE - 1u) / MX_TILE);
     if (fused)
-        hipLaunchKernelGGL((k_matmul_mx<KIND, true>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
+        TMH_LAUNCH((k_matmul_mx<KIND, true>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
                            rows, n, k, tiles_m, tiles);
     else
-        hipLaunchKernelGGL((k_matmul_mx<KIND, false>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
+        TMH_LAUNCH((k_matmul_mx<KIND, false>), dim3(tiles), dim3(MX_THREADS), 0, stream, w, act, dst, bias,
                            rows, n, k, tiles_m, tiles);
     return hipGetLastError();
 }
@@ -3435,10 +3438,10 @@ static hipError_t launch_few(const uint8_t* w, Activations act, float* dst, cons
                              uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
     const uint32_t grid = (n + FEW_COLS - 1u) / FEW_COLS;
     if (grid > 256u)
-        hipLaunchKernelGGL((k_matmul_few<KIND, 3, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+        TMH_LAUNCH((k_matmul_few<KIND, 3, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
                            bias_ld, rows, n, k);
     else
-        hipLaunchKernelGGL((k_matmul_few<KIND, 6, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+        TMH_LAUNCH((k_matmul_few<KIND, 6, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
                            bias_ld, rows, n, k);
     return hipGetLastError();
 }
@@ -3536,7 +3539,7 @@ template <int KIND, int NB>
 static hipError_t launch_glu_nb(const uint8_t* w, Activations act, uint32_t H, uint32_t k, Activations glu,
                                 hipStream_t stream) {
     const uint32_t nb = k >> 5, h = glu_half(nb);
-    hipLaunchKernelGGL((k_matvec_glu<KIND, NB>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H, k,
+    TMH_LAUNCH((k_matvec_glu<KIND, NB>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H, k,
                        2u * h, lanes_stride(nb), glu);
     return hipGetLastError();
 }
@@ -3618,7 +3621,7 @@ static hipError_t launch_one(const uint8_t* w, const float* x, const float* nw, 
     const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units, PLAIN, XR);
     const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false, PLAIN, XR);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_one<KIND, NORM, false, PLAIN, XR>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end,
+    TMH_LAUNCH((k_matvec_one<KIND, NORM, false, PLAIN, XR>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end,
                        stream, w, x, nw, eps, act, dst, bias, n, k, tr, stride, Activations{}, ldx);
     return hipGetLastError();
 }
@@ -3681,7 +3684,7 @@ static hipError_t launch_glu_one(const uint8_t* w, const float* x, const float* 
     const uint32_t nb = k >> 5, h = glu_half(nb), stride = lanes_stride(nb);
     const OneLds L = one_lds(k, 2u * h, nb * Fmt<KIND>::BB, stride, true, true);
     if (L.end > ONE_LDS_LIMIT || H % h != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_one<KIND, true, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w, x, norm, eps,
+    TMH_LAUNCH((k_matvec_one<KIND, true, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w, x, norm, eps,
                        Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu, 0u);
     return hipGetLastError();
 }
@@ -3773,7 +3776,7 @@ static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, cons
     const uint32_t bufs = nb_bufs(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
     const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp, bufs);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS), L.end,
+    TMH_LAUNCH((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS), L.end,
                        stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, bufs, Activations{});
     return hipGetLastError();
 }
@@ -3861,7 +3864,7 @@ static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, 
     const uint32_t tpp = nb_tpp(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
     const uint32_t bufs = nb_bufs(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
     const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp, bufs);
-    hipLaunchKernelGGL((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream, w, x,
+    TMH_LAUNCH((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream, w, x,
                        ldx, nw,
                        eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, bufs, glu);
     return hipGetLastError();
@@ -3941,13 +3944,13 @@ hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows
     if (total == 0) return hipSuccess;
     const uint32_t grid = (total + 255u) / 256u;
     if (kind == 0)
-        hipLaunchKernelGGL(k_gather_blocks<0>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+        TMH_LAUNCH(k_gather_blocks<0>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
                            width, total);
     else if (kind == 1)
-        hipLaunchKernelGGL(k_gather_blocks<1>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+        TMH_LAUNCH(k_gather_blocks<1>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
                            width, total);
     else
-        hipLaunchKernelGGL(k_gather_blocks<2>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
+        TMH_LAUNCH(k_gather_blocks<2>, dim3(grid), dim3(256), 0, stream, table, ids, dst, errors, table_rows,
                            width, total);
     return hipGetLastError();
 }

@@ -236,7 +236,7 @@ struct Device {
     std::mutex staging_lock;
     Staging staging;
 
-    std::atomic<int64_t> uploads{0}, downloads{0}, gpu_ops{0}, device_bytes{0}, frees{0};
+    std::atomic<int64_t> uploads{0}, downloads{0}, gpu_ops{0}, device_bytes{0}, frees{0}, launches{0};
 };
 
 Device g_devices[MAX_DEVICES];
@@ -245,6 +245,15 @@ std::atomic<bool> g_kernels_off{false};
 thread_local int t_device = 0;
 
 int code(hipError_t e) { return (int)e; }
+
+}  // namespace
+
+void tmh::count_launch() {
+    const int i = t_device;
+    if (i >= 0 && i < MAX_DEVICES) g_devices[i].launches.fetch_add(1, std::memory_order_relaxed);
+}
+
+namespace {
 
 int count_devices() {
     int n = g_count.load();
@@ -628,6 +637,7 @@ int tmh_counters_get(tmh_counters* out) {
     out->pool_hits = d->pool.hits.load();
     out->pool_misses = d->pool.misses.load();
     out->frees = d->frees.load();
+    out->launches = d->launches.load();
     return TMH_SUCCESS;
 }
 

@@ -103,7 +103,7 @@ class QuantisedInput:
 class Counters(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int64) for name in
                 ("uploads", "downloads", "gpu_ops", "device_bytes", "pool_held", "pool_limit", "pool_hits",
-                 "pool_misses", "frees")]
+                 "pool_misses", "frees", "launches")]
 
 
 class LlamaConfig(ctypes.Structure):
@@ -427,6 +427,27 @@ class HIPDevice:
         m = MODES[mode or self.block_mode]
         check("tmh_block_matmul", self.lib.tmh_block_matmul(
             kk, w.pointer, w_row * rb, x.pointer, k if ldx is None else ldx, dst.pointer,
+            bias.pointer if bias is not None else 0, rows, n, k, m))
+        return dst
+
+    def block_matmul_quantised(self, kind, w: Buffer, act, rows: int, n: int, k: int, dst: Optional[Buffer] = None,
+                               bias: Optional[Buffer] = None, w_row: int = 0, mode: Optional[str] = None) -> Buffer:
+        """The product kernel alone on activations quantize_rows gave: act = (scales, sums, totals, qs)."""
+        kk = kind_of(kind)
+        rb = row_bytes(kk, k)
+        scales, sums, totals, qs = act
+        if (w_row + n) * rb > w.bytesize:
+            raise ShapeError(f"{w.bytesize} bytes do not hold rows {w_row}...{w_row + n} of {k} values")
+        nb = k // 32
+        if k % 32 or qs.bytesize < rows * k or min(scales.bytesize, sums.bytesize, totals.bytesize) < 4 * rows * nb:
+            raise ShapeError(f"quantised activations too small for [{rows}, {k}]")
+        if dst is None:
+            dst = self.alloc(max(4 * rows * n, 4))
+        if rows * n * 4 > dst.bytesize or (bias is not None and n * 4 > bias.bytesize):
+            raise ShapeError(f"output or bias too small for [{rows}, {n}]")
+        m = MODES[mode or self.block_mode]
+        check("tmh_block_matmul_quantised", self.lib.tmh_block_matmul_quantised(
+            kk, w.pointer, w_row * rb, scales.pointer, sums.pointer, totals.pointer, qs.pointer, dst.pointer,
             bias.pointer if bias is not None else 0, rows, n, k, m))
         return dst
 

@@ -289,6 +289,48 @@ def test_small_llama_generate_matches_cpu(dev, kind):
     assert gpu.length() == len(prompt) + 29
 
 
+@pytest.mark.parametrize("kind,rows", [("Q8_0", 1), ("Q4_0", 1), ("Q4_1", 3)])
+def test_decoder_nan_at_a_lane_start(dev, kind, rows):
+    # The decoder's fused quantisers (RMSNorm+quantise before qkv, gate_up
+    # and the head; SwiGLU+quantise after gate_up; the attention output's
+    # quantiser before o) take 8 lanes a block, 4 values a lane. The host's
+    # amax (quant.cr:428-442) skips a NaN anywhere but a block's first value,
+    # so a NaN first in a lane's 4 values (block index 4j, j >= 1) is skipped
+    # and quantised to 0 like any other. NaNs there come from: a norm weight
+    # (attention, FFN and final norms), a v row whose first block scale is a
+    # NaN half (the attention output's column), a gate row likewise (SwiGLU's
+    # output). Logits stay finite; prefill (12 rows) and decode (rows 1 or 3)
+    # against the CPU.
+    say("nan at lane start", kind, rows)
+    config = small_config(kind)
+    weights = random_llama(config, seed=27, norm_jitter=0.1)
+    w, hw = config["width"], config["head_width"]
+    rb = w // 32 * {"Q8_0": 34, "Q4_0": 18, "Q4_1": 20}[kind]
+    nan_half = np.frombuffer(np.array([0x7E00], np.uint16).tobytes(), np.uint8)
+    for layer in range(config["layers"]):
+        weights["attn_norm"][layer][[12, 36]] = np.nan  # block 0 lane 3, block 1 lane 1
+        weights["ffn_norm"][layer][72] = np.nan          # block 2 lane 2
+        v_row = (config["heads"] + config["kv_heads"]) * hw + 8  # column 8 of kv head 0
+        weights["qkv"][layer] = weights["qkv"][layer].copy()
+        weights["qkv"][layer][v_row * rb:v_row * rb + 2] = nan_half
+        weights["gate_up"][layer] = weights["gate_up"][layer].copy()
+        weights["gate_up"][layer][20 * rb:20 * rb + 2] = nan_half  # gate output 20: block 0 lane 5
+    weights["norm"][100] = np.nan  # block 3 lane 1
+    cpu = oracle.Llama(config, weights)
+    rng = np.random.default_rng(28)
+    prompts = [list(rng.integers(0, config["vocab"], 12 - r)) for r in range(rows)]
+    gpu = th.HIPLlama(dev, config, weights, rows=rows, max_tokens=16)
+    for r, p in enumerate(prompts):
+        got = gpu.forward(p, row=r, last_only=True)
+        cpu.reset()
+        want = cpu.forward(p, last_only=True)
+        assert np.isfinite(want).all()
+        assert np.array_equal(bits(got), bits(want)), r
+    tokens = gpu.generate(10, graph=True)
+    for r, p in enumerate(prompts):
+        assert list(tokens[r]) == oracle.Llama(config, weights).generate(p, 10), r
+
+
 def test_batch_rows_decode_matches_each_sequence(dev):
     # rows of different prompt lengths decoded together: each row's tokens
     # are those of its sequence alone (a row alone == in a batch).

@@ -172,12 +172,19 @@ CONFIG_SHAPES = {
     "gate_up_135m": ("Q4_0", 3072, 576, 1),
     "down_135m": ("Q4_0", 576, 1536, 1),
     "head_135m": ("Q4_0", 49152, 576, 1),
-    # config 3: Q4_1 batched decode (one row: the quantise pass and the
-    # lanes product, as every one-row product over 4 MB of weights takes)
-    "q41_up_b16": ("Q4_1", 8192, 2048, 16),
-    "q41_down_b5": ("Q4_1", 2048, 8192, 5),
+    # config 3: Q4_1 batched decode, every B the bench times on both shapes
+    # (B = 5 besides: a group of 4 and one row)
     "q41_up_b1": ("Q4_1", 8192, 2048, 1),
+    "q41_up_b2": ("Q4_1", 8192, 2048, 2),
+    "q41_up_b4": ("Q4_1", 8192, 2048, 4),
+    "q41_up_b8": ("Q4_1", 8192, 2048, 8),
+    "q41_up_b16": ("Q4_1", 8192, 2048, 16),
     "q41_down_b1": ("Q4_1", 2048, 8192, 1),
+    "q41_down_b2": ("Q4_1", 2048, 8192, 2),
+    "q41_down_b4": ("Q4_1", 2048, 8192, 4),
+    "q41_down_b5": ("Q4_1", 2048, 8192, 5),
+    "q41_down_b8": ("Q4_1", 2048, 8192, 8),
+    "q41_down_b16": ("Q4_1", 2048, 8192, 16),
     # config 5: 1.7B Q4_0 products at batch 1 and 8
     "qkv_1p7b": ("Q4_0", 6144, 2048, 1),
     "gate_up_1p7b_b8": ("Q4_0", 16384, 2048, 8),
@@ -203,9 +210,11 @@ def test_config_shapes_bit_exact(dev, name):
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("n,k", [(4096, 2048), (1024, 8192), (2500, 4096)])
 def test_one_row_over_4mb_with_bias(dev, fmt, n, k):
-    # One-row products of more than 4 MB of weights go through the quantise
-    # pass and the lanes product rather than the one-row kernel; with a bias
-    # added after each sum (host.cr:725-734), in every format.
+    # One-row products of more than 4 MB of weights, with a bias added after
+    # each sum (host.cr:725-734), in every format, by both routes: AUTO's
+    # one-row f32 kernel (weights staged into LDS, x quantised in every
+    # workgroup's prologue), and the quantise pass followed by the lanes
+    # product (the route of the reference's launch_blocks, cuda.cr:736-756).
     say("one row > 4 MB", fmt, n, k)
     wq = weights(fmt, n, k, n + k)
     assert wq.nbytes > 4 << 20
@@ -214,16 +223,23 @@ def test_one_row_over_4mb_with_bias(dev, fmt, n, k):
     want = oracle.add_bias(oracle.matmul(fmt, x, wq, 1, n, k), bias)
     got = run_product(dev, fmt, wq, x, 1, n, k, bias=bias)
     assert np.array_equal(bits(got), bits(want))
+    wbuf, xbuf, bbuf = dev.from_array(wq), dev.from_array(x), dev.from_array(bias)
+    act = dev.quantize_rows(xbuf, 1, k)
+    out = dev.block_matmul_quantised(fmt, wbuf, act, 1, n, k, bias=bbuf, mode="lanes")
+    lanes = dev.to_array(out, np.float32, n).reshape(1, n)
+    assert np.array_equal(bits(lanes), bits(want))
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("n,k", [(1000, 4096), (1200, 8192), (2049, 8192), (8192, 2048)])
+@pytest.mark.parametrize("n,k", [(16384, 512), (1000, 4096), (1200, 8192), (2049, 8192), (8192, 2048)])
 @pytest.mark.parametrize("rows", [1, 2])
 def test_one_long_row_quantised_in_kernel(dev, fmt, n, k, rows):
     # One row over 4 MB of weights (and two rows, rows ldx apart): the
     # one-row kernel quantises x in its prologue (no norm). Whole blocks of
     # zeros (scale 0), a spike, exact halves (rounding ties), a ragged last
-    # tile; the second row Gaussian.
+    # tile; the second row Gaussian. k = 512 stages x in one piece (its
+    # halves would start a rotation group out of step); k = 2048..8192 in
+    # two halves.
     wq = weights(fmt, n, k, n * 7 + k)
     if wq.nbytes <= 4 << 20:
         wq = np.concatenate([wq] * 2)
@@ -231,8 +247,10 @@ def test_one_long_row_quantised_in_kernel(dev, fmt, n, k, rows):
     say("long rows", fmt, rows, n, k)
     x = acts(rows, k, k + 9)
     x[:256] = 0.0
+    t = min(1024, x.size // 2)
+    m = min(512, x.size - t)
+    x[t:t + m] = (np.arange(m) % 255 - 127).astype(np.float32) * np.float32(0.5)
     x[300] = 1e4
-    x[1024:1536] = (np.arange(512) % 255 - 127).astype(np.float32) * np.float32(0.5)
     ldx = k + 32
     strided = np.zeros(rows * ldx, np.float32)
     for r in range(rows):
@@ -302,6 +320,22 @@ def test_few_rows_nan_and_inf_blocks(dev, fmt):
         out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k)
         got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
         assert same_or_both_nan(got, want[:rows]), rows
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 16, 40])
+def test_zero_rows_fold_from_plus_zero(dev, rows):
+    # Q4_0 with negative block scales and all-zero activation rows: every
+    # contribution (0·d)·0 is -0.0, and the host's fold from 0.0f gives +0.0
+    # (quant.cr:446-491); every route (one row, few rows, lanes, the
+    # matrix-core kernel from 32 rows) must keep the +0.0 start.
+    n, k = 3000, 512
+    w = np.tile(np.array([1.0] + [0.25] * 31, np.float32), n * k // 32)
+    wq = oracle.quantize("Q4_0", w)
+    x = np.zeros(rows * k, np.float32)
+    say("zero rows", rows)
+    for mode in ("auto", "lanes", "thread", "matrix"):
+        got = run_product(dev, "Q4_0", wq, x, rows, n, k, mode=mode)
+        assert np.all(bits(got) == 0), mode
 
 
 @pytest.mark.parametrize("fmt", FORMATS)

@@ -9,7 +9,12 @@ own model-level fixtures and invariants:
 * prefill gives the bits of one-by-one decode (block_matmul_spec.cr:253-260);
 * forward_last's row equals the full forward's last row;
 * RMSNorm, SwiGLU and the RoPE tables against float64 restatements of their
-  definitions (bounds, not retyped bits).
+  definitions (bounds, not retyped bits);
+* the order of every sequential f32 fold of the decode graph -- RMSNorm's
+  sum of squares (host.cr:374-386), attention's dot products, softmax
+  total and value fold (host.cr:408-440) -- against plain f32 loops in index
+  order, where a reversed fold and a pairwise tree must each give other bits
+  on the same inputs.
 """
 import json
 import os
@@ -170,3 +175,106 @@ def test_rope_against_definition():
     want = xd * cos[pos][:, None, :] + rot * sin[pos][:, None, :]
     assert np.allclose(got, want, atol=1e-6)
     assert np.array_equal(got[0], x[0].reshape(3, 8))  # position 0: cos 1, sin 0
+
+
+def fold_sequential(values):
+    total = np.float32(0.0)
+    for v in values:
+        total = np.float32(total + np.float32(v))
+    return total
+
+
+def fold_reversed(values):
+    return fold_sequential(list(values)[::-1])
+
+
+def fold_pairwise(values):
+    v = [np.float32(a) for a in values]
+    while len(v) > 1:
+        nxt = [np.float32(v[i] + v[i + 1]) for i in range(0, len(v) - 1, 2)]
+        if len(v) % 2:
+            nxt.append(v[-1])
+        v = nxt
+    return v[0]
+
+
+def rmsnorm_with_fold(x, w, eps, fold):
+    """host.cr:374-386 with the squares' sum taken by `fold`: squares rounded
+    one by one, root = sqrt(Σ/n + eps) rounded, then x / root · w."""
+    f32 = np.float32
+    n = x.size
+    total = fold([f32(v * v) for v in x])
+    root = np.sqrt(f32(f32(total / f32(n)) + f32(eps)))
+    out = x / root
+    return out * w if w is not None else out
+
+
+def test_rmsnorm_sums_squares_in_index_order():
+    # Rows whose Σx² crosses many binades (values scaled by 2^u) or adds many
+    # near-equal terms: the index-order fold gives the oracle's bits on every
+    # row; reversed and pairwise folds differ on some.
+    rng = np.random.default_rng(2)
+    rows = []
+    for n in (5, 64, 100, 1000):
+        for _ in range(6):
+            rows.append((rng.normal(0, 1, n) * 2.0 ** rng.uniform(-8, 8, n)).astype(np.float32))
+        rows.append(rng.normal(0, 1, n).astype(np.float32))
+        rows.append(np.sort(np.abs(rng.normal(0, 1, n))).astype(np.float32))
+    rev = pair = 0
+    for x in rows:
+        w = rng.normal(1, 0.1, x.size).astype(np.float32)
+        got = oracle.rmsnorm(x[None, :], w, 1e-5)[0]
+        want = rmsnorm_with_fold(x, w, 1e-5, fold_sequential)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), x.size
+        rev += int(not np.array_equal(rmsnorm_with_fold(x, w, 1e-5, fold_reversed).view(np.uint32), got.view(np.uint32)))
+        pair += int(not np.array_equal(rmsnorm_with_fold(x, w, 1e-5, fold_pairwise).view(np.uint32), got.view(np.uint32)))
+    assert rev > 0 and pair > 0, (rev, pair)
+
+
+def attention_with_folds(q, k, v, last, n, scale, total_fold, value_fold):
+    """host.cr:408-440 for one query head: scores q·k in column order, · scale,
+    + the causal mask (0 up to `last`, -inf after), the first highest score,
+    Maths.exp(score - top), the total by `total_fold`, then per column the
+    fold by `value_fold` of (e_p / total) · v_p[col]."""
+    f32 = np.float32
+    scores = np.empty(n, np.float32)
+    top = f32(0.0)
+    for p in range(n):
+        x = f32(fold_sequential([f32(q[c] * k[p, c]) for c in range(q.size)]) * f32(scale))
+        x = f32(x + (f32(-np.inf) if p > last else f32(0.0)))
+        scores[p] = x
+        if p == 0 or x > top:
+            top = x
+    e = oracle.exp_many((scores - top).astype(np.float32))
+    total = total_fold(list(e))
+    out = np.empty(v.shape[1], np.float32)
+    for c in range(v.shape[1]):
+        out[c] = value_fold([f32(f32(e[p] / total) * v[p, c]) for p in range(n)])
+    return out
+
+
+def test_attention_folds_in_position_order():
+    # The softmax total and each output column's value fold are sums in
+    # position order from 0f32: the index-order loops give the oracle's bits
+    # for every head; a pairwise total, or a reversed value fold, differs on
+    # some heads. Grouped heads, a causal mask past `last`, several lengths.
+    rng = np.random.default_rng(7)
+    heads, kv_heads, width, capacity = 4, 2, 8, 72
+    table = [[0, 3, 4], [0, 40, 41], [1, 70, 72], [1, 20, 33], [0, 63, 64]]
+    q = rng.normal(0, 2, (len(table), heads, width)).astype(np.float32)
+    keys = rng.normal(0, 1, (2, kv_heads, capacity, width)).astype(np.float32)
+    values = (rng.normal(0, 1, (2, kv_heads, capacity, width)) *
+              2.0 ** rng.uniform(-6, 6, (2, kv_heads, capacity, 1))).astype(np.float32)
+    got = oracle.attention(q, keys, values, table, 0.35)
+    total_differs = value_differs = 0
+    for t, (r, last, n) in enumerate(table):
+        for h in range(heads):
+            kv = h // (heads // kv_heads)
+            args = (q[t, h], keys[r, kv, :n], values[r, kv, :n], last, n, 0.35)
+            want = attention_with_folds(*args, fold_sequential, fold_sequential)
+            assert np.array_equal(got[t, h].view(np.uint32), want.view(np.uint32)), (t, h)
+            a = attention_with_folds(*args, fold_pairwise, fold_sequential)
+            b = attention_with_folds(*args, fold_sequential, fold_reversed)
+            total_differs += int(not np.array_equal(a.view(np.uint32), want.view(np.uint32)))
+            value_differs += int(not np.array_equal(b.view(np.uint32), want.view(np.uint32)))
+    assert total_differs > 0 and value_differs > 0, (total_differs, value_differs)

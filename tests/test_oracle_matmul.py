@@ -117,12 +117,42 @@ def test_element_pairing_probe(fmt):
 
 
 def contributions_with_order(fmt, x, wq, k, order):
-    """One output's block contributions folded left to right, each written in
-    a stated association, from the oracle's own activation quantisation."""
+    """One output's block contributions folded left to right from +0.0, each
+    written in a stated association, from the oracle's own activation
+    quantisation."""
+    return fold_sequential(block_contributions(fmt, x, wq, k, order))
+
+
+def fold_sequential(values):
+    """sum = 0f32, then sum += value in index order (quant.cr:446-491)."""
+    total = np.float32(0.0)
+    for v in values:
+        total = np.float32(total + v)
+    return total
+
+
+def fold_reversed(values):
+    return fold_sequential(values[::-1])
+
+
+def fold_pairwise(values):
+    """A balanced tree of f32 adds (what a parallel reduction computes)."""
+    v = list(values)
+    while len(v) > 1:
+        nxt = [np.float32(v[i] + v[i + 1]) for i in range(0, len(v) - 1, 2)]
+        if len(v) % 2:
+            nxt.append(v[-1])
+        v = nxt
+    return np.float32(v[0])
+
+
+def block_contributions(fmt, x, wq, k, order):
+    """One output's per-block contributions (Appendix A's expressions), each
+    written in a stated association, as a list in block order."""
     scales, sums, qs = oracle.quantize_activations(x, with_sums=(fmt == "Q4_1"))
     bb = oracle.BLOCK_BYTES[oracle.kind_of(fmt)]
     f32 = np.float32
-    total = f32(0.0)
+    out = []
     for b in range(k // 32):
         blk = wq[b * bb:(b + 1) * bb]
         d = f32(np.frombuffer(blk[:2].tobytes(), np.float16)[0])
@@ -141,8 +171,8 @@ def contributions_with_order(fmt, x, wq, k, order):
             c = order(tf, d, sx) + f32(m * sums[b])
         else:
             c = order(tf, d, sx)
-        total = f32(total + c)
-    return total
+        out.append(f32(c))
+    return out
 
 
 ORDERS = {
@@ -175,6 +205,46 @@ def test_expression_order(fmt):
         alt = contributions_with_order(fmt, x, wq, k, ORDERS[other])
         differs += int(alt.view(np.uint32) != got.view(np.uint32))
     assert differs > 0
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("k", [128, 256, 2048])
+def test_blocks_fold_in_block_order(fmt, k):
+    # quant.cr:446-491 folds the block contributions left to right from
+    # 0.0f. At k >= 128 (4 blocks or more) the order shows in the bits: the
+    # sequential fold must reproduce the oracle every time, while a reversed
+    # fold and a pairwise tree must each differ somewhere. Blocks of x are
+    # scaled by 2^u, u in [-6, 6], so partial sums cross binades.
+    rng = np.random.default_rng(k + len(fmt))
+    order = ORDERS[REFERENCE_ORDER[fmt]]
+    reversed_differs = pairwise_differs = 0
+    trials = 120 if k < 2048 else 30
+    for trial in range(trials):
+        w = rng.uniform(-2, 2, k).astype(np.float32)
+        scale = np.repeat(2.0 ** rng.uniform(-6, 6, k // 32), 32)
+        x = (rng.uniform(-1, 1, k) * scale).astype(np.float32)
+        wq = oracle.quantize(fmt, w)
+        got = oracle.matmul_reference(fmt, x, wq, 1, 1, k)[0, 0]
+        c = block_contributions(fmt, x, wq, k, order)
+        assert got.view(np.uint32) == fold_sequential(c).view(np.uint32), trial
+        reversed_differs += int(fold_reversed(c).view(np.uint32) != got.view(np.uint32))
+        pairwise_differs += int(fold_pairwise(c).view(np.uint32) != got.view(np.uint32))
+    assert reversed_differs > 0 and pairwise_differs > 0, (reversed_differs, pairwise_differs)
+
+
+def test_fold_starts_from_plus_zero():
+    # Q4_0 with a negative scale d and an all-zero activation row: every
+    # contribution (0·d)·0 is -0.0, and a fold from +0.0 gives +0.0 (a fold
+    # that starts from the first contribution would give -0.0).
+    k, n = 256, 4
+    w = np.tile(np.array([1.0] + [0.25] * 31, np.float32), n * k // 32)  # m = +1: d = -1/8
+    wq = oracle.quantize("Q4_0", w)
+    x = np.zeros(k, np.float32)
+    c = block_contributions("Q4_0", x, wq[:k // 32 * 18], k, ORDERS[REFERENCE_ORDER["Q4_0"]])
+    assert all(v.view(np.uint32) == 0x80000000 for v in c)  # -0.0 each
+    for fn in (oracle.matmul_reference, oracle.matmul):
+        got = fn("Q4_0", x, wq, 1, n, k)
+        assert np.all(got.view(np.uint32) == 0), fn
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
