@@ -765,6 +765,74 @@ def config4(dev, warmup, cpu_seconds=None):
     return out
 
 
+# ---------------------------------------------------------------- ceilings
+
+def ceilings(dev, warmup):
+    """The box's own ceilings beside the vendor peaks: the HBM read rate of a
+    grid-stride read kernel (tmh_debug_read: 16 B a lane a load, four in
+    flight, non-temporal) at 77 MB (config 2's bytes) and 1 GiB, by
+    workgroup count; the device-to-device copy rate (tmh_copy: bytes read +
+    written); each the median over >= 100 launches rotating through >= 512
+    MB so the 256 MB Infinity Cache cannot serve them; and what rocminfo
+    and amd-smi report of the device."""
+    import subprocess
+    import tensomite_hip as th
+
+    out = {"device": {"name": dev.name, "arch": dev.arch, "compute_units": dev.compute_units}, "read": {},
+           "copy": {}}
+    info = th.DeviceInfo()
+    th.check("tmh_device_info_get", dev.lib.tmh_device_info_get(0, ctypes_byref(info)))
+    out["device"].update({"memory_bytes": info.memory, "clock_khz": info.clock_khz,
+                          "memory_clock_khz": info.memory_clock_khz, "memory_bus_width": info.memory_bus_width,
+                          "l2_bytes": info.l2_bytes})
+    tools = {}
+    for cmd in (["rocminfo"], ["amd-smi", "static", "--gpu", "0"], ["amd-smi", "metric", "--gpu", "0", "--clock"]):
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=60)
+            keep = [ln.strip() for ln in r.stdout.splitlines()
+                    if any(key in ln for key in ("Marketing Name", "gfx950", "Compute Unit", "Max Clock", "MARKET_NAME",
+                                                 "MAX_SCLK", "MAX_MCLK", "VRAM", "SIZE", "TYPE", "BUS", "CLK",
+                                                 "SCLK", "MCLK", "Memory"))]
+            tools[" ".join(cmd)] = keep[:40]
+        except (OSError, subprocess.SubprocessError) as e:
+            tools[" ".join(cmd)] = [f"unavailable: {e}"]
+    out["tools"] = tools
+    sink = dev.alloc(4 * 8192)
+    for label, size in (("77MB", 76_857_600 // 16 * 16), ("1GiB", 1 << 30)):
+        copies = max(2, math.ceil(2 * MALL_BYTES / size))
+        bufs = [dev.alloc(size) for _ in range(copies)]  # contents do not matter to a read rate
+        dev.sync()
+        groups = 100 if size < (1 << 28) else 20
+        per_group = 10 if size < (1 << 28) else 2
+        for wgs in (256, 512, 1024, 1536, 2048, 4096):
+            call = lambda i: th.check("tmh_debug_read", dev.lib.tmh_debug_read(bufs[i % copies].pointer, size, wgs,
+                                                                              sink.pointer))
+            warm_up(dev, call, warmup)
+            per, _ = time_launches(dev, call, groups * per_group, per_group)
+            st = launch_stats(per, size, per_group)
+            out["read"][f"{label} wgs={wgs}"] = {"us_median": st["median_us"], "GB_per_s": st["GB_per_s_median"],
+                                                 "frac_of_8TBs": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 4)}
+        half = size // 2
+        call = lambda i: dev.copy(bufs[i % copies], bufs[(i + 1) % copies], half, dst_offset=half)
+        warm_up(dev, call, warmup)
+        per, _ = time_launches(dev, call, groups * per_group, per_group)
+        st = launch_stats(per, 2 * half, per_group)
+        out["copy"][label] = {"bytes_copied": half, "us_median": st["median_us"], "GB_per_s_read_plus_write":
+                              st["GB_per_s_median"], "frac_of_8TBs": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 4)}
+        for b in bufs:
+            b.release()
+        dev.sync()
+    sink.release()
+    best = max(out["read"].items(), key=lambda kv: kv[1]["GB_per_s"])
+    out["best_read"] = {"where": best[0], **best[1]}
+    return out
+
+
+def ctypes_byref(obj):
+    import ctypes
+    return ctypes.byref(obj)
+
+
 class _View:
     """A buffer seen from a byte offset (a product's weights inside a packed buffer)."""
 
@@ -793,6 +861,8 @@ def main():
     ap.add_argument("--no-config4", action="store_true", help="skip the config-4 (Q8_0 prefill GEMM) measurement")
     ap.add_argument("--cpu-point-seconds", type=float, default=0.4,
                     help="CPU baseline sample per config-3/4 point and build")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="the box's read and copy rates and device facts instead; its own JSON line")
     ap.add_argument("--decode-only", action="store_true",
                     help="config 5 only (decode at batch 1 and 8); its own JSON line")
     ap.add_argument("--decode-eager", action="store_true",
@@ -817,6 +887,9 @@ def main():
     dev = th.HIPDevice(0)
     log(f"device {dev.name or '?'} {dev.arch} CUs={dev.compute_units}")
     cpu_points = None if args.no_cpu else args.cpu_point_seconds
+    if args.ceilings:
+        print(json.dumps(ceilings(dev, args.warmup)), flush=True)
+        return
     if args.gemm:
         print(json.dumps(config4(dev, args.warmup, cpu_points)), flush=True)
         return

@@ -211,6 +211,14 @@ int tmh_debug_disable_kernels(int32_t off);
  * conversion (the activation scales and sums use it). Queued on the stream. */
 int tmh_debug_f16_words(uint32_t first, uint32_t count, uint64_t dst);
 
+/* Measurement hook (no counterpart in the reference): `workgroups`
+ * workgroups of 256 threads read `bytes` (a multiple of 16, src 16-byte
+ * aligned) grid-stride, 16 bytes a lane a load and four loads in flight,
+ * non-temporal, and write the XOR of what each read to out[workgroup]
+ * (uint32, device). Timed with tmh_event_*, it gives the HBM read rate the
+ * product kernels are measured against. Queued on the stream. */
+int tmh_debug_read(uint64_t src, uint64_t bytes, uint32_t workgroups, uint64_t out);
+
 /* ------------------------------------------------------------ events */
 
 /* Timing on the library's stream: cuEventCreate/Record/ElapsedTime

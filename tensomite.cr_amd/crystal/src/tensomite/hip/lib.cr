@@ -130,6 +130,7 @@ module Tensomite
     fun debug_fail_allocations = tmh_debug_fail_allocations(count : Int32) : Int32
     fun debug_disable_kernels = tmh_debug_disable_kernels(off : Int32) : Int32
     fun debug_f16_words = tmh_debug_f16_words(first : UInt32, count : UInt32, dst : DevicePtr) : Int32
+    fun debug_read = tmh_debug_read(src : DevicePtr, bytes : UInt64, workgroups : UInt32, out : DevicePtr) : Int32
 
     # events
     fun event_create = tmh_event_create(event : UInt64*) : Int32

@@ -226,6 +226,10 @@ hipError_t launch_product_f32_one(uint32_t kind, const uint8_t* w, const float* 
 // dst[i] = the F16 bits of the float with word first + i, i < count.
 hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream);
 
+// The read-rate hook: `workgroups` workgroups read bytes / 16 pieces at src
+// grid-stride, out[b] the XOR of workgroup b's.
+hipError_t launch_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* out, hipStream_t stream);
+
 // Launches the block gather; ids out of range go to `errors` (count, id, rows).
 hipError_t launch_gather(uint32_t kind, const uint8_t* table, int32_t table_rows, uint32_t width, const int32_t* ids,
                          uint32_t count, float* dst, int32_t* errors, hipStream_t stream);

@@ -2983,7 +2983,40 @@ __global__ __launch_bounds__(256) void k_f16_words(uint32_t first, uint32_t coun
         dst[i] = (uint16_t)round_to_half_bits(__uint_as_float(first + (uint32_t)i));
 }
 
+// The read-rate hook (tmh_debug_read): workgroup b of G reads 16-byte
+// pieces b·256 + t, then G·256 further on, four pieces in flight a lane, and
+// writes the XOR of what it read to out[b] (so no load can be dropped).
+// Pieces = bytes / 16.
+typedef uint32_t piece16 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_read_pieces(const piece16* __restrict__ src, uint64_t pieces,
+                                                     uint32_t* __restrict__ out) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    piece16 acc = {0u, 0u, 0u, 0u};
+    for (; i + 3u * stride < pieces; i += 4u * stride) {
+        const piece16 a = __builtin_nontemporal_load(src + i);
+        const piece16 b = __builtin_nontemporal_load(src + i + stride);
+        const piece16 c = __builtin_nontemporal_load(src + i + 2u * stride);
+        const piece16 d = __builtin_nontemporal_load(src + i + 3u * stride);
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < pieces; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+    uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    for (int o = 32; o > 0; o >>= 1) v ^= __shfl_xor(v, o);
+    __shared__ uint32_t waves[4];
+    if ((threadIdx.x & 63u) == 0) waves[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = waves[0] ^ waves[1] ^ waves[2] ^ waves[3];
+}
+
 // ---------------------------------------------------------------- launchers
+
+hipError_t launch_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* out, hipStream_t stream) {
+    if (bytes < 16u || workgroups == 0) return hipSuccess;
+    TMH_LAUNCH(k_read_pieces, dim3(workgroups), dim3(256), 0, stream, (const piece16*)src, bytes / 16u, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_f16_words(uint32_t first, uint32_t count, uint16_t* dst, hipStream_t stream) {
     if (count == 0) return hipSuccess;

@@ -685,6 +685,18 @@ int tmh_debug_f16_words(uint32_t first, uint32_t count, uint64_t dst) {
     return code(e);
 }
 
+int tmh_debug_read(uint64_t src, uint64_t bytes, uint32_t workgroups, uint64_t out) {
+    if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    int err;
+    Device* d = current(&err);
+    if (!d) return err;
+    if (bytes == 0 || workgroups == 0) return TMH_SUCCESS;
+    if (!src || !out || src % 16u != 0 || bytes % 16u != 0 || out % 4u != 0) return TMH_ERROR_INVALID_VALUE;
+    hipError_t e = tmh::launch_read((const void*)src, bytes, workgroups, (uint32_t*)out, d->stream);
+    if (e == hipSuccess) d->gpu_ops.fetch_add(1);
+    return code(e);
+}
+
 int tmh_event_create(uint64_t* event) {
     if (!event) return TMH_ERROR_INVALID_VALUE;
     int err;

@@ -157,6 +157,7 @@ SIGNATURES = {
     "tmh_gather_blocks": (INT, [U32, U64, U64, I32, U32, U64, U32, U64]),
     "tmh_quantize_weights": (INT, [U32, VP, U64, VP, I32]),
     "tmh_debug_f16_words": (INT, [U32, U32, U64]),
+    "tmh_debug_read": (INT, [U64, U64, U32, U64]),
     "tmh_plan_create": (INT, [U32, ctypes.POINTER(Product), U32, ctypes.POINTER(U64)]),
     "tmh_plan_run": (INT, [U64]),
     "tmh_plan_destroy": (INT, [U64]),
