@@ -305,6 +305,17 @@ def config2(dev, args):
     achieved = stats["GB_per_s_median"]
     gpu_out = [dev.to_array(y, np.float32, n) for y, (_, n, _) in zip(ybufs, prods)]
 
+    # The same launch in UNORDERED (each row's contributions as four running
+    # sums instead of the host's block order; measurement only): the price
+    # of the host's order.
+    for plan in plans:
+        plan.set_mode("unordered")
+    warm_up(dev, run, args.warmup)
+    per_u, _ = time_launches(dev, run, ROOFLINE_GROUPS * GROUP, GROUP)
+    u_stats = launch_stats(per_u, algorithmic, GROUP)
+    for plan in plans:
+        plan.set_mode("auto")
+
     # Per-product launches (the reference's one launch per product), for comparison.
     def per_product(s):
         for i, (name, n, k) in enumerate(prods):
@@ -361,6 +372,12 @@ def config2(dev, args):
             "groups": stats["groups"],
             "launches_per_group": stats["launches_per_group"],
             "warmup_launches": warm,
+        },
+        "unordered": {
+            "launch_us_median": u_stats["median_us"], "GB_per_s": u_stats["GB_per_s_median"],
+            "frac": round(u_stats["GB_per_s_median"] / HBM_PEAK_GBS, 4),
+            "note": "the same plan in BlockMatMulMode UNORDERED (tmh_plan_set_mode): each row's contributions "
+                    "summed as four running sums instead of in block order; measurement only",
         },
         "per_product_launches": {
             "ms_per_token": round(per_product_ms, 4),
@@ -526,6 +543,22 @@ def decode_1p7b(dev, steps, cpu_seconds, with_cpu, graph=True):
                                "repeat_tokens_equal": bool(np.array_equal(again, tokens)),
                                "prefill_128_ms": round(1e3 * float(np.median(prefill)), 2),
                                "weight_GB_per_s": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
+        # The same steps with the products in UNORDERED (tmh_llama_set_mode;
+        # each product's contributions as four running sums, measurement
+        # only): what the host's order costs a step. Its tokens may differ.
+        model.set_mode("unordered")
+        model.reset()
+        for r in range(rows):
+            model.forward(prompts[r], row=r, last_only=True)
+        model.generate(2, graph=graph)  # the UNORDERED step graph captured
+        model.reset()
+        for r in range(rows):
+            model.forward(prompts[r], row=r, last_only=True)
+        dev.record(e0)
+        model.generate(steps, graph=graph)
+        dev.record(e1)
+        dev.sync()
+        out[f"batch{rows}"]["unordered_ms_per_step"] = round(dev.elapsed_ms(e0, e1) / (steps - 1), 4)
         model.destroy()
         log(f"decode batch {rows}: {ms * 1e3:.0f} us/step")
     if with_cpu:
@@ -655,6 +688,10 @@ def config3(dev, warmup, cpu_seconds=None):
                                   "unit": "GB/s", "frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 4)}}
             want = oracle.matmul("Q4_1", xh, wq, b, n, k, oracle.best_variant())
             point["bit_exact_vs_oracle"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            ucall = lambda i: dev.block_matmul("Q4_1", ws[i % copies], x, b, n, k, dst=dst, mode="unordered")
+            warm_up(dev, ucall, warmup)
+            per_u, _ = time_launches(dev, ucall, ROOFLINE_GROUPS * 10, 10)
+            point["unordered_us_per_call_median"] = round(statistics.median(per_u) * 1e3, 3)
             if cpu_seconds:
                 builds = {}
                 for variant in variants:

@@ -66,8 +66,10 @@ extern "C" {
  * measurement only (quant.cr:14-17 prices the ordered sum the same way):
  * from 32 activation rows, where k is a multiple of 256, it runs the
  * matrix-core kernel with each block's contribution added by one fused
- * multiply-add, and its results may differ in the last bits; elsewhere it
- * runs as LANES. LOADS, STREAM and STREAM_ACTIVATIONS are Metal measurement
+ * multiply-add; below that it runs AUTO's kernels with each row's
+ * contributions summed as four running sums instead of in block order (as
+ * block_matmul_unordered_f32, cuda/kernels.cu:1334-1375, prices the lanes
+ * product); its results may differ in the last bits. LOADS, STREAM and STREAM_ACTIVATIONS are Metal measurement
  * modes the reference runs as LANES elsewhere; so does this device. MATRIX
  * has no counterpart in the reference: the int8 matrix-core path for many
  * activation rows. */
@@ -338,6 +340,13 @@ int tmh_plan_destroy(uint64_t plan);
  * reference: it names the kernel for profilers and benchmarks. */
 int tmh_plan_describe(uint64_t plan, char* text, uint32_t size);
 
+/* The plan's BlockMatMulMode (quant.cr:5-28): TMH_MODE_AUTO (the host's
+ * block-order fold, the default) or TMH_MODE_UNORDERED (the same kernel and
+ * loads, each row's contributions summed as four running sums: results may
+ * differ in the last bits; a measurement mode, as block_matmul_unordered_f32
+ * is for the reference's lanes products, cuda/kernels.cu:1334-1375). */
+int tmh_plan_set_mode(uint64_t plan, uint32_t mode);
+
 /* ------------------------------------------------- the rest of the decode graph
  *
  * The F32 ops a Llama decode step runs besides its products, each with the
@@ -459,6 +468,14 @@ int tmh_llama_reset(uint64_t model, uint32_t row);
 /* Queues one decode step of every row with the device-held state, for timing
  * (the step tmh_llama_generate repeats); `graph` as there. Does not wait. */
 int tmh_llama_step(uint64_t model, uint32_t graph);
+
+/* The BlockMatMulMode of the decoder's products: TMH_MODE_AUTO (default:
+ * the host's bits) or TMH_MODE_UNORDERED (each product folds in its own
+ * order, as tmh_plan_set_mode; a measurement mode that prices the host's
+ * order in a decode step, as the reference's CUDA device does with
+ * block_mode = Unordered, cuda.cr:750-756). A captured step graph is
+ * dropped when the mode changes. */
+int tmh_llama_set_mode(uint64_t model, uint32_t mode);
 
 int tmh_llama_destroy(uint64_t model);
 

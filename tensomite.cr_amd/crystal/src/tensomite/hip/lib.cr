@@ -164,6 +164,7 @@ module Tensomite
     fun plan_run = tmh_plan_run(plan : UInt64) : Int32
     fun plan_destroy = tmh_plan_destroy(plan : UInt64) : Int32
     fun plan_describe = tmh_plan_describe(plan : UInt64, text : UInt8*, size : UInt32) : Int32
+    fun plan_set_mode = tmh_plan_set_mode(plan : UInt64, mode : UInt32) : Int32
 
     # the rest of the decode graph, with the host kernels' bits
     fun rmsnorm = tmh_rmsnorm(x : DevicePtr, ldx : UInt32, weight : DevicePtr, rows : UInt32, n : UInt32,
@@ -191,6 +192,7 @@ module Tensomite
     fun llama_length = tmh_llama_length(model : UInt64, row : UInt32, length : Int32*) : Int32
     fun llama_reset = tmh_llama_reset(model : UInt64, row : UInt32) : Int32
     fun llama_step = tmh_llama_step(model : UInt64, graph : UInt32) : Int32
+    fun llama_set_mode = tmh_llama_set_mode(model : UInt64, mode : UInt32) : Int32
     fun llama_destroy = tmh_llama_destroy(model : UInt64) : Int32
 
     # GGUF files

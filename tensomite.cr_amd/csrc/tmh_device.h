@@ -104,6 +104,21 @@ __device__ __forceinline__ Q8Quad quantize_quad(float v0, float v1, float v2, fl
     return out;
 }
 
+// ---------------------------------------------------------- UNORDERED fold
+
+// The fold of BlockMatMulMode::Unordered (quant.cr:14-17, a measurement
+// mode): a row's contributions as four interleaved running sums, s[i % 4]
+// += c[i], then (s0 + s1) + (s2 + s3) -- four independent chains of adds
+// where the host's block order is one, so the last bits may differ. Each
+// kernel's fold reads its contributions exactly as for the ordered fold and
+// only adds them this way, so the mode prices the order alone.
+struct Fold4 {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    __device__ __forceinline__ void add4(float a, float b, float c, float d) { s0 += a, s1 += b, s2 += c, s3 += d; }
+    __device__ __forceinline__ void add2(float a, float b) { s0 += a, s1 += b; }
+    __device__ __forceinline__ float total() const { return (s0 + s1) + (s2 + s3); }
+};
+
 // ---------------------------------------------------------------- Maths.exp
 
 // Maths.exp (maths.cr:36-54): x = n·ln2 + r with n = round(x·log2 e) by the

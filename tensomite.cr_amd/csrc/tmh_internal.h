@@ -25,6 +25,18 @@ void count_launch();
         hipLaunchKernelGGL(__VA_ARGS__); \
     } while (0)
 
+// Whether the product launches this thread queues fold each row's
+// contributions in UNORDERED's order (Fold4: four running sums) rather than the
+// host's block order: set, for the launches of one call, by tmh_block_matmul
+// in TMH_MODE_UNORDERED and by plans and decoders set to that mode
+// (measurement only). The launchers pass it to the kernels.
+bool tree_fold();
+struct TreeFold {
+    bool saved;
+    explicit TreeFold(bool on);
+    ~TreeFold();
+};
+
 // Bytes of one block of 32 values, by kind (dtype.cr:237-244).
 constexpr uint32_t block_bytes(uint32_t kind) { return kind == 0 ? 34u : kind == 1 ? 18u : 20u; }
 
@@ -136,6 +148,7 @@ struct StreamLaunch {
     const StreamStart* starts;
     uint32_t total, grid, ring, has_bias, act_bytes, part_floats, x_floats, act_offset;
     size_t lds;
+    uint32_t tree;  // UNORDERED's fold
 };
 
 // Host side: fills in each product's geometry and steps (w, x, dst, bias, n,

@@ -24,6 +24,14 @@
 
 namespace tmh {
 
+namespace {
+thread_local bool t_tree_fold = false;
+}  // namespace
+
+bool tree_fold() { return t_tree_fold; }
+TreeFold::TreeFold(bool on) : saved(t_tree_fold) { t_tree_fold = on; }
+TreeFold::~TreeFold() { t_tree_fold = saved; }
+
 // ------------------------------------------------------ activation quantise
 
 // One group of 8 lanes per block of 32 activations, 4 values a lane: the
@@ -280,11 +288,12 @@ __device__ __forceinline__ void load_activations(const Activations& act, uint32_
 // each 8-lane group takes a block of 32 of them, SwiGLU
 // (gate / (Maths.exp(-gate) + 1) · up) 4 a lane, and quantises the block
 // into `glu` as the quantise pass lays out an [NB, H] activation.
-template <int KIND, int NB, bool GLU = false>
+template <int KIND, int NB, bool GLU = false, bool TREE = false>
 __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activations act, float* __restrict__ dst,
                                             const float* __restrict__ bias, uint32_t bias_ld, uint32_t n,
                                             uint32_t k, uint32_t tr, uint32_t stride, uint32_t tile, float* part,
                                             Activations glu = Activations{}) {
+    constexpr bool tree = TREE;  // UNORDERED's fold (Fold4)
     constexpr uint32_t PW = Fmt<KIND>::PW;
     const uint32_t t = threadIdx.x;
     const uint32_t nb = k >> 5;
@@ -335,14 +344,24 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
             const float* c = part + (size_t)o * stride;
             float sum = 0.0f;
             uint32_t i = 0;
-            for (; i + 4 <= nb; i += 4) {
-                const float4 v = *(const float4*)(c + i);
-                sum += v.x;
-                sum += v.y;
-                sum += v.z;
-                sum += v.w;
+            if (tree) {
+                Fold4 u;
+                for (; i + 4 <= nb; i += 4) {
+                    const float4 v = *(const float4*)(c + i);
+                    u.add4(v.x, v.y, v.z, v.w);
+                }
+                for (; i < nb; ++i) u.s0 += c[i];
+                sum = u.total();
+            } else {
+                for (; i + 4 <= nb; i += 4) {
+                    const float4 v = *(const float4*)(c + i);
+                    sum += v.x;
+                    sum += v.y;
+                    sum += v.z;
+                    sum += v.w;
+                }
+                for (; i < nb; ++i) sum += c[i];
             }
-            for (; i < nb; ++i) sum += c[i];
             if constexpr (GLU) {
                 outs[o] = sum;
             } else {
@@ -376,23 +395,23 @@ __device__ __forceinline__ void matvec_tile(const uint8_t* __restrict__ w, Activ
 
 // bias_ld: the bias's elements per activation row (0: one bias row for
 // every activation row; n: a row each, e.g. a residual).
-template <int KIND, int NB>
+template <int KIND, int NB, bool TREE>
 __global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ w, Activations act,
                                                 float* __restrict__ dst, const float* __restrict__ bias,
                                                 uint32_t bias_ld, uint32_t n, uint32_t k, uint32_t tr,
                                                 uint32_t stride) {
     extern __shared__ float part[];
-    matvec_tile<KIND, NB>(w, act, dst, bias, bias_ld, n, k, tr, stride, blockIdx.x, part);
+    matvec_tile<KIND, NB, false, TREE>(w, act, dst, bias, bias_ld, n, k, tr, stride, blockIdx.x, part);
 }
 
 // The lanes product over a merged [gate | up] matrix with SwiGLU and the
 // activation quantiser in its epilogue (matvec_tile's GLU form): `glu`
 // receives quantised SwiGLU(gate, up) rows of n / 2.
-template <int KIND, int NB>
+template <int KIND, int NB, bool TREE>
 __global__ __launch_bounds__(256) void k_matvec_glu(const uint8_t* __restrict__ w, Activations act, uint32_t n,
                                                     uint32_t k, uint32_t tr, uint32_t stride, Activations glu) {
     extern __shared__ float part[];
-    matvec_tile<KIND, NB, true>(w, act, nullptr, nullptr, 0, n, k, tr, stride, blockIdx.x, part, glu);
+    matvec_tile<KIND, NB, true, TREE>(w, act, nullptr, nullptr, 0, n, k, tr, stride, blockIdx.x, part, glu);
 }
 
 
@@ -504,13 +523,14 @@ __host__ __device__ inline OneLds one_lds(uint32_t k, uint32_t tr, uint32_t row_
 // quantiser on the tile's gate/up outputs into glu. k a multiple of 64 with
 // ONE_THREADS % (k / 64) == 0 (whole rows of pairs per pass), rows whole
 // 16-byte pieces starting 16-byte aligned.
-template <int KIND, bool NORM, bool GLU, bool PLAIN = false, uint32_t XR = 1>
+template <int KIND, bool NORM, bool GLU, bool PLAIN = false, uint32_t XR = 1, bool TREE = false>
 __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ nw, float eps, Activations act,
                                                             float* __restrict__ dst, const float* __restrict__ bias,
                                                             uint32_t n, uint32_t k, uint32_t tr, uint32_t stride,
                                                             Activations glu, uint32_t ldx) {
+    constexpr bool tree = TREE;  // UNORDERED's fold (Fold4)
     extern __shared__ float4 lds4[];
     uint8_t* base = reinterpret_cast<uint8_t*>(lds4);
     __shared__ float root_slot;
@@ -687,26 +707,43 @@ __global__ __launch_bounds__(ONE_THREADS) void k_matvec_one(const uint8_t* __res
         const float* c = part + (size_t)(b * tr + o) * stride;
         float sum = 0.0f;
         uint32_t i = 0;
-        for (; i + 64u <= nb; i += 64u) {
-            float4 v[16];
+        if (tree) {
+            Fold4 u;
+            for (; i + 64u <= nb; i += 64u) {
+                float4 v[16];
 #pragma unroll
-            for (int q = 0; q < 16; ++q) v[q] = *(const float4*)(c + i + 4u * q);
+                for (int q = 0; q < 16; ++q) v[q] = *(const float4*)(c + i + 4u * q);
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                sum += v[q].x;
-                sum += v[q].y;
-                sum += v[q].z;
-                sum += v[q].w;
+                for (int q = 0; q < 16; ++q) u.add4(v[q].x, v[q].y, v[q].z, v[q].w);
             }
+            for (; i + 4 <= nb; i += 4) {
+                const float4 v = *(const float4*)(c + i);
+                u.add4(v.x, v.y, v.z, v.w);
+            }
+            for (; i < nb; ++i) u.s0 += c[i];
+            sum = u.total();
+        } else {
+            for (; i + 64u <= nb; i += 64u) {
+                float4 v[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v[q] = *(const float4*)(c + i + 4u * q);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    sum += v[q].x;
+                    sum += v[q].y;
+                    sum += v[q].z;
+                    sum += v[q].w;
+                }
+            }
+            for (; i + 4 <= nb; i += 4) {
+                const float4 v = *(const float4*)(c + i);
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+            }
+            for (; i < nb; ++i) sum += c[i];
         }
-        for (; i + 4 <= nb; i += 4) {
-            const float4 v = *(const float4*)(c + i);
-            sum += v.x;
-            sum += v.y;
-            sum += v.z;
-            sum += v.w;
-        }
-        for (; i < nb; ++i) sum += c[i];
         if constexpr (GLU) {
             outs[o] = sum;
         } else {
@@ -848,6 +885,7 @@ __device__ __forceinline__ void compute_steps(const RowProduct& p, const TileGeo
 
 // Adds each row of a tile's contributions in block order -- the host's order
 // -- and writes it plus its bias, already loaded (thread r takes row r).
+template <bool tree>
 __device__ __forceinline__ void fold_tile(const float* part, const RowProduct& p, const TileGeo& g, float bias) {
     const uint32_t r = threadIdx.x;
     if (r >= p.tr) return;
@@ -856,14 +894,24 @@ __device__ __forceinline__ void fold_tile(const float* part, const RowProduct& p
     const float* c = part + (size_t)r * p.stride;
     float sum = 0.0f;
     uint32_t i = 0;
-    for (; i + 4 <= g.nb; i += 4) {
-        const float4 v = *(const float4*)(c + i);
-        sum += v.x;
-        sum += v.y;
-        sum += v.z;
-        sum += v.w;
+    if (tree) {
+        Fold4 u;
+        for (; i + 4 <= g.nb; i += 4) {
+            const float4 v = *(const float4*)(c + i);
+            u.add4(v.x, v.y, v.z, v.w);
+        }
+        for (; i < g.nb; ++i) u.s0 += c[i];
+        sum = u.total();
+    } else {
+        for (; i + 4 <= g.nb; i += 4) {
+            const float4 v = *(const float4*)(c + i);
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+        }
+        for (; i < g.nb; ++i) sum += c[i];
     }
-    for (; i < g.nb; ++i) sum += c[i];
     *(__attribute__((address_space(1))) float*)(p.dst + row) = p.bias ? sum + bias : sum;
 }
 
@@ -946,7 +994,7 @@ __device__ __forceinline__ uint32_t owner_of(const uint32_t* __restrict__ owner,
 // activations and biases) ahead of this tile's fold. LDS: act_bytes for
 // activations, then the contributions. Every workgroup leaves after its last
 // tile; all loop bounds are uniform over the workgroup.
-template <int KIND, uint32_t D>
+template <int KIND, uint32_t D, bool TREE>
 __device__ __forceinline__ void matvec_rows(const RowProduct* __restrict__ table, const uint32_t* __restrict__ owner,
                                             const RowProduct& single, uint32_t total, uint32_t act_bytes) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1005,24 +1053,24 @@ __device__ __forceinline__ void matvec_rows(const RowProduct* __restrict__ table
         compute_steps<KIND, D>(p, g, s0 + D, ub, v, part);
 
         __syncthreads();  // every contribution of this tile is in `part`
-        fold_tile(part, p, g, bias);
+        fold_tile<TREE>(part, p, g, bias);
         if (!more) break;
         __syncthreads();  // the fold has read `part`; `act` may be replaced
         tile = next, pi = npi, p = q, g = h, bias = nbias;
     }
 }
 
-template <int KIND, uint32_t D>
+template <int KIND, uint32_t D, bool TREE>
 __global__ __launch_bounds__(256) void k_matvec_rows(const RowProduct* __restrict__ table,
                                                      const uint32_t* __restrict__ owner, uint32_t total,
                                                      uint32_t act_bytes) {
     const RowProduct none{};
-    matvec_rows<KIND, D>(table, owner, none, total, act_bytes);
+    matvec_rows<KIND, D, TREE>(table, owner, none, total, act_bytes);
 }
 
-template <int KIND, uint32_t D>
+template <int KIND, uint32_t D, bool TREE>
 __global__ __launch_bounds__(256) void k_matvec_row(RowProduct p, uint32_t act_bytes) {
-    matvec_rows<KIND, D>(nullptr, nullptr, p, p.tiles, act_bytes);
+    matvec_rows<KIND, D, TREE>(nullptr, nullptr, p, p.tiles, act_bytes);
 }
 
 // ------------------------------------------- one row, streamed through LDS
@@ -1198,7 +1246,11 @@ __device__ __forceinline__ void prepare_global(uint8_t* act, const StreamProduct
 // trip rather than one per four values (the fold is on every step's
 // critical path); the last batch reads up to 14 floats past c[nb-1], other
 // LDS data of the workgroup, and skips them.
+__device__ __forceinline__ float fold_row_unordered(const float* c, uint32_t nb);
+
+template <bool TREE>
 __device__ __forceinline__ float fold_row(const float* c, uint32_t nb) {
+    if constexpr (TREE) return fold_row_unordered(c, nb);
     float sum = 0.0f;
     for (uint32_t q = 0; q < nb; q += 16u) {
         float4 e[4];
@@ -1220,6 +1272,27 @@ __device__ __forceinline__ float fold_row(const float* c, uint32_t nb) {
         }
     }
     return sum;
+}
+
+// fold_row's reads with UNORDERED's four running sums.
+__device__ __forceinline__ float fold_row_unordered(const float* c, uint32_t nb) {
+    Fold4 s;
+    for (uint32_t q = 0; q < nb; q += 16u) {
+        float4 e[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) e[u] = *(const float4*)(c + q + 4u * u);
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) asm volatile("" : "+v"(e[u].x), "+v"(e[u].y), "+v"(e[u].z), "+v"(e[u].w));
+        const uint32_t left = nb - q;
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) {
+            if (4u * u >= left) break;
+            s.add2(e[u].x, e[u].y);
+            if (4u * u + 2u >= left) break;
+            s.s2 += e[u].z, s.s3 += e[u].w;
+        }
+    }
+    return s.total();
 }
 
 // Per-thread geometry of a product: the thread's row r of a step and pair j,
@@ -1245,7 +1318,7 @@ __device__ __forceinline__ StreamLane stream_lane(const StreamProduct& P) {
 // the activations (two buffers of act_bytes; one for a one-product plan). Before the loop, the x of the range's first two products
 // (x_floats apart; none when x_floats is 0) is staged from ring slot R-1
 // on, over memory first written in the loop.
-template <int KIND, uint32_t R, bool HB>
+template <int KIND, uint32_t R, bool HB, bool TREE>
 __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __restrict__ table,
                                                        const StreamStart* __restrict__ starts, uint32_t total,
                                                        uint32_t act_bytes, uint32_t part_floats, uint32_t x_floats,
@@ -1379,7 +1452,7 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
         if (issued < count) issue_next();
         // The previous step's fold.
         if (t < frows) {
-            float sum = fold_row(parts + ((i - 1u) & 1u) * part_floats + t * fstride, fnb);
+            float sum = fold_row<TREE>(parts + ((i - 1u) & 1u) * part_floats + t * fstride, fnb);
             if (HB && fbias) sum += biases[fbslot * 256u + t];
             *(__attribute__((address_space(1))) float*)(fdst + t) = sum;
         }
@@ -1415,7 +1488,7 @@ __global__ __launch_bounds__(256) void k_matvec_stream(const StreamProduct* __re
     }
     step_barrier<0>();
     if (t < frows) {
-        float sum = fold_row(parts + ((count - 1u) & 1u) * part_floats + t * fstride, fnb);
+        float sum = fold_row<TREE>(parts + ((count - 1u) & 1u) * part_floats + t * fstride, fnb);
         if (HB && fbias) sum += biases[fbslot * 256u + t];
         *(__attribute__((address_space(1))) float*)(fdst + t) = sum;
     }
@@ -2125,10 +2198,11 @@ struct Few {
     static_assert(LDS <= 160u * 1024u, "one workgroup's LDS");
 };
 
-template <int KIND, uint32_t DEPTH, uint32_t SB>
+template <int KIND, uint32_t DEPTH, uint32_t SB, bool TREE>
 __global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __restrict__ w, Activations act,
                                                             float* __restrict__ dst, const float* __restrict__ bias,
                                                             uint32_t bias_ld, uint32_t rows, uint32_t n, uint32_t k) {
+    constexpr bool tree = TREE;  // UNORDERED's fold (four running sums a stage)
     using F = Few<KIND, DEPTH, SB>;
     constexpr uint32_t PER = F::PER;
     __shared__ __attribute__((aligned(16))) uint8_t lds[F::LDS];
@@ -2268,8 +2342,16 @@ __global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __res
             // c + 16 (r / 4).
             const float* ct = (const float*)(lds + F::PK + ((s - 1u) & 1u) * F::P_BYTES) +
                               (fc + 16u * (fr >> 2)) * 4u + (fr & 3u);
+            if (tree) {
+                // UNORDERED: the stage's contributions as four running sums
+                float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (uint32_t b = 0; b < SB; ++b) acc += ct[b * 256u];
+                for (uint32_t b = 0; b < SB; ++b) u[b & 3u] += ct[b * 256u];
+                acc += (u[0] + u[1]) + (u[2] + u[3]);
+            } else {
+#pragma unroll
+                for (uint32_t b = 0; b < SB; ++b) acc += ct[b * 256u];
+            }
         }
         // Stage s + 1 has landed (the loads of later stages stay in
         // flight); the contributions written above are complete, and the
@@ -2560,11 +2642,12 @@ __device__ __forceinline__ v4i pair_acts(const uint8_t* row, uint32_t b, uint32_
 // the quantiser on the tile's gate/up outputs into glu, as k_matvec_one. Each
 // output depends on its own activation row only, so the bits are those of one
 // row at a time.
-template <int KIND, uint32_t MODE, bool GLU, int NB>
+template <int KIND, uint32_t MODE, bool GLU, int NB, bool TREE>
 __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
     const uint8_t* __restrict__ w, const float* __restrict__ x, uint32_t ldx, const float* __restrict__ nw, float eps,
     Activations act, float* __restrict__ dst, const float* __restrict__ bias, uint32_t bias_ld, uint32_t n, uint32_t k,
     uint32_t tr, uint32_t tpp, uint32_t bufs, Activations glu) {
+    constexpr bool tree = TREE;  // UNORDERED's fold (Fold4)
     static_assert(NB >= 1 && NB <= 8, "activation rows of a launch");
     constexpr uint32_t WAVES = NbShape<NB>::WAVES, THREADS = NbShape<NB>::THREADS, PER = NbShape<NB>::PER;
     constexpr uint32_t PP = PER / 2u;  // pairs of a chunk a wave (up to 8 rows)
@@ -2711,17 +2794,30 @@ __global__ __launch_bounds__(NbShape<NB>::THREADS) void k_matvec_nb(
         // read 32 at a time into registers before they are added
         const float* cp = from + ft * tile_floats + fb * prow + fr * pstride;
         uint32_t i = 0;
-        for (; i + 32u <= cl; i += 32u) {
-            float2 vv[16];
+        if (tree) {
+            Fold4 u;
+            for (; i + 32u <= cl; i += 32u) {
+                float2 vv[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
+                for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                acc += vv[e].x;
-                acc += vv[e].y;
+                for (int e = 0; e < 16; e += 2) u.add4(vv[e].x, vv[e].y, vv[e + 1].x, vv[e + 1].y);
             }
+            for (; i < cl; ++i) u.s0 += cp[i];
+            acc += u.total();
+        } else {
+            for (; i + 32u <= cl; i += 32u) {
+                float2 vv[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) vv[e] = *reinterpret_cast<const float2*>(cp + i + 2u * e);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc += vv[e].x;
+                    acc += vv[e].y;
+                }
+            }
+            for (; i < cl; ++i) acc += cp[i];
         }
-        for (; i < cl; ++i) acc += cp[i];
         if (last) {
             const uint32_t r = 16u * oc + fr;
             if constexpr (GLU) {
@@ -3093,8 +3189,12 @@ static hipError_t launch_lanes_nb(const uint8_t* w, Activations act, float* dst,
     const uint32_t stride = lanes_stride(nb);
     const size_t lds = (size_t)NB * tr * stride * sizeof(float);
     const uint32_t grid = (n + tr - 1u) / tr;
-    TMH_LAUNCH((k_matvec<KIND, NB>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k, tr,
-                       stride);
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec<KIND, NB, true>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k,
+                   tr, stride);
+    else
+        TMH_LAUNCH((k_matvec<KIND, NB, false>), dim3(grid), dim3(256), lds, stream, w, act, dst, bias, bias_ld, n, k,
+                   tr, stride);
     return hipGetLastError();
 }
 
@@ -3226,15 +3326,29 @@ hipError_t launch_rows(uint32_t kind, const RowProduct* table, const uint32_t* o
     const uint32_t grid = balanced_grid(tiles, compute_units);
     const uint32_t ab = (uint32_t)align16(act_bytes);
     const size_t lds = ab + part_bytes;
-    if (kind == 0)
-        TMH_LAUNCH((k_matvec_rows<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
-                           ab);
-    else if (kind == 1)
-        TMH_LAUNCH((k_matvec_rows<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
-                           ab);
-    else
-        TMH_LAUNCH((k_matvec_rows<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, table, owner, tiles,
-                           ab);
+    const bool tree = tree_fold();
+    if (kind == 0) {
+        if (tree)
+            TMH_LAUNCH((k_matvec_rows<0, Depth<0>::D, true>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+        else
+            TMH_LAUNCH((k_matvec_rows<0, Depth<0>::D, false>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+    } else if (kind == 1) {
+        if (tree)
+            TMH_LAUNCH((k_matvec_rows<1, Depth<1>::D, true>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+        else
+            TMH_LAUNCH((k_matvec_rows<1, Depth<1>::D, false>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+    } else {
+        if (tree)
+            TMH_LAUNCH((k_matvec_rows<2, Depth<2>::D, true>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+        else
+            TMH_LAUNCH((k_matvec_rows<2, Depth<2>::D, false>), dim3(grid), dim3(256), lds, stream, table,
+                       owner, tiles, ab);
+    }
     return hipGetLastError();
 }
 
@@ -3252,12 +3366,23 @@ hipError_t launch_row(uint32_t kind, const uint8_t* w, const float* x, float* ds
     const uint32_t grid = balanced_grid(p.tiles, compute_units);
     const uint32_t ab = (uint32_t)row_act_bytes(p);
     const size_t lds = ab + row_part_bytes(p);
-    if (kind == 0)
-        TMH_LAUNCH((k_matvec_row<0, Depth<0>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
-    else if (kind == 1)
-        TMH_LAUNCH((k_matvec_row<1, Depth<1>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
-    else
-        TMH_LAUNCH((k_matvec_row<2, Depth<2>::D>), dim3(grid), dim3(256), lds, stream, p, ab);
+    const bool tree = tree_fold();
+    if (kind == 0) {
+        if (tree)
+            TMH_LAUNCH((k_matvec_row<0, Depth<0>::D, true>), dim3(grid), dim3(256), lds, stream, p, ab);
+        else
+            TMH_LAUNCH((k_matvec_row<0, Depth<0>::D, false>), dim3(grid), dim3(256), lds, stream, p, ab);
+    } else if (kind == 1) {
+        if (tree)
+            TMH_LAUNCH((k_matvec_row<1, Depth<1>::D, true>), dim3(grid), dim3(256), lds, stream, p, ab);
+        else
+            TMH_LAUNCH((k_matvec_row<1, Depth<1>::D, false>), dim3(grid), dim3(256), lds, stream, p, ab);
+    } else {
+        if (tree)
+            TMH_LAUNCH((k_matvec_row<2, Depth<2>::D, true>), dim3(grid), dim3(256), lds, stream, p, ab);
+        else
+            TMH_LAUNCH((k_matvec_row<2, Depth<2>::D, false>), dim3(grid), dim3(256), lds, stream, p, ab);
+    }
     return hipGetLastError();
 }
 
@@ -3392,8 +3517,12 @@ template <int KIND, bool HB>
 static hipError_t launch_stream_kind(const StreamLaunch& l, hipStream_t stream) {
 #define TMH_STREAM(RING)                                                                                     \
     case RING:                                                                                               \
-        TMH_LAUNCH((k_matvec_stream<KIND, RING, HB>), dim3(l.grid), dim3(256), l.lds, stream, l.table, \
-                           l.starts, l.total, l.act_bytes, l.part_floats, l.x_floats, l.act_offset);          \
+        if (l.tree)                                                                                          \
+            TMH_LAUNCH((k_matvec_stream<KIND, RING, HB, true>), dim3(l.grid), dim3(256), l.lds, stream,      \
+                       l.table, l.starts, l.total, l.act_bytes, l.part_floats, l.x_floats, l.act_offset);    \
+        else                                                                                                 \
+            TMH_LAUNCH((k_matvec_stream<KIND, RING, HB, false>), dim3(l.grid), dim3(256), l.lds, stream,     \
+                       l.table, l.starts, l.total, l.act_bytes, l.part_floats, l.x_floats, l.act_offset);    \
         break;
     switch (l.ring) {
         TMH_STREAM(2) TMH_STREAM(3) TMH_STREAM(4) TMH_STREAM(5) TMH_STREAM(6) TMH_STREAM(7) TMH_STREAM(8)
@@ -3404,7 +3533,9 @@ static hipError_t launch_stream_kind(const StreamLaunch& l, hipStream_t stream) 
     return hipGetLastError();
 }
 
-hipError_t launch_stream(uint32_t kind, const StreamLaunch& l, hipStream_t stream) {
+hipError_t launch_stream(uint32_t kind, const StreamLaunch& given, hipStream_t stream) {
+    StreamLaunch l = given;
+    l.tree = tree_fold() ? 1u : 0u;
     if (l.grid == 0) return hipSuccess;
     switch (kind * 2u + l.has_bias) {
     case 0: return launch_stream_kind<0, false>(l, stream);
@@ -3470,12 +3601,19 @@ template <int KIND>
 static hipError_t launch_few(const uint8_t* w, Activations act, float* dst, const float* bias, uint32_t bias_ld,
                              uint32_t rows, uint32_t n, uint32_t k, hipStream_t stream) {
     const uint32_t grid = (n + FEW_COLS - 1u) / FEW_COLS;
-    if (grid > 256u)
-        TMH_LAUNCH((k_matmul_few<KIND, 3, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
-                           bias_ld, rows, n, k);
+    const bool tree = tree_fold();
+    if (grid > 256u && tree)
+        TMH_LAUNCH((k_matmul_few<KIND, 3, 16, true>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                   bias_ld, rows, n, k);
+    else if (grid > 256u)
+        TMH_LAUNCH((k_matmul_few<KIND, 3, 16, false>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                   bias_ld, rows, n, k);
+    else if (tree)
+        TMH_LAUNCH((k_matmul_few<KIND, 6, 16, true>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                   bias_ld, rows, n, k);
     else
-        TMH_LAUNCH((k_matmul_few<KIND, 6, 16>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
-                           bias_ld, rows, n, k);
+        TMH_LAUNCH((k_matmul_few<KIND, 6, 16, false>), dim3(grid), dim3(FEW_THREADS), 0, stream, w, act, dst, bias,
+                   bias_ld, rows, n, k);
     return hipGetLastError();
 }
 
@@ -3505,6 +3643,9 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
     const bool fits = lanes_fit(w, k);
     const bool matrix = fits && (mode == 7u /* MATRIX */ || (mode == 0u /* AUTO */ && rows >= MATRIX_ROWS));
     const bool fused = mode == 3u /* UNORDERED */ && rows >= MATRIX_ROWS;
+    // Below MATRIX_ROWS, UNORDERED takes AUTO's kernels, each folding in its
+    // own order (tree_fold, set by the entry point)
+    const bool autoish = mode == 0u /* AUTO */ || mode == 3u /* UNORDERED */;
     if ((matrix || fused) && mx_fits(w, act, kind, k)) {
         switch (kind) {
         case 0: return launch_mx<0>(fused, w, act, dst, bias, rows, n, k, stream);
@@ -3512,7 +3653,7 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
         default: return launch_mx<2>(fused, w, act, dst, bias, rows, n, k, stream);
         }
     }
-    if (mode == 0u /* AUTO */ && (rows == 1u || rows == 8u) && few_rows_kernel()) {
+    if (autoish && (rows == 1u || rows == 8u) && few_rows_kernel()) {
         // one or 8 rows: the weights of each workgroup's tile staged into LDS
         // at once, the products on the matrix cores (measured, Q4_1: 8 rows
         // 9.8 / 13.4 us against 12.2 / 14.9 for the lanes kernel at 8192x2048
@@ -3523,7 +3664,7 @@ hipError_t launch_block_matmul(uint32_t kind, uint32_t mode, const uint8_t* w, A
                                                  n, k, compute_units, stream);
         if (e != hipErrorInvalidValue) return e;
     }
-    if (mode == 0u /* AUTO */ && few_fits(w, act, kind, rows, k))
+    if (autoish && few_fits(w, act, kind, rows, k))
         return launch_few_kind(kind, w, act, dst, bias, 0, rows, n, k, stream);
     if (matrix) {
         switch (kind) {
@@ -3572,8 +3713,12 @@ template <int KIND, int NB>
 static hipError_t launch_glu_nb(const uint8_t* w, Activations act, uint32_t H, uint32_t k, Activations glu,
                                 hipStream_t stream) {
     const uint32_t nb = k >> 5, h = glu_half(nb);
-    TMH_LAUNCH((k_matvec_glu<KIND, NB>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H, k,
-                       2u * h, lanes_stride(nb), glu);
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec_glu<KIND, NB, true>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H, k,
+                   2u * h, lanes_stride(nb), glu);
+    else
+        TMH_LAUNCH((k_matvec_glu<KIND, NB, false>), dim3(H / h), dim3(256), glu_lds(NB, nb), stream, w, act, 2u * H,
+                   k, 2u * h, lanes_stride(nb), glu);
     return hipGetLastError();
 }
 
@@ -3654,8 +3799,12 @@ static hipError_t launch_one(const uint8_t* w, const float* x, const float* nw, 
     const uint32_t tr = one_tile(KIND, n, k, NORM, compute_units, PLAIN, XR);
     const OneLds L = one_lds(k, tr, nb * Fmt<KIND>::BB, stride, NORM, false, PLAIN, XR);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    TMH_LAUNCH((k_matvec_one<KIND, NORM, false, PLAIN, XR>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS), L.end,
-                       stream, w, x, nw, eps, act, dst, bias, n, k, tr, stride, Activations{}, ldx);
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec_one<KIND, NORM, false, PLAIN, XR, true>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS),
+                   L.end, stream, w, x, nw, eps, act, dst, bias, n, k, tr, stride, Activations{}, ldx);
+    else
+        TMH_LAUNCH((k_matvec_one<KIND, NORM, false, PLAIN, XR, false>), dim3((n + tr - 1u) / tr), dim3(ONE_THREADS),
+                   L.end, stream, w, x, nw, eps, act, dst, bias, n, k, tr, stride, Activations{}, ldx);
     return hipGetLastError();
 }
 
@@ -3717,8 +3866,12 @@ static hipError_t launch_glu_one(const uint8_t* w, const float* x, const float* 
     const uint32_t nb = k >> 5, h = glu_half(nb), stride = lanes_stride(nb);
     const OneLds L = one_lds(k, 2u * h, nb * Fmt<KIND>::BB, stride, true, true);
     if (L.end > ONE_LDS_LIMIT || H % h != 0) return hipErrorInvalidValue;
-    TMH_LAUNCH((k_matvec_one<KIND, true, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w, x, norm, eps,
-                       Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu, 0u);
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec_one<KIND, true, true, false, 1u, true>), dim3(H / h), dim3(ONE_THREADS), L.end, stream, w,
+                   x, norm, eps, Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu, 0u);
+    else
+        TMH_LAUNCH((k_matvec_one<KIND, true, true, false, 1u, false>), dim3(H / h), dim3(ONE_THREADS), L.end, stream,
+                   w, x, norm, eps, Activations{}, nullptr, nullptr, 2u * H, k, 2u * h, stride, glu, 0u);
     return hipGetLastError();
 }
 
@@ -3809,8 +3962,12 @@ static hipError_t launch_nb(const uint8_t* w, const float* x, uint32_t ldx, cons
     const uint32_t bufs = nb_bufs(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp);
     const NbLds L = nb_lds(NB, KIND, k, tr, nb * Fmt<KIND>::BB, MODE, false, tpp, bufs);
     if (L.end > ONE_LDS_LIMIT) return hipErrorInvalidValue;
-    TMH_LAUNCH((k_matvec_nb<KIND, MODE, false, NB>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS), L.end,
-                       stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, bufs, Activations{});
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec_nb<KIND, MODE, false, NB, true>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS),
+                   L.end, stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, bufs, Activations{});
+    else
+        TMH_LAUNCH((k_matvec_nb<KIND, MODE, false, NB, false>), dim3((n + tr - 1u) / tr), dim3(NbShape<NB>::THREADS),
+                   L.end, stream, w, x, ldx, nw, eps, act, dst, bias, bias_ld, n, k, tr, tpp, bufs, Activations{});
     return hipGetLastError();
 }
 
@@ -3897,9 +4054,12 @@ static hipError_t launch_nb_glu(const uint8_t* w, const float* x, uint32_t ldx, 
     const uint32_t tpp = nb_tpp(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true);
     const uint32_t bufs = nb_bufs(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp);
     const NbLds L = nb_lds(NB, KIND, k, 2u * h, nb * Fmt<KIND>::BB, MODE, true, tpp, bufs);
-    TMH_LAUNCH((k_matvec_nb<KIND, MODE, true, NB>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream, w, x,
-                       ldx, nw,
-                       eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, bufs, glu);
+    if (tree_fold())
+        TMH_LAUNCH((k_matvec_nb<KIND, MODE, true, NB, true>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream,
+                   w, x, ldx, nw, eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, bufs, glu);
+    else
+        TMH_LAUNCH((k_matvec_nb<KIND, MODE, true, NB, false>), dim3(H / h), dim3(NbShape<NB>::THREADS), L.end, stream,
+                   w, x, ldx, nw, eps, act, nullptr, nullptr, 0, 2u * H, k, 2u * h, tpp, bufs, glu);
     return hipGetLastError();
 }
 

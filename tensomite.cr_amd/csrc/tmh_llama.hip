@@ -75,6 +75,7 @@ struct Llama {
 
     hipGraphExec_t graph = nullptr;
     void* owned = nullptr;  // weights this decoder loaded itself (tmh_llama_load_gguf)
+    uint32_t mode = TMH_MODE_AUTO;  // the products' BlockMatMulMode: AUTO, or UNORDERED (tmh_llama_set_mode)
 };
 
 // Rows a forward takes through the products whose workgroups stage their
@@ -172,6 +173,7 @@ hipError_t residual(const Llama& m, const DeviceContext& ctx, const uint8_t* w, 
 // its RoPE and cache write run inside the attention launch.
 hipError_t forward_tokens(const Llama& m, const DeviceContext& ctx, uint32_t tokens, uint32_t final_from,
                           uint32_t final_rows, uint32_t logits_row, bool decode) {
+    const tmh::TreeFold order(m.mode == TMH_MODE_UNORDERED);
     const tmh_llama_config& c = m.c;
     const uint32_t W = (uint32_t)c.width, H = (uint32_t)c.hidden, hw = (uint32_t)c.head_width;
     const float scale = (float)(1.0 / std::sqrt((double)hw));
@@ -684,6 +686,23 @@ int tmh_llama_reset(uint64_t model, uint32_t row) {
     m->length[row] = 0;
     m->has_logits[row] = 0;
     m->generating = false;
+    return TMH_SUCCESS;
+}
+
+int tmh_llama_set_mode(uint64_t model, uint32_t mode) {
+    DeviceContext ctx;
+    int err = tmh::device_context(&ctx, false);
+    if (err) return err;
+    Llama* m = model_of(model, ctx, &err);
+    if (!m) return err;
+    if (mode != TMH_MODE_AUTO && mode != TMH_MODE_UNORDERED) return TMH_ERROR_INVALID_VALUE;
+    if (mode != m->mode && m->graph) {
+        // the captured step holds the old mode's kernel arguments
+        (void)hipStreamSynchronize(ctx.stream);
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+    m->mode = mode;
     return TMH_SUCCESS;
 }
 

@@ -767,6 +767,10 @@ constexpr uint64_t ROW_KERNEL_MAX_BYTES = 4ull << 20;
 // hipErrorInvalidValue, nothing launched, when the call is not for it.
 // TMH_FEW_ROWS_KERNEL=lanes keeps the quantise pass and the lanes product,
 // for comparisons.
+// AUTO, or UNORDERED below the matrix cores' rows: the same kernels (UNORDERED
+// folding in its own order).
+bool auto_like(uint32_t mode) { return mode == TMH_MODE_AUTO || mode == TMH_MODE_UNORDERED; }
+
 hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const float* x, uint32_t ldx, float* dst,
                         const float* bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
     static const bool lanes = [] {
@@ -774,7 +778,7 @@ hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const 
         return env && strcmp(env, "lanes") == 0;
     }();
     const uint64_t bytes = (uint64_t)n * (k / 32u) * tmh::block_bytes(kind);
-    if (lanes || mode != TMH_MODE_AUTO || rows > 8u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
+    if (lanes || !auto_like(mode) || rows > 8u || (rows == 1u && bytes <= ROW_KERNEL_MAX_BYTES))
         return hipErrorInvalidValue;
     // One row (k up to 8192), or two of k up to 2048: the one-row kernel
     // quantising x in its prologue (measured, Q4_1, one box: 8192x2048 one
@@ -801,6 +805,7 @@ hipError_t few_rows_f32(const Device& d, uint32_t kind, const uint8_t* w, const 
 int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
                      uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
     if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    const tmh::TreeFold order(mode == TMH_MODE_UNORDERED);
     int err;
     Device* d = current(&err);
     if (!d) return err;
@@ -811,7 +816,7 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
     const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
     // One row of a product of at most ROW_KERNEL_MAX_BYTES of weights: the
     // one-row kernel, which quantises x itself (one launch).
-    if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
+    if (rows == 1 && (!auto_like(mode) || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
         tmh::row_kernel_fits(mode, wrow, k)) {
         hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
                                        d->compute_units, d->stream);
@@ -838,6 +843,7 @@ int tmh_block_matmul(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t
 int tmh_block_matmul_fixed(uint32_t kind, uint64_t w, uint64_t w_byte_offset, uint64_t x, uint32_t ldx, uint64_t dst,
                            uint64_t bias, uint32_t rows, uint32_t n, uint32_t k, uint32_t mode) {
     if (g_kernels_off.load()) return TMH_ERROR_NO_KERNELS;
+    const tmh::TreeFold order(mode == TMH_MODE_UNORDERED);
     const int n_devices = count_devices();
     if (n_devices == 0 || t_device < 0 || t_device >= n_devices) return TMH_ERROR_NO_DEVICE;
     Device* d = &g_devices[t_device];
@@ -857,7 +863,7 @@ int tmh_block_matmul_fixed(uint32_t kind, uint64_t w, uint64_t w_byte_offset, ui
     const uint8_t* wrow = (const uint8_t*)(w + w_byte_offset);
     // The same choice of kernels as tmh_block_matmul: a product that the
     // one-row or the few-rows kernel takes needs no scratch at all.
-    if (rows == 1 && (mode != TMH_MODE_AUTO || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
+    if (rows == 1 && (!auto_like(mode) || (uint64_t)n * (k / 32u) * tmh::block_bytes(kind) <= ROW_KERNEL_MAX_BYTES) &&
         tmh::row_kernel_fits(mode, wrow, k)) {
         hipError_t e = tmh::launch_row(kind, wrow, (const float*)x, (float*)dst, (const float*)bias, n, k,
                                        d->compute_units, d->stream);
@@ -894,6 +900,7 @@ int tmh_block_matmul_quantised(uint32_t kind, uint64_t w, uint64_t w_byte_offset
     if (rows == 0 || n == 0) return TMH_SUCCESS;
     if (!w || !scales || !sums || !totals || !qs || !dst) return TMH_ERROR_INVALID_VALUE;
     if (qs % 16u != 0 || scales % 8u != 0 || sums % 8u != 0 || totals % 8u != 0) return TMH_ERROR_INVALID_VALUE;
+    const tmh::TreeFold order(mode == TMH_MODE_UNORDERED);
     tmh::Activations act{(const float*)scales, (const float*)sums, (const int32_t*)totals, (const int8_t*)qs};
     hipError_t e = tmh::launch_block_matmul(kind, mode, (const uint8_t*)(w + w_byte_offset), act, (float*)dst,
                                             (const float*)bias, rows, n, k, d->compute_units, d->stream);
@@ -936,6 +943,7 @@ struct Plan {
     bool streamed;
     tmh::StreamLaunch stream;
     void* mem;
+    uint32_t mode = TMH_MODE_AUTO;  // AUTO, or UNORDERED (tmh_plan_set_mode)
 };
 
 // Builds the streamed form of a plan; false (nothing allocated) when the
@@ -1061,11 +1069,18 @@ int tmh_plan_run(uint64_t plan) {
     if (!d) return err;
     Plan* p = (Plan*)plan;
     if (p->device != d->index) return TMH_ERROR_INVALID_VALUE;
+    const tmh::TreeFold order(p->mode == TMH_MODE_UNORDERED);
     hipError_t e = p->streamed ? tmh::launch_stream(p->kind, p->stream, d->stream)
                                : tmh::launch_rows(p->kind, p->table, p->owner, p->tiles, p->act_bytes,
                                                   p->part_bytes, d->compute_units, d->stream);
     if (e == hipSuccess) d->gpu_ops.fetch_add(p->count);
     return code(e);
+}
+
+int tmh_plan_set_mode(uint64_t plan, uint32_t mode) {
+    if (!plan || (mode != TMH_MODE_AUTO && mode != TMH_MODE_UNORDERED)) return TMH_ERROR_INVALID_VALUE;
+    ((Plan*)plan)->mode = mode;
+    return TMH_SUCCESS;
 }
 
 int tmh_plan_describe(uint64_t plan, char* text, uint32_t size) {

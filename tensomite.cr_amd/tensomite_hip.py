@@ -162,6 +162,7 @@ SIGNATURES = {
     "tmh_plan_run": (INT, [U64]),
     "tmh_plan_destroy": (INT, [U64]),
     "tmh_plan_describe": (INT, [U64, ctypes.c_char_p, U32]),
+    "tmh_plan_set_mode": (INT, [U64, U32]),
     "tmh_rmsnorm": (INT, [U64, U32, U64, U32, U32, F32, U64]),
     "tmh_rope_write": (INT, [U64, U32, U32, U32, U32, U32, U64, U64, U32, U64, U32, U32, U64, U64, U64]),
     "tmh_attention": (INT, [U64, U32, U32, U32, U64, U64, U32, U32, U32, U32, U64, F32, U64, U32]),
@@ -175,6 +176,7 @@ SIGNATURES = {
     "tmh_llama_length": (INT, [U64, U32, ctypes.POINTER(I32)]),
     "tmh_llama_reset": (INT, [U64, U32]),
     "tmh_llama_step": (INT, [U64, U32]),
+    "tmh_llama_set_mode": (INT, [U64, U32]),
     "tmh_llama_destroy": (INT, [U64]),
     "tmh_gguf_open": (INT, [ctypes.c_char_p, ctypes.POINTER(U64)]),
     "tmh_gguf_close": (INT, [U64]),
@@ -279,6 +281,10 @@ class Plan:
 
     def run(self) -> None:
         check("tmh_plan_run", self.device.lib.tmh_plan_run(self.handle))
+
+    def set_mode(self, mode: str) -> None:
+        """BlockMatMulMode of the plan's launch: "auto" (the host's bits) or "unordered" (measurement only)."""
+        check("tmh_plan_set_mode", self.device.lib.tmh_plan_set_mode(self.handle, MODES[mode]))
 
     def describe(self) -> str:
         """The plan's launch: kernel, grid, LDS."""
@@ -703,6 +709,10 @@ class HIPLlama:
         self.device.check_synced("tmh_llama_generate", self.device.lib.tmh_llama_generate(
             self.handle, steps, out.ctypes.data, 1 if graph else 0))
         return out
+
+    def set_mode(self, mode: str) -> None:
+        """BlockMatMulMode of the decoder's products: "auto" (the host's bits) or "unordered" (measurement only)."""
+        check("tmh_llama_set_mode", self.device.lib.tmh_llama_set_mode(self.handle, MODES[mode]))
 
     def step(self, graph: bool = True) -> None:
         check("tmh_llama_step", self.device.lib.tmh_llama_step(self.handle, 1 if graph else 0))

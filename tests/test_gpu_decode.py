@@ -331,6 +331,42 @@ def test_decoder_nan_at_a_lane_start(dev, kind, rows):
         assert list(tokens[r]) == oracle.Llama(config, weights).generate(p, 10), r
 
 
+@pytest.mark.parametrize("rows", [1, 8])
+def test_decoder_unordered_mode(dev, rows):
+    # tmh_llama_set_mode(UNORDERED): the decoder's products fold in their own
+    # order (a measurement mode). A last-bit change in one product can move
+    # an activation by a quantisation step in the next, so after two layers
+    # the logits are close to the host's as a whole (relative L2 under 2%;
+    # the reference's spec allows 1e-2 a product in this mode,
+    # block_matmul_spec.cr:152-158), not bit for bit; back in AUTO (a fresh
+    # capture of the step graph), the CPU's bits and tokens again.
+    config = dict(SMOLLM2_1P7B, layers=2, context=64)
+    weights = random_block_llama(config, seed=60 + rows)
+    rng = np.random.default_rng(61)
+    prompts = [list(rng.integers(0, config["vocab"], 12)) for _ in range(rows)]
+    cpu = oracle.Llama(config, weights)
+    want = cpu.forward(prompts[0], last_only=True)
+    gpu = th.HIPLlama(dev, config, weights, rows=rows, capacity=64, max_tokens=16)
+    gpu.set_mode("unordered")
+    for r, p in enumerate(prompts):
+        got = gpu.forward(p, row=r, last_only=True)
+        if r == 0:
+            rel = float(np.linalg.norm((got - want).astype(np.float64)) / np.linalg.norm(want.astype(np.float64)))
+            say("unordered decoder rel L2", rel)
+            assert rel < 2e-2
+            assert not np.array_equal(bits(got), bits(want))
+    gpu.generate(4, graph=True)  # a step graph captured in UNORDERED
+    gpu.set_mode("auto")
+    gpu.reset()
+    for r, p in enumerate(prompts):
+        got = gpu.forward(p, row=r, last_only=True)
+        if r == 0:
+            assert np.array_equal(bits(got), bits(want))
+    tokens = gpu.generate(6, graph=True)
+    for r, p in enumerate(prompts):
+        assert list(tokens[r]) == oracle.Llama(config, weights).generate(p, 6), r
+
+
 def test_batch_rows_decode_matches_each_sequence(dev):
     # rows of different prompt lengths decoded together: each row's tokens
     # are those of its sequence alone (a row alone == in a batch).
