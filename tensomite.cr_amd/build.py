@@ -11,6 +11,13 @@ Flags that the results depend on:
                           MFMA results in VGPRs, not AGPRs: the matrix-core
                           kernels read every result with VALU operations,
                           and an AGPR would cost a v_accvgpr_read each
+  -mllvm -amdgpu-kernarg-preload-count=16
+                          the first kernel arguments arrive in SGPRs when a
+                          wave starts (gfx950 kernarg preloading) instead of
+                          through a scalar load: the decode kernels are chains
+                          of latencies from their first instruction (measured,
+                          one box, alternating builds: 1.7B decode batch 1
+                          831 -> 806 us/step, config 2 15.56 -> 15.33 us)
 """
 from __future__ import annotations
 
@@ -34,6 +41,7 @@ FLAGS = [
     "-fno-gpu-rdc",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
     "-I", os.path.join(ROOT, "include"),
