@@ -472,6 +472,23 @@ __device__ __forceinline__ void wait_vm_lds_upto(uint32_t n) {
     }
 }
 
+// wait_vm_lds<n> for a runtime n in [LO, HI] (n past HI waits for HI),
+// chosen by halving the range: log2 of its width uniform branches rather
+// than one compare per value above n (the stage loops of the matrix-core
+// kernels wait once a stage).
+template <uint32_t LO, uint32_t HI>
+__device__ __forceinline__ void wait_vm_lds_in(uint32_t n) {
+    if constexpr (LO == HI) {
+        wait_vm_lds<LO>();
+    } else {
+        constexpr uint32_t MID = (LO + HI + 1u) / 2u;
+        if (n >= MID)
+            wait_vm_lds_in<MID, HI>(n);
+        else
+            wait_vm_lds_in<LO, MID - 1u>(n);
+    }
+}
+
 // A workgroup barrier after this wave's LDS (and scalar memory) operations,
 // leaving its direct loads in flight: __syncthreads() would wait for them.
 // The empty asm statements keep the compiler from moving memory operations

@@ -2016,7 +2016,7 @@ __global__ __launch_bounds__(MX_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     };
     auto barrier = [&](uint32_t outstanding) {
         asm volatile("" ::: "memory");
-        wait_vm_lds_upto<16>(outstanding);
+        wait_vm_lds_in<0u, 16u>(outstanding);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -2252,7 +2252,7 @@ __global__ __launch_bounds__(FEW_THREADS) void k_matmul_few(const uint8_t* __res
     };
     auto barrier = [&](uint32_t outstanding) {
         asm volatile("" ::: "memory");
-        wait_vm_lds_upto<32>(outstanding);
+        wait_vm_lds_in<0u, 32u>(outstanding);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
