@@ -22,7 +22,7 @@ BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
 
 
 def build() -> None:
-    """Compiles the three oracle builds (portable, x86-64-v3, x86-64-v4)."""
+    """Compiles the four oracle builds (portable, x86-64-v3, x86-64-v4, x86-64-v4 with VNNI)."""
     subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
 
 
@@ -37,11 +37,20 @@ def _cpu_flags() -> set:
     return set()
 
 
+def variant_runs(variant: str) -> bool:
+    """Whether the host CPU can run an oracle build."""
+    flags = _cpu_flags()
+    v4 = {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd"} <= flags
+    return {"portable": True, "v3": {"avx2", "fma", "bmi2", "f16c", "movbe"} <= flags, "v4": v4,
+            "vnni": v4 and "avx512_vnni" in flags}[variant]
+
+
 def best_variant() -> str:
-    """The widest oracle build the host CPU can run: v4 (AVX-512), v3 (AVX2) or portable."""
+    """The widest oracle build the host CPU can run: vnni (AVX-512 with VNNI), v4 (AVX-512), v3 (AVX2) or
+    portable."""
     flags = _cpu_flags()
     if {"avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd"} <= flags:
-        return "v4"
+        return "vnni" if "avx512_vnni" in flags else "v4"
     if {"avx2", "fma", "bmi2", "f16c", "movbe"} <= flags:
         return "v3"
     return "portable"
@@ -53,7 +62,8 @@ _LIBS: dict = {}
 def lib(variant: str = "portable") -> ctypes.CDLL:
     if variant in _LIBS:
         return _LIBS[variant]
-    name = {"portable": "libtmq_oracle.so", "v3": "libtmq_oracle_v3.so", "v4": "libtmq_oracle_v4.so"}[variant]
+    name = {"portable": "libtmq_oracle.so", "v3": "libtmq_oracle_v3.so", "v4": "libtmq_oracle_v4.so",
+            "vnni": "libtmq_oracle_vnni.so"}[variant]
     path = os.path.join(HERE, name)
     if not os.path.exists(path):
         build()

@@ -33,6 +33,10 @@
 #include <string.h>
 #include <time.h>
 #include <unistd.h>
+#if defined(__AVX512VNNI__) && defined(__AVX512VL__) && defined(__AVX512BW__)
+#include <immintrin.h>
+#define TMO_VNNI 1
+#endif
 
 /* Block kinds, numbered as the reference's GPU kernels number them
  * (src/tensomite/cuda.cr:774-781). */
@@ -358,6 +362,33 @@ static void build_halves(void) {
 }
 static inline float fast_half(const uint8_t* at) { return HALVES[at[0] | (at[1] << 8)]; }
 
+#ifdef TMO_VNNI
+/* The integer block dots of the fast path on AVX-512 VNNI (the vnni build):
+ * vpdpbusd multiplies unsigned bytes by signed ones and sums them in 32-bit
+ * lanes without saturation, so each dot is the exact integer the scalar
+ * loops give (integer sums are exact in any order); the f32 arithmetic
+ * around them is unchanged. */
+static inline int32_t hsum8(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4e));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xb1));
+    return _mm_cvtsi128_si32(s);
+}
+
+/* Σ u·y over a block of 32 (u unsigned bytes, y signed). */
+static inline int32_t udot32(__m256i u, __m256i y) {
+    return hsum8(_mm256_dpbusd_epi32(_mm256_setzero_si256(), u, y));
+}
+
+/* A Q4 block's 16 bytes of nibbles as 32 unsigned bytes in value order:
+ * values 0-15 the low nibbles, 16-31 the high ones (quant.cr:62-69). */
+static inline __m256i nibbles32(const uint8_t* p) {
+    const __m128i b = _mm_loadu_si128((const __m128i*)p);
+    const __m128i m = _mm_set1_epi8(0x0f);
+    return _mm256_set_m128i(_mm_and_si128(_mm_srli_epi16(b, 4), m), _mm_and_si128(b, m));
+}
+#endif
+
 /* fast_q8_0, quant.cr:349-366: two weight rows share each activation pass. */
 static void fast_q8_0(const uint8_t* w0, const uint8_t* w1, const float* sp, const int8_t* qp, int32_t blocks,
                       float* out0, float* out1) {
@@ -365,15 +396,26 @@ static void fast_q8_0(const uint8_t* w0, const uint8_t* w1, const float* sp, con
     for (int32_t block = 0; block < blocks; block++) {
         const uint8_t* base0 = w0 + block * 34;
         const uint8_t* base1 = w1 + block * 34;
-        const int8_t* v0 = (const int8_t*)(base0 + 2);
-        const int8_t* v1 = (const int8_t*)(base1 + 2);
         const int8_t* qb = qp + block * 32;
         int32_t total0 = 0, total1 = 0;
+#ifdef TMO_VNNI
+        {
+            /* Σ v·y = Σ (v + 128)·y − 128·Σy, v + 128 as an unsigned byte */
+            const __m256i y = _mm256_loadu_si256((const __m256i*)qb);
+            const __m256i flip = _mm256_set1_epi8((char)0x80);
+            const int32_t bias = udot32(flip, y);
+            total0 = udot32(_mm256_xor_si256(_mm256_loadu_si256((const __m256i*)(base0 + 2)), flip), y) - bias;
+            total1 = udot32(_mm256_xor_si256(_mm256_loadu_si256((const __m256i*)(base1 + 2)), flip), y) - bias;
+        }
+#else
+        const int8_t* v0 = (const int8_t*)(base0 + 2);
+        const int8_t* v1 = (const int8_t*)(base1 + 2);
         for (int j = 0; j < 32; j++) {
             int32_t y = qb[j];
             total0 += v0[j] * y;
             total1 += v1[j] * y;
         }
+#endif
         float s0 = fast_half(base0) * sp[block];
         float s1 = fast_half(base1) * sp[block];
         sum0 += (float)total0 * s0;
@@ -385,6 +427,14 @@ static void fast_q8_0(const uint8_t* w0, const uint8_t* w1, const float* sp, con
 
 /* nibble_dot, quant.cr:373-386: nibbles less 8 as signed bytes. */
 static inline void nibble_dot(const uint8_t* p0, const uint8_t* p1, const int8_t* qb, int32_t* t0, int32_t* t1) {
+#ifdef TMO_VNNI
+    /* Σ (q − 8)·y = Σ q·y − 8·Σy */
+    const __m256i y = _mm256_loadu_si256((const __m256i*)qb);
+    const int32_t eight = udot32(_mm256_set1_epi8(8), y);
+    *t0 = udot32(nibbles32(p0), y) - eight;
+    *t1 = udot32(nibbles32(p1), y) - eight;
+    return;
+#endif
     int32_t total0 = 0, total1 = 0;
     for (int j = 0; j < 16; j++) {
         int32_t y = qb[j];

@@ -247,11 +247,16 @@ def test_fold_starts_from_plus_zero():
         assert np.all(got.view(np.uint32) == 0), fn
 
 
+VARIANTS = [v for v in ("portable", "v3", "v4", "vnni") if oracle.variant_runs(v)]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
 @pytest.mark.parametrize("fmt", FORMATS)
-def test_fast_path_equals_reference_bit_for_bit(fmt):
+def test_fast_path_equals_reference_bit_for_bit(fmt, variant):
     # quant_spec.cr:30-48: shapes {1,37,64}, {3,5,1280}, {2,9,4096}, with a
     # zero first block, a spike of 50, a zero activation block and the
-    # [127, j - 15.5] row.
+    # [127, j - 15.5] row; on every build the host runs (the vnni build
+    # computes the block dots with vpdpbusd).
     rng = np.random.default_rng(11)
     for count, n, k in ((1, 37, 64), (3, 5, 1280), (2, 9, 4096)):
         values = rng.uniform(-2.0, 2.0, n * k).astype(np.float32)
@@ -263,9 +268,34 @@ def test_fast_path_equals_reference_bit_for_bit(fmt):
         if count > 2:
             x[2 * k:2 * k + 32] = [127.0 if j == 0 else j - 15.5 for j in range(32)]
         wq = oracle.quantize(fmt, values)
-        fast = oracle.matmul(fmt, x, wq, count, n, k)
+        fast = oracle.matmul(fmt, x, wq, count, n, k, variant)
         ref = oracle.matmul_reference(fmt, x, wq, count, n, k)
         assert np.array_equal(fast.view(np.uint32), ref.view(np.uint32)), (count, n, k)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_fast_path_on_every_byte_value(fmt, variant):
+    # Raw weight bytes over the whole byte range (Q8_0 values down to -128,
+    # every nibble) under finite half scales, and activations with the
+    # extreme +-127 and 0: the fast path's integer dots against the
+    # reference's, bit for bit.
+    rng = np.random.default_rng(21)
+    count, n, k = 3, 19, 1024
+    blocks = n * k // 32
+    size = oracle.row_bytes(fmt, k) // (k // 32)
+    raw = rng.integers(0, 256, (blocks, size), dtype=np.uint8)
+    halves = rng.uniform(-4.0, 4.0, (blocks, 2)).astype(np.float16).view(np.uint8).reshape(blocks, 4)
+    raw[:, :2] = halves[:, :2]
+    if fmt == "Q4_1":
+        raw[:, 2:4] = halves[:, 2:]
+    x = rng.uniform(-3.0, 3.0, count * k).astype(np.float32)
+    x[:32] = [127.0 if j % 2 else -127.0 for j in range(32)]
+    x[k:k + 64] = 0
+    wq = raw.reshape(-1)
+    fast = oracle.matmul(fmt, x, wq, count, n, k, variant)
+    ref = oracle.matmul_reference(fmt, x, wq, count, n, k)
+    assert np.array_equal(fast.view(np.uint32), ref.view(np.uint32))
 
 
 def test_same_bits_on_any_number_of_threads():
