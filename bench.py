@@ -724,6 +724,79 @@ def config3(dev, warmup, cpu_seconds=None):
     return out
 
 
+# ---------------------------------------------------------------- heads
+
+HEADS = (("135m", 49152, 576), ("1p7b", 49152, 2048))
+
+
+def heads(dev, warmup, cpu_seconds=None):
+    """The two tied heads as single one-row Q4_0 products (W ~ N(0, 0.02)
+    quantised, seed 0x5EED0006 + k; x ~ N(0, 1)): SmolLM2-135M's [49152, 576]
+    (15.9 MB) and the 1.7B shape's [49152, 2048] (56.6 MB), the largest
+    single products of configs 2 and 5. Two routes each: one
+    tmh_block_matmul call in AUTO mode, and a plan of that one product (the
+    streamed kernel). Calls rotate through >= 512 MB of weight copies; HIP
+    events every 20 calls, the median over 100 groups. Bytes a call:
+    weights + 4·K of x + 4·N of y. Both routes' output bits are checked
+    against the oracle; with cpu_seconds, the oracle's Quant.matmul
+    restatement is timed on the same product (portable and native builds,
+    every host core)."""
+    import quant_host
+    from oracle import oracle
+
+    host = host_cpu()
+    variants = list(dict.fromkeys(["portable", oracle.best_variant()]))
+    out = {"workload": "the tied heads as single one-row Q4_0 products: [49152, 576] (SmolLM2-135M, 15.9 MB) and "
+                       "[49152, 2048] (1.7B shape, 56.6 MB)", "unit": "GB/s", "points": {}}
+    rng = np.random.default_rng(0x5EED0006)
+    for name, n, k in HEADS:
+        wq = quant_host.synthetic_weights("Q4_0", n, k, seed=0x5EED0006 + k)
+        xh = rng.standard_normal(k, dtype=np.float32)
+        copies = max(2, math.ceil(2 * MALL_BYTES / wq.nbytes))
+        first = dev.from_array(wq)
+        ws = [first] + [dev.alloc(wq.nbytes) for _ in range(copies - 1)]
+        for w in ws[1:]:
+            dev.copy(w, first, wq.nbytes)
+        x = dev.from_array(xh)
+        dst = dev.alloc(4 * n)
+        nbytes = wq.nbytes + 4 * k + 4 * n
+        want = oracle.matmul("Q4_0", xh, wq, 1, n, k, oracle.best_variant())[0]
+        point = {"n": n, "k": k, "weight_bytes": int(wq.nbytes), "algorithmic_bytes": nbytes,
+                 "weight_copies_rotated": copies}
+        plans = [dev.plan("Q4_0", [(w, 0, x, dst, None, n, k)]) for w in ws]
+        routes = (("auto", lambda i: dev.block_matmul("Q4_0", ws[i % copies], x, 1, n, k, dst=dst)),
+                  ("plan", lambda i: plans[i % copies].run()))
+        for route, call in routes:
+            warm_up(dev, call, warmup)
+            per, _ = time_launches(dev, call, ROOFLINE_GROUPS * GROUP, GROUP)
+            st = launch_stats(per, nbytes, GROUP)
+            got = dev.to_array(dst, np.float32, n)
+            point[route] = {"us_per_call_median": st["median_us"], "us_per_call_mean": st["mean_us"],
+                            "roofline": {"bound": "hbm", "achieved": st["GB_per_s_median"], "peak": HBM_PEAK_GBS,
+                                         "unit": "GB/s", "frac": round(st["GB_per_s_median"] / HBM_PEAK_GBS, 4)},
+                            "bit_exact_vs_oracle": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))}
+        point["auto"]["route"] = "tmh_block_matmul, AUTO"
+        point["plan"]["route"] = plans[0].describe()
+        if cpu_seconds:
+            builds = {}
+            for variant in variants:
+                sec, calls, _ = cpu_rate("Q4_0", xh, wq, 1, n, k, cpu_seconds, variant, host["cores"])
+                builds[variant] = {"GB_per_s": round(nbytes / sec / 1e9, 2), "us_per_call": round(sec * 1e6, 1),
+                                   "calls": calls}
+            best = max(builds, key=lambda v: builds[v]["GB_per_s"])
+            point["cpu_baseline"] = {"value": builds[best]["GB_per_s"], "unit": "GB/s", "cores": host["cores"],
+                                     "kind": "port", "build": best, "builds": builds,
+                                     "sample": f"the product repeated for ~{cpu_seconds:g} s per build"}
+        out["points"][name] = point
+        for plan in plans:
+            plan.destroy()
+        for buf in ws + [x, dst]:
+            buf.release()
+    out["bit_exact_vs_oracle"] = all(p[r]["bit_exact_vs_oracle"] for p in out["points"].values()
+                                     for r in ("auto", "plan"))
+    return out
+
+
 # ---------------------------------------------------------------- config 4
 
 def config4(dev, warmup, cpu_seconds=None):
@@ -807,8 +880,8 @@ def config4(dev, warmup, cpu_seconds=None):
 def ceilings(dev, warmup):
     """The box's own ceilings beside the vendor peaks: the HBM read rate of a
     grid-stride read kernel (tmh_debug_read: 16 B a lane a load, four in
-    flight, non-temporal) at 77 MB (config 2's bytes) and 1 GiB, by
-    workgroup count; the device-to-device copy rate (tmh_copy: bytes read +
+    flight, non-temporal) at 15.9 and 56.6 MB (the heads' single products),
+    77 MB (config 2's bytes) and 1 GiB, by workgroup count; the device-to-device copy rate (tmh_copy: bytes read +
     written); each the median over >= 100 launches rotating through >= 512
     MB so the 256 MB Infinity Cache cannot serve them; and what rocminfo
     and amd-smi report of the device."""
@@ -835,7 +908,8 @@ def ceilings(dev, warmup):
             tools[" ".join(cmd)] = [f"unavailable: {e}"]
     out["tools"] = tools
     sink = dev.alloc(4 * 8192)
-    for label, size in (("77MB", 76_857_600 // 16 * 16), ("1GiB", 1 << 30)):
+    sizes = [(f"head_{name}", (q4_0_bytes(n, k) + 4 * k + 4 * n) // 16 * 16) for name, n, k in HEADS]
+    for label, size in sizes + [("77MB", 76_857_600 // 16 * 16), ("1GiB", 1 << 30)]:
         copies = max(2, math.ceil(2 * MALL_BYTES / size))
         bufs = [dev.alloc(size) for _ in range(copies)]  # contents do not matter to a read rate
         dev.sync()
@@ -896,6 +970,9 @@ def main():
                     help="config 4 instead (Q8_0 prefill GEMM on the matrix cores); its own JSON line")
     ap.add_argument("--no-config3", action="store_true", help="skip the config-3 (Q4_1 batched) measurement")
     ap.add_argument("--no-config4", action="store_true", help="skip the config-4 (Q8_0 prefill GEMM) measurement")
+    ap.add_argument("--no-heads", action="store_true", help="skip the single-product head measurement")
+    ap.add_argument("--heads", action="store_true",
+                    help="the two heads as single products instead (AUTO and a one-product plan); its own JSON line")
     ap.add_argument("--cpu-point-seconds", type=float, default=0.4,
                     help="CPU baseline sample per config-3/4 point and build")
     ap.add_argument("--ceilings", action="store_true",
@@ -933,6 +1010,9 @@ def main():
     if args.batched:
         print(json.dumps(config3(dev, args.warmup, cpu_points)), flush=True)
         return
+    if args.heads:
+        print(json.dumps(heads(dev, args.warmup, cpu_points)), flush=True)
+        return
     if args.decode_only:
         print(json.dumps(decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
                                      graph=not args.decode_eager)), flush=True)
@@ -949,6 +1029,9 @@ def main():
     if not args.no_config4:
         log("config 4 ...")
         result["config4"] = config4(dev, args.warmup, cpu_points)
+    if not args.no_heads:
+        log("heads ...")
+        result["heads"] = heads(dev, args.warmup, cpu_points)
     if not args.no_decode:
         log("decode at the 1.7B shape ...")
         result["decode_1p7b"] = decode_1p7b(dev, args.decode_steps, args.cpu_seconds, not args.no_cpu,
