@@ -387,13 +387,67 @@ static inline __m256i nibbles32(const uint8_t* p) {
     const __m128i m = _mm_set1_epi8(0x0f);
     return _mm256_set_m128i(_mm_and_si128(_mm_srli_epi16(b, 4), m), _mm_and_si128(b, m));
 }
+
+/* Eight blocks' 8-lane partial sums reduced together: lane b of the result
+ * is the total of a[b] (three rounds of pairwise horizontal adds, then the
+ * two 128-bit halves; integer sums, exact in any order). */
+static inline __m256i hsum8x8(const __m256i a[8]) {
+    const __m256i s01 = _mm256_hadd_epi32(a[0], a[1]), s23 = _mm256_hadd_epi32(a[2], a[3]);
+    const __m256i s45 = _mm256_hadd_epi32(a[4], a[5]), s67 = _mm256_hadd_epi32(a[6], a[7]);
+    const __m256i s0123 = _mm256_hadd_epi32(s01, s23), s4567 = _mm256_hadd_epi32(s45, s67);
+    return _mm256_add_epi32(_mm256_permute2x128_si256(s0123, s4567, 0x20),
+                            _mm256_permute2x128_si256(s0123, s4567, 0x31));
+}
+
+/* The halves at byte offset `at` of eight consecutive blocks `stride` bytes
+ * apart, as floats (the F16 table, so every half converts as the host's
+ * F16#to_f32 does). */
+static inline __m256 halves8(const uint8_t* at, int stride) {
+    float v[8];
+    for (int b = 0; b < 8; b++) v[b] = fast_half(at + b * stride);
+    return _mm256_loadu_ps(v);
+}
+
+/* Adds eight contributions to a running sum one by one, in block order. */
+static inline float fold8(float sum, __m256 c) {
+    float v[8];
+    _mm256_storeu_ps(v, c);
+    for (int b = 0; b < 8; b++) sum += v[b];
+    return sum;
+}
 #endif
 
 /* fast_q8_0, quant.cr:349-366: two weight rows share each activation pass. */
 static void fast_q8_0(const uint8_t* w0, const uint8_t* w1, const float* sp, const int8_t* qp, int32_t blocks,
                       float* out0, float* out1) {
     float sum0 = 0.0f, sum1 = 0.0f;
-    for (int32_t block = 0; block < blocks; block++) {
+    int32_t block = 0;
+#ifdef TMO_VNNI
+    /* eight blocks at a time: their totals as one vector, each block's
+     * contribution (float(t) · (d · sx), each product rounded) as one
+     * vector operation, then the eight added in block order */
+    for (; block + 8 <= blocks; block += 8) {
+        const __m256i flip = _mm256_set1_epi8((char)0x80), z = _mm256_setzero_si256();
+        __m256i a0[8], a1[8], e[8];
+        for (int b = 0; b < 8; b++) {
+            const __m256i y = _mm256_loadu_si256((const __m256i*)(qp + (block + b) * 32));
+            e[b] = _mm256_dpbusd_epi32(z, flip, y);
+            a0[b] = _mm256_dpbusd_epi32(
+                z, _mm256_xor_si256(_mm256_loadu_si256((const __m256i*)(w0 + (block + b) * 34 + 2)), flip), y);
+            a1[b] = _mm256_dpbusd_epi32(
+                z, _mm256_xor_si256(_mm256_loadu_si256((const __m256i*)(w1 + (block + b) * 34 + 2)), flip), y);
+        }
+        const __m256i bias = hsum8x8(e);
+        const __m256 t0 = _mm256_cvtepi32_ps(_mm256_sub_epi32(hsum8x8(a0), bias));
+        const __m256 t1 = _mm256_cvtepi32_ps(_mm256_sub_epi32(hsum8x8(a1), bias));
+        const __m256 sx = _mm256_loadu_ps(sp + block);
+        const __m256 s0 = _mm256_mul_ps(halves8(w0 + block * 34, 34), sx);
+        const __m256 s1 = _mm256_mul_ps(halves8(w1 + block * 34, 34), sx);
+        sum0 = fold8(sum0, _mm256_mul_ps(t0, s0));
+        sum1 = fold8(sum1, _mm256_mul_ps(t1, s1));
+    }
+#endif
+    for (; block < blocks; block++) {
         const uint8_t* base0 = w0 + block * 34;
         const uint8_t* base1 = w1 + block * 34;
         const int8_t* qb = qp + block * 32;
@@ -454,7 +508,27 @@ static inline void nibble_dot(const uint8_t* p0, const uint8_t* p1, const int8_t
 static void fast_q4_0(const uint8_t* w0, const uint8_t* w1, const float* sp, const int8_t* qp, int32_t blocks,
                       float* out0, float* out1) {
     float sum0 = 0.0f, sum1 = 0.0f;
-    for (int32_t block = 0; block < blocks; block++) {
+    int32_t block = 0;
+#ifdef TMO_VNNI
+    /* eight blocks at a time (as fast_q8_0): (float(t) · d) · sx */
+    for (; block + 8 <= blocks; block += 8) {
+        const __m256i eight = _mm256_set1_epi8(8), z = _mm256_setzero_si256();
+        __m256i a0[8], a1[8], e[8];
+        for (int b = 0; b < 8; b++) {
+            const __m256i y = _mm256_loadu_si256((const __m256i*)(qp + (block + b) * 32));
+            e[b] = _mm256_dpbusd_epi32(z, eight, y);
+            a0[b] = _mm256_dpbusd_epi32(z, nibbles32(w0 + (block + b) * 18 + 2), y);
+            a1[b] = _mm256_dpbusd_epi32(z, nibbles32(w1 + (block + b) * 18 + 2), y);
+        }
+        const __m256i e8 = hsum8x8(e);
+        const __m256 t0 = _mm256_cvtepi32_ps(_mm256_sub_epi32(hsum8x8(a0), e8));
+        const __m256 t1 = _mm256_cvtepi32_ps(_mm256_sub_epi32(hsum8x8(a1), e8));
+        const __m256 sx = _mm256_loadu_ps(sp + block);
+        sum0 = fold8(sum0, _mm256_mul_ps(_mm256_mul_ps(t0, halves8(w0 + block * 18, 18)), sx));
+        sum1 = fold8(sum1, _mm256_mul_ps(_mm256_mul_ps(t1, halves8(w1 + block * 18, 18)), sx));
+    }
+#endif
+    for (; block < blocks; block++) {
         const uint8_t* base0 = w0 + block * 18;
         const uint8_t* base1 = w1 + block * 18;
         int32_t total0, total1;
@@ -472,7 +546,33 @@ static void fast_q4_0(const uint8_t* w0, const uint8_t* w1, const float* sp, con
 static void fast_q4_1(const uint8_t* w0, const uint8_t* w1, const float* sp, const float* mp, const int32_t* tp,
                       const int8_t* qp, int32_t blocks, float* out0, float* out1) {
     float sum0 = 0.0f, sum1 = 0.0f;
-    for (int32_t block = 0; block < blocks; block++) {
+    int32_t block = 0;
+#ifdef TMO_VNNI
+    /* eight blocks at a time (as fast_q8_0): (d · sx) · float(dot + 8·Σq)
+     * + m · mx */
+    for (; block + 8 <= blocks; block += 8) {
+        const __m256i eight = _mm256_set1_epi8(8), z = _mm256_setzero_si256();
+        __m256i a0[8], a1[8], e[8];
+        for (int b = 0; b < 8; b++) {
+            const __m256i y = _mm256_loadu_si256((const __m256i*)(qp + (block + b) * 32));
+            e[b] = _mm256_dpbusd_epi32(z, eight, y);
+            a0[b] = _mm256_dpbusd_epi32(z, nibbles32(w0 + (block + b) * 20 + 4), y);
+            a1[b] = _mm256_dpbusd_epi32(z, nibbles32(w1 + (block + b) * 20 + 4), y);
+        }
+        const __m256i e8 = hsum8x8(e);
+        const __m256i shift = _mm256_slli_epi32(_mm256_loadu_si256((const __m256i*)(tp + block)), 3);
+        const __m256 t0 = _mm256_cvtepi32_ps(_mm256_add_epi32(_mm256_sub_epi32(hsum8x8(a0), e8), shift));
+        const __m256 t1 = _mm256_cvtepi32_ps(_mm256_add_epi32(_mm256_sub_epi32(hsum8x8(a1), e8), shift));
+        const __m256 sx = _mm256_loadu_ps(sp + block), mx = _mm256_loadu_ps(mp + block);
+        const __m256 c0 = _mm256_add_ps(_mm256_mul_ps(_mm256_mul_ps(halves8(w0 + block * 20, 20), sx), t0),
+                                        _mm256_mul_ps(halves8(w0 + block * 20 + 2, 20), mx));
+        const __m256 c1 = _mm256_add_ps(_mm256_mul_ps(_mm256_mul_ps(halves8(w1 + block * 20, 20), sx), t1),
+                                        _mm256_mul_ps(halves8(w1 + block * 20 + 2, 20), mx));
+        sum0 = fold8(sum0, c0);
+        sum1 = fold8(sum1, c1);
+    }
+#endif
+    for (; block < blocks; block++) {
         const uint8_t* base0 = w0 + block * 20;
         const uint8_t* base1 = w1 + block * 20;
         int32_t dot0, dot1;
