@@ -38,6 +38,7 @@
 int tmo_block_bytes(int kind);
 int tmo_matmul(int kind, const float* x, const uint8_t* w, int32_t rows, int32_t n, int32_t k, float* dst);
 int tmo_dequantize(int kind, const uint8_t* bytes, int64_t count, float* values);
+void tmo_parallel_for(int32_t count, void (*fn)(void*, int32_t, int32_t), void* ctx);
 
 /* ------------------------------------------------------------ Maths.exp */
 
@@ -195,6 +196,49 @@ int32_t tmo_llama_length(const tmo_llama* m) { return m->length; }
 const float* tmo_llama_cos(const tmo_llama* m) { return m->cos; }
 const float* tmo_llama_sin(const tmo_llama* m) { return m->sin; }
 
+typedef struct {
+    const float *q, *keys, *values;
+    int32_t heads, kv_heads, capacity, width;
+    const int32_t* table;
+    float scale;
+    float* out;
+} attention_job;
+
+/* Items first .. stop - 1 (item = token · heads + head), each with its own
+ * scores. */
+static void attention_items(void* arg, int32_t first, int32_t stop) {
+    const attention_job* j = arg;
+    const int32_t group = j->heads / j->kv_heads, width = j->width;
+    float* scores = malloc(sizeof(float) * (size_t)j->capacity);
+    for (int32_t item = first; item < stop; item++) {
+        const int32_t t = item / j->heads, h = item - t * j->heads;
+        const int32_t row = j->table[3 * t], last = j->table[3 * t + 1], positions = j->table[3 * t + 2];
+        const int32_t kv = h / group;
+        const float* kh = j->keys + ((size_t)row * j->kv_heads + kv) * j->capacity * width;
+        const float* vh = j->values + ((size_t)row * j->kv_heads + kv) * j->capacity * width;
+        const float* qi = j->q + ((size_t)t * j->heads + h) * width;
+        float top = 0.0f;
+        for (int32_t p = 0; p < positions; p++) {
+            float dot = 0.0f;
+            for (int32_t col = 0; col < width; col++) dot += qi[col] * kh[(size_t)p * width + col];
+            float x = dot * j->scale;
+            float mask = p > last ? -INFINITY : 0.0f;
+            x = x + mask;
+            scores[p] = x;
+            if (p == 0 || x > top) top = x;
+        }
+        float total = 0.0f;
+        for (int32_t p = 0; p < positions; p++) total += (scores[p] = tmo_exp(scores[p] - top));
+        float* oi = j->out + ((size_t)t * j->heads + h) * width;
+        for (int32_t col = 0; col < width; col++) {
+            float acc = 0.0f;
+            for (int32_t p = 0; p < positions; p++) acc += scores[p] / total * vh[(size_t)p * width + col];
+            oi[col] = acc;
+        }
+    }
+    free(scores);
+}
+
 /* The Attention op on a host device, host.cr:408-440, for `tokens` packed
  * query rows q [tokens, heads, width] against caches [rows, kv_heads,
  * capacity, width]: token t reads cache row table[3t] up to table[3t+2]
@@ -202,39 +246,14 @@ const float* tmo_llama_sin(const tmo_llama* m) { return m->sin; }
  * composite.cr:282-290). Per head h (kv head h / group): scores[p] = (q · k_p)
  * in column order, · scale, + mask (-inf past the last seen position), top =
  * the first highest, e_p = Maths.exp(scores[p] - top), total in position
- * order, out[c] = Σ_p (e_p / total) · v_p[c] in position order. */
+ * order, out[c] = Σ_p (e_p / total) · v_p[c] in position order. The
+ * reference walks the (token, head) items on one thread; here they run on
+ * the spinning pool, each item's arithmetic the same sequence, so the bits
+ * are the same. */
 void tmo_attention(const float* q, int32_t tokens, int32_t heads, const float* keys, const float* values,
                    int32_t kv_heads, int32_t capacity, int32_t width, const int32_t* table, float scale, float* out) {
-    int32_t group = heads / kv_heads;
-    float* scores = malloc(sizeof(float) * (size_t)capacity);
-    for (int32_t t = 0; t < tokens; t++) {
-        int32_t row = table[3 * t], last = table[3 * t + 1], positions = table[3 * t + 2];
-        for (int32_t h = 0; h < heads; h++) {
-            int32_t kv = h / group;
-            const float* kh = keys + ((size_t)row * kv_heads + kv) * capacity * width;
-            const float* vh = values + ((size_t)row * kv_heads + kv) * capacity * width;
-            const float* qi = q + ((size_t)t * heads + h) * width;
-            float top = 0.0f;
-            for (int32_t p = 0; p < positions; p++) {
-                float dot = 0.0f;
-                for (int32_t col = 0; col < width; col++) dot += qi[col] * kh[(size_t)p * width + col];
-                float x = dot * scale;
-                float mask = p > last ? -INFINITY : 0.0f;
-                x = x + mask;
-                scores[p] = x;
-                if (p == 0 || x > top) top = x;
-            }
-            float total = 0.0f;
-            for (int32_t p = 0; p < positions; p++) total += (scores[p] = tmo_exp(scores[p] - top));
-            float* oi = out + ((size_t)t * heads + h) * width;
-            for (int32_t col = 0; col < width; col++) {
-                float acc = 0.0f;
-                for (int32_t p = 0; p < positions; p++) acc += scores[p] / total * vh[(size_t)p * width + col];
-                oi[col] = acc;
-            }
-        }
-    }
-    free(scores);
+    attention_job j = {q, keys, values, heads, kv_heads, capacity, width, table, scale, out};
+    tmo_parallel_for(tokens * heads, attention_items, &j);
 }
 
 /* The Rope op, host.cr:448-466, on `heads` heads of `width` per token (token

@@ -601,10 +601,17 @@ typedef struct {
     const int32_t* totals;
     const int8_t* qs;
     float* out;
+    /* set for tmo_parallel_for's jobs instead of a product */
+    void (*fn)(void* ctx, int32_t first, int32_t stop);
+    void* ctx;
 } tmo_job;
 
 /* One span of a product: columns first...stop in pairs, quant.cr:167-180. */
 static void run_span(const tmo_job* job, int32_t first, int32_t stop) {
+    if (job->fn) {
+        job->fn(job->ctx, first, stop);
+        return;
+    }
     for (int32_t col = first; col < stop; col += 2) {
         const uint8_t* w0 = job->w + col * job->row_bytes;
         const uint8_t* w1 = col + 1 < stop ? w0 + job->row_bytes : w0;
@@ -726,6 +733,28 @@ static void in_parallel(int32_t count, int64_t bytes, const tmo_job* job) {
     pthread_mutex_lock(&pool_lock);
     if (pool == NULL) pool = pool_new(threads - 1);
     pool_run(pool, (int32_t)spans, count, job);
+    pthread_mutex_unlock(&pool_lock);
+}
+
+/* fn(ctx, first, stop) over spans of items 0 .. count - 1 on the spinning
+ * pool (at most tmo_threads()·4 spans): for host ops whose items are
+ * independent, each computed by one thread in its own order. */
+void tmo_parallel_for(int32_t count, void (*fn)(void*, int32_t, int32_t), void* ctx) {
+    int threads = tmo_threads();
+    int64_t spans = (int64_t)threads * 4;
+    if (count < spans) spans = count;
+    if (spans > 65535) spans = 65535;
+    if (spans <= 1 || threads <= 1) {
+        if (count > 0) fn(ctx, 0, count);
+        return;
+    }
+    tmo_job job;
+    memset(&job, 0, sizeof job);
+    job.fn = fn;
+    job.ctx = ctx;
+    pthread_mutex_lock(&pool_lock);
+    if (pool == NULL) pool = pool_new(threads - 1);
+    pool_run(pool, (int32_t)spans, count, &job);
     pthread_mutex_unlock(&pool_lock);
 }
 
