@@ -137,6 +137,23 @@ void tmo_swiglu_many(const float* gate, const float* value, int64_t count, float
     for (int64_t i = 0; i < count; i++) out[i] = swiglu(gate[i], value[i]);
 }
 
+/* SwiGLU of each row's gate and up halves (rows of 2·hidden), a[r, j] =
+ * swiglu(gu[r, j], gu[r, hidden + j]), in spans of elements on the
+ * spinning pool (elementwise, so any split gives the same bits). */
+typedef struct {
+    const float* gu;
+    float* a;
+    int32_t hidden;
+} swiglu_job;
+
+static void swiglu_items(void* arg, int32_t first, int32_t stop) {
+    const swiglu_job* j = arg;
+    for (int32_t e = first; e < stop; e++) {
+        const int32_t r = e / j->hidden, c = e - r * j->hidden;
+        j->a[e] = swiglu(j->gu[(size_t)r * 2 * j->hidden + c], j->gu[(size_t)r * 2 * j->hidden + j->hidden + c]);
+    }
+}
+
 /* ------------------------------------------------------------ the model */
 
 typedef struct {
@@ -317,9 +334,8 @@ int tmo_llama_forward(tmo_llama* m, const int32_t* ids, int32_t count, int32_t l
         for (int64_t j = 0; j < (int64_t)count * W; j++) x[j] = x[j] + o[j];
         tmo_rmsnorm(x, m->w.ffn_norm[layer], count, W, c->eps, h);
         tmo_matmul(c->kind, h, m->w.gate_up[layer], count, 2 * H, W, gu);
-        for (int32_t i = 0; i < count; i++)
-            for (int32_t j = 0; j < H; j++)
-                a[(size_t)i * H + j] = swiglu(gu[(size_t)i * 2 * H + j], gu[(size_t)i * 2 * H + H + j]);
+        swiglu_job sj = {gu, a, H};
+        tmo_parallel_for(count * H, swiglu_items, &sj);
         tmo_matmul(c->kind, a, m->w.down[layer], count, W, H, o);
         for (int64_t j = 0; j < (int64_t)count * W; j++) x[j] = x[j] + o[j];
     }
