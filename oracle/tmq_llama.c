@@ -68,7 +68,7 @@ float tmo_exp(float x) {
     p = p * r + 5.0000001201e-1f;
     p = p * z + r;
     p = p + 1.0f;
-    int32_t whole = (int32_t)n;
+    int32_t whole = isnan(n) ? INT32_MIN : (int32_t)n; /* n is clamped: only NaN is out of range */
     int32_t half = whole >> 1;
     float result = p * bits_float((uint32_t)(half + 127) << 23);
     result = result * bits_float((uint32_t)(whole - half + 127) << 23);

@@ -100,6 +100,14 @@ static void write_half(uint8_t* at, float value) {
     at[1] = (uint8_t)(bits >> 8);
 }
 
+/* Crystal's unchecked Float32#to_i32! / #to_i8! (LLVM fptosi, which x86-64
+ * carries out as cvttss2si): truncation toward zero, and for NaN or a value
+ * outside Int32's range the "integer indefinite" INT32_MIN, whose low byte
+ * (what to_i8! keeps) is 0. Written out so that C defines those cases. */
+static inline int32_t unchecked_i32(float v) {
+    return v >= -2147483648.0f && v < 2147483648.0f ? (int32_t)v : INT32_MIN;
+}
+
 /* ------------------------------------------------------ weight quantisers */
 
 /* quantize_q8_0, quant.cr:499-505 */
@@ -110,7 +118,7 @@ static void quantize_q8_0(const float* x, uint8_t* target) {
     float d = amax / 127.0f;
     float id = d == 0 ? 0.0f : 1.0f / d;
     write_half(target, d);
-    for (int j = 0; j < 32; j++) target[2 + j] = (uint8_t)(int8_t)(int)roundf(x[j] * id);
+    for (int j = 0; j < 32; j++) target[2 + j] = (uint8_t)(int8_t)unchecked_i32(roundf(x[j] * id));
 }
 
 /* quantize_q4_0, quant.cr:509-520: the first value of largest magnitude,
@@ -127,7 +135,7 @@ static void quantize_q4_0(const float* x, uint8_t* target) {
         lo_v = lo_v + 8.5f;
         float hi_v = x[j + 16] * id;
         hi_v = hi_v + 8.5f;
-        int8_t lo = (int8_t)lo_v, hi = (int8_t)hi_v;
+        int8_t lo = (int8_t)unchecked_i32(lo_v), hi = (int8_t)unchecked_i32(hi_v);
         if (lo > 15) lo = 15;
         if (hi > 15) hi = 15;
         target[2 + j] = (uint8_t)((uint8_t)lo | (uint8_t)((uint8_t)hi << 4));
@@ -151,7 +159,7 @@ static void quantize_q4_1(const float* x, uint8_t* target) {
         lo_v = lo_v + 0.5f;
         float hi_v = (x[j + 16] - mn) * id;
         hi_v = hi_v + 0.5f;
-        int8_t lo = (int8_t)lo_v, hi = (int8_t)hi_v;
+        int8_t lo = (int8_t)unchecked_i32(lo_v), hi = (int8_t)unchecked_i32(hi_v);
         if (lo > 15) lo = 15;
         if (hi > 15) hi = 15;
         target[4 + j] = (uint8_t)((uint8_t)lo | (uint8_t)((uint8_t)hi << 4));
@@ -230,7 +238,7 @@ void tmo_quantize_activations(const float* x, int32_t k, float* scales, float* s
         float id = d == 0 ? 0.0f : 1.0f / d;
         int32_t total = 0;
         for (int j = 0; j < 32; j++) {
-            int8_t q = (int8_t)(int)roundf(values[j] * id);
+            int8_t q = (int8_t)unchecked_i32(roundf(values[j] * id));
             qs[block * 32 + j] = q;
             total += q;
         }
@@ -329,7 +337,7 @@ void tmo_add_bias(float* dst, const float* bias, int64_t rows, int32_t n) {
 
 /* round_away, quant.cr:309-313 */
 static inline int32_t round_away(float value) {
-    int32_t whole = (int32_t)value;
+    int32_t whole = unchecked_i32(value);
     float fraction = value - (float)whole;
     return whole + (fraction >= 0.5f ? 1 : 0) - (fraction <= -0.5f ? 1 : 0);
 }

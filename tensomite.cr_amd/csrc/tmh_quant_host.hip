@@ -10,6 +10,7 @@
 // finite f32 values.
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <thread>
 #include <vector>
@@ -43,18 +44,30 @@ void put_half(uint8_t* at, float v) {
     at[1] = (uint8_t)(h >> 8);
 }
 
-// A nibble: trunc(t) (t ≥ 0 for finite inputs), at most 15.
+// The reference converts with Crystal's unchecked Float32#to_i8! (LLVM
+// fptosi, which x86-64 carries out as cvttss2si): truncation toward zero,
+// and for NaN or a value outside Int32's range the "integer indefinite"
+// INT32_MIN, whose low byte -- what to_i8! keeps -- is 0. Written out, so
+// that the C++ conversion is defined for those inputs too.
+inline int32_t unchecked_i32(float v) {
+    return v >= -2147483648.0f && v < 2147483648.0f ? (int32_t)v : INT32_MIN;
+}
+
+// A nibble: trunc(t) (t in [0, 16.5] for finite inputs), at most 15.
 inline uint8_t nibble(float t) {
-    const int q = (int)t;
+    const int32_t q = unchecked_i32(t);
     return (uint8_t)(q > 15 ? 15 : q);
 }
 
 // round(:ties_away) of a value within int8's range, as an int8 byte.
-inline uint8_t round_away_byte(float v) { return (uint8_t)(int8_t)(int)std::round(v); }
+inline uint8_t round_away_byte(float v) { return (uint8_t)(int8_t)unchecked_i32(std::round(v)); }
 
 void block_q8_0(const float* x, uint8_t* out) {
-    float amax = 0.0f;
-    for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(x[j]));
+    // x.max_of(&.abs): the first value's magnitude, replaced by any larger
+    // one (a NaN first stays; a NaN later is never larger)
+    float amax = std::fabs(x[0]);
+    for (int j = 1; j < 32; ++j)
+        if (std::fabs(x[j]) > amax) amax = std::fabs(x[j]);
     const float d = amax / 127.0f;
     const float id = d == 0.0f ? 0.0f : 1.0f / d;
     put_half(out, d);

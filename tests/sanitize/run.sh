@@ -1,5 +1,5 @@
 #!/bin/bash
-# Host-side AddressSanitizer runs of the library's CPU code (no GPU needed):
+# Host-side AddressSanitizer and UndefinedBehaviorSanitizer runs of the library's CPU code (no GPU needed):
 # the GGUF reader on every fixture, each truncation of its first 64 KB and
 # 20000 random header mutations (gguf_fuzz), and the host weight quantiser
 # over every format, block counts 0-300 and larger, thread counts and special
@@ -9,19 +9,19 @@
 set -e
 R=$(cd "$(dirname "$0")/../.." && pwd)
 B=${TMPDIR:-/tmp}/tmh_sanitize; mkdir -p $B
-F="--offload-arch=gfx950 -O1 -g -std=c++17 -fPIC -ffp-contract=off -fno-gpu-rdc -Xclang -target-feature -Xclang -packed-fp32-ops -Xarch_host -fsanitize=address -Xarch_host -fno-omit-frame-pointer -I $R/include"
+F="--offload-arch=gfx950 -O1 -g -std=c++17 -fPIC -ffp-contract=off -fno-gpu-rdc -Xclang -target-feature -Xclang -packed-fp32-ops -Xarch_host -fsanitize=address,undefined -Xarch_host -fno-omit-frame-pointer -I $R/include"
 pids=""
 for f in tmh_runtime tmh_kernels tmh_decode tmh_llama tmh_gguf tmh_quant_host; do
   /opt/rocm/bin/hipcc $F -c $R/tensomite.cr_amd/csrc/$f.hip -o $B/$f.o > $B/$f.log 2>&1 &
   pids="$pids $!"
 done
 for d in gguf_fuzz quant_fuzz; do
-  /opt/rocm/bin/hipcc -O1 -g -std=c++17 -Xarch_host -fsanitize=address -I $R/include -c $R/tests/sanitize/$d.cpp -o $B/$d.drv
+  /opt/rocm/bin/hipcc -O1 -g -std=c++17 -Xarch_host -fsanitize=address,undefined -I $R/include -c $R/tests/sanitize/$d.cpp -o $B/$d.drv
 done
 for p in $pids; do wait $p; done
 LIB="$B/tmh_runtime.o $B/tmh_kernels.o $B/tmh_decode.o $B/tmh_llama.o $B/tmh_gguf.o $B/tmh_quant_host.o"
 for d in gguf_fuzz quant_fuzz; do
-  /opt/rocm/bin/hipcc --offload-arch=gfx950 -fno-gpu-rdc -Xarch_host -fsanitize=address $LIB $B/$d.drv -o $B/$d
+  /opt/rocm/bin/hipcc --offload-arch=gfx950 -fno-gpu-rdc -Xarch_host -fsanitize=address,undefined $LIB $B/$d.drv -o $B/$d
 done
 $B/gguf_fuzz $R/tests/golden/*/*.gguf
 $B/quant_fuzz

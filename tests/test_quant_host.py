@@ -48,6 +48,36 @@ def test_edge_values_equal_oracle(fmt):
     assert np.array_equal(quant_host.quantize(fmt, v), oracle.quantize(fmt, v))
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_nan_and_infinities_equal_oracle(fmt):
+    # A NaN or an infinity at each position of a block (and whole blocks of
+    # them): the host quantiser's bytes equal the oracle's. Q8_0's scale is
+    # x.max_of(&.abs) (quant.cr:499-500): the first value's magnitude,
+    # replaced only by a larger one, so a NaN first makes the scale NaN
+    # while a NaN later is skipped.
+    rng = np.random.default_rng(17)
+    blocks = []
+    for special in (np.nan, np.inf, -np.inf):
+        for pos in range(32):
+            b = rng.uniform(-1, 1, 32).astype(np.float32)
+            b[pos] = special
+            blocks.append(b)
+        blocks.append(np.full(32, special, np.float32))
+    v = np.concatenate(blocks)
+    assert np.array_equal(quant_host.quantize(fmt, v), oracle.quantize(fmt, v))
+
+
+def test_q8_0_nan_first_value():
+    # scale NaN/127 = NaN -> half 0x7E00 (f16.cr: NaN keeps its sign; |NaN|
+    # has none); every value NaN·(1/NaN) rounds to NaN, and to_i8! of NaN is
+    # 0 as x86-64 converts it (cvttss2si's integer indefinite, low byte 0)
+    b = np.linspace(-1, 1, 32).astype(np.float32)
+    b[0] = np.nan
+    want = np.array([0x00, 0x7E] + [0] * 32, np.uint8)
+    assert np.array_equal(oracle.quantize("Q8_0", b), want)
+    assert np.array_equal(quant_host.quantize("Q8_0", b), want)
+
+
 def test_f16_bits_match_oracle():
     rng = np.random.default_rng(9)
     words = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
