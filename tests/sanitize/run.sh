@@ -3,7 +3,9 @@
 # the GGUF reader on every fixture, each truncation of its first 64 KB and
 # 20000 random header mutations (gguf_fuzz), and the host weight quantiser
 # over every format, block counts 0-300 and larger, thread counts and special
-# values (quant_fuzz). The sanitizer instruments host code only (-Xarch_host);
+# values (quant_fuzz); and ThreadSanitizer over the oracle's spinning pool
+# (oracle_pool: 8-thread products and attention equal to 1-thread ones). The
+# library's sanitizers instrument host code only (-Xarch_host);
 # device code is built as usual. Usage, from the repository root:
 #   bash tests/sanitize/run.sh
 set -e
@@ -25,3 +27,6 @@ for d in gguf_fuzz quant_fuzz; do
 done
 $B/gguf_fuzz $R/tests/golden/*/*.gguf
 $B/quant_fuzz
+gcc -O1 -g -std=c11 -ffp-contract=off -fsanitize=thread -pthread -march=x86-64 \
+  $R/tests/sanitize/oracle_pool.c $R/oracle/tmq_oracle.c $R/oracle/tmq_llama.c -o $B/oracle_pool -lm
+$B/oracle_pool
