@@ -3,6 +3,10 @@ own model-level fixtures and invariants:
 
 * Maths.exp (maths.cr:36-54) within 2 ulp of the correctly rounded exp over
   its range, with the special values its spec states (spec/maths_spec.cr);
+  its range reduction and 2^n scaling bit for bit by an identity they
+  imply (exp(k·LN2_HI + y) == 2^k · exp(r)); the order of its last sums by
+  the rounding profile that order gives near zero. The polynomial's
+  coefficients are pinned by the bound only;
 * the tiny_llama quantised GGUFs against the F32 PyTorch logits of
   logits.json: Q8_0 strays less than a quarter of Q4_0's error
   (block_matmul_spec.cr:275-284), and both stay close;
@@ -46,6 +50,52 @@ def test_exp_within_two_ulp_and_special_values():
     s = oracle.exp_many(special)
     assert s[0] == 1 and s[1] == 1 and np.isinf(s[2]) and s[3] == 0 and np.isinf(s[4]) and s[5] == 0
     assert np.isnan(s[6])
+
+
+def test_exp_range_reduction_identity():
+    # Maths.exp (maths.cr:36-54) reduces x to r = (x - n·LN2_HI) - n·LN2_LO
+    # with n = round(x·log2 e), evaluates one polynomial at r and scales it
+    # by 2^⌊n/2⌋ · 2^(n - ⌊n/2⌋). For x = k·LN2_HI + y (LN2_HI = 355/512, so
+    # k·LN2_HI is exact for |k| <= 128, and y a multiple of 2^-17 keeps x
+    # exact) n is k, x - k·LN2_HI is y exactly, and the polynomial is taken at
+    # r = f32(y - f32(k·LN2_LO)) -- the r that exp(r) itself reduces to with
+    # n = 0. Powers of two scale exactly, so exp(x) == 2^k · exp(r) bit for
+    # bit. A one-constant reduction, a floor for the rounding, a dropped low
+    # part or a single 2^n (which overflows at k = 128) each break it; the
+    # polynomial itself is pinned only by the 2 ulp bound above.
+    LN2_HI, LN2_LO = np.float32(0.693359375), np.float32(-2.12194440e-4)
+    rng = np.random.default_rng(5)
+    ks, ys = [], []
+    for k in range(-125, 128):
+        for y in rng.integers(-13107, 13108, 40):  # |y| <= 0.1
+            ks.append(k), ys.append(np.float32(y) * np.float32(2.0 ** -17))
+    for y in rng.integers(-45875, -3932, 400):  # k = 128: x in [88.40, 88.72]
+        ks.append(128), ys.append(np.float32(y) * np.float32(2.0 ** -17))
+    k = np.array(ks, np.int64)
+    y = np.array(ys, np.float32)
+    x = (k.astype(np.float32) * LN2_HI + y).astype(np.float32)
+    assert np.all(x.astype(np.float64) == k * 0.693359375 + y.astype(np.float64))  # x exact
+    r = (y - (k.astype(np.float32) * LN2_LO).astype(np.float32)).astype(np.float32)
+    got = oracle.exp_many(x).astype(np.float64)
+    scaled = np.ldexp(oracle.exp_many(r).astype(np.float64), k)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got, scaled), np.flatnonzero(got != scaled)[:5]
+
+
+def test_exp_assembly_order_near_zero():
+    # For |x| <= 2^-8, n = 0 and Maths.exp returns f32(1 + f32(r + f32(p·r²)))
+    # (maths.cr:46-47): the inner sum is within 2^-24·|r| of r + p·r², so the
+    # one rounding at the end misses the correctly rounded exp only where
+    # exp(x) lies that close to a rounding boundary, a share of about |x| of
+    # the inputs (<= 0.4% here). Rounding 1 + r first and adding p·r² after
+    # (two roundings of comparable size) misrounds about a quarter of them.
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-2.0 ** -8, 2.0 ** -8, 1 << 18).astype(np.float32)
+    got = oracle.exp_many(x)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    d = ulp_distance(got, want)
+    assert d.max() <= 1
+    assert (d == 0).mean() >= 0.99, (d == 0).mean()
 
 
 def test_rmsnorm_swiglu_against_definitions():
