@@ -717,6 +717,11 @@ MATRIX_SHAPES = [
     # (rows, n, k): config 4 prefill, ragged edges, short k, the 1.7B MLP
     (512, 2048, 2048), (512, 8192, 2048), (33, 100, 576), (64, 64, 64), (100, 130, 1024), (128, 8192, 2048),
     (40, 2048, 8192),
+    # more tiles than compute units (several rounds of workgroups): a tile
+    # count that is a multiple of 8 (ids regrouped by XCD) with ragged rows
+    # and outputs and tiles of one stage (k = 256); a count that is not (516);
+    # an odd count
+    (250, 8300, 256), (100, 16500, 512), (520, 2100, 256),
 ]
 
 
@@ -790,12 +795,13 @@ def test_matrix_cores_with_bias_and_slice(dev, fmt):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-def test_unordered_matrix_close(dev, fmt):
+@pytest.mark.parametrize("rows,n,k", [(64, 192, 1024), (64, 16448, 1024)])
+def test_unordered_matrix_close(dev, fmt, rows, n, k):
     # UNORDERED from 32 rows runs the matrix-core kernel with each block's
     # contribution added by one fused multiply-add: the host's sums to within
-    # the rounding of 32 products and sums (k = 1024), not its bits.
-    rows, n, k = 64, 192, 1024
-    say("unordered matrix", fmt)
+    # the rounding of 32 products and sums (k = 1024), not its bits (257
+    # tiles: more than one round of workgroups).
+    say("unordered matrix", fmt, rows, n, k)
     wq = weights(fmt, n, k, 910)
     x = acts(rows, k, 911)
     want = oracle.matmul(fmt, x, wq, rows, n, k)
