@@ -19,6 +19,7 @@
 
 #include "../../include/tensomite_hip.h"
 #include "tmh_internal.h"
+#include "tmh_pool.h"
 
 namespace {
 std::atomic<int> g_fail_allocations{0};
@@ -82,116 +83,11 @@ static __device__ __align__(256) uint8_t scratch[TMH_FIXED_SCRATCH_BYTES];
 namespace {
 
 using tmh::device_malloc;
+using tmh::Pool;
+using tmh::Retired;
 using tmh::scratch_need;
 
 constexpr int MAX_DEVICES = 16;
-
-// Exact-size pool of freed device memory, as BufferPool (buffer_pool.cr:12-74):
-// `take` and `give` never wait -- while another caller holds the lock, take
-// returns nothing and give returns false, and the caller allocates or frees
-// instead.
-class Pool {
-  public:
-    int64_t limit = 1ll << 30;
-    int64_t held = 0;
-    std::atomic<int64_t> hits{0}, misses{0};
-
-    uint64_t take(uint64_t bytes) {
-        uint64_t ptr = 0;
-        if (lock()) {
-            auto it = free_.find(bytes);
-            if (it != free_.end() && !it->second.empty()) {
-                ptr = it->second.back();
-                it->second.pop_back();
-                held -= (int64_t)bytes;
-            }
-            unlock();
-        }
-        (ptr ? hits : misses).fetch_add(1);
-        return ptr;
-    }
-
-    bool give(uint64_t ptr, uint64_t bytes) {
-        if (bytes == 0 || !lock()) return false;
-        bool kept = false;
-        if (held + (int64_t)bytes <= limit) {
-            free_[bytes].push_back(ptr);
-            held += (int64_t)bytes;
-            kept = true;
-        }
-        unlock();
-        return kept;
-    }
-
-    // Frees everything held (at process teardown or on request).
-    template <typename F>
-    void drain_all(F&& free_fn) {
-        while (!lock()) std::this_thread::yield();
-        for (auto& [bytes, list] : free_)
-            for (uint64_t p : list) free_fn(p, bytes);
-        free_.clear();
-        held = 0;
-        unlock();
-    }
-
-  private:
-    std::unordered_map<uint64_t, std::vector<uint64_t>> free_;
-    std::atomic<bool> lock_{false};
-    bool lock() {
-        bool expected = false;
-        return lock_.compare_exchange_strong(expected, true);
-    }
-    void unlock() { lock_.store(false); }
-};
-
-// Memory given back from any thread, waiting to move into the pool, as
-// RetiredList (buffer_pool.cr:87-129): `push` never allocates and never
-// waits; it stores into one of two fixed arrays and returns false when busy
-// or full. `drain` swaps the arrays, on the device's own calls only.
-class Retired {
-  public:
-    static constexpr int CAPACITY = 16384;
-    struct Entry {
-        uint64_t ptr, bytes;
-    };
-
-    bool push(uint64_t ptr, uint64_t bytes) {
-        bool expected = false;
-        if (!lock_.compare_exchange_strong(expected, true)) return false;
-        bool kept = false;
-        if (count_ < CAPACITY) {
-            filling_[count_++] = Entry{ptr, bytes};
-            kept = true;
-        }
-        lock_.store(false);
-        return kept;
-    }
-
-    template <typename F>
-    void drain(F&& each) {
-        if (count_ == 0) return;
-        bool expected = false;
-        while (!lock_.compare_exchange_strong(expected, true)) {
-            expected = false;
-            std::this_thread::yield();
-        }
-        Entry* full = filling_;
-        int count = count_;
-        filling_ = draining_;
-        draining_ = full;
-        count_ = 0;
-        lock_.store(false);
-        for (int i = 0; i < count; ++i) each(full[i].ptr, full[i].bytes);
-    }
-
-  private:
-    Entry a_[CAPACITY];
-    Entry b_[CAPACITY];
-    Entry* filling_ = a_;
-    Entry* draining_ = b_;
-    int count_ = 0;
-    std::atomic<bool> lock_{false};
-};
 
 // Pinned host memory for asynchronous uploads: SLOTS buffers of SLOT_BYTES,
 // used round robin; a slot is reused once the copy out of it has finished.
@@ -207,7 +103,9 @@ struct Staging {
 
 struct Device {
     std::mutex setup;
-    bool ready = false;
+    // Set (release) once the fields below are; read (acquire) before use by
+    // any thread.
+    std::atomic<bool> ready{false};
     int index = 0;
     hipStream_t stream = nullptr;
     int compute_units = 256;

@@ -4,7 +4,9 @@
 # 20000 random header mutations (gguf_fuzz), and the host weight quantiser
 # over every format, block counts 0-300 and larger, thread counts and special
 # values (quant_fuzz); and ThreadSanitizer over the oracle's spinning pool
-# (oracle_pool: 8-thread products and attention equal to 1-thread ones). The
+# (oracle_pool: 8-thread products and attention equal to 1-thread ones) and
+# over the library's retired list and device-memory pool (pool_race: pushes
+# and concurrent drains, every pointer back exactly once). The
 # library's sanitizers instrument host code only (-Xarch_host);
 # device code is built as usual. Usage, from the repository root:
 #   bash tests/sanitize/run.sh
@@ -30,3 +32,5 @@ $B/quant_fuzz
 gcc -O1 -g -std=c11 -ffp-contract=off -fsanitize=thread -pthread -march=x86-64 \
   $R/tests/sanitize/oracle_pool.c $R/oracle/tmq_oracle.c $R/oracle/tmq_llama.c -o $B/oracle_pool -lm
 $B/oracle_pool
+g++ -O1 -g -std=c++17 -fsanitize=thread -pthread $R/tests/sanitize/pool_race.cpp -o $B/pool_race
+$B/pool_race 50000
