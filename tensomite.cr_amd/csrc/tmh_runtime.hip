@@ -115,6 +115,7 @@ struct Device {
     int32_t* errors = nullptr;
     std::atomic<bool> errors_pending{false};
     int32_t report[3] = {0, 0, 0};
+    std::mutex report_lock;  // report is written by tmh_sync, read by tmh_error_report, on any threads
 
     // Scratch for quantised activations, kept and grown across launches
     // (cuda.cr:788-798); `launch` keeps a quantise pass and its product
@@ -503,7 +504,10 @@ int tmh_sync(void) {
         e = hipMemcpy(got, d->errors, sizeof(got), hipMemcpyDeviceToHost);
         if (e != hipSuccess) return code(e);
         if (got[0] != 0) {
-            std::memcpy(d->report, got, sizeof(got));
+            {
+                std::lock_guard<std::mutex> guard(d->report_lock);
+                std::memcpy(d->report, got, sizeof(got));
+            }
             e = hipMemset(d->errors, 0, sizeof(got));
             if (e != hipSuccess) return code(e);
             return TMH_ERROR_EXECUTION;
@@ -556,6 +560,7 @@ int tmh_error_report(int32_t out[3]) {
     int err;
     Device* d = current(&err);
     if (!d) return err;
+    std::lock_guard<std::mutex> guard(d->report_lock);
     std::memcpy(out, d->report, sizeof(d->report));
     std::memset(d->report, 0, sizeof(d->report));
     return TMH_SUCCESS;
