@@ -640,9 +640,18 @@ def test_stream_plan_input_modes(dev, fmt, wgs, ring, rows, monkeypatch):
     # 8192 is past the staging budget, so every product is prepared from
     # global memory); the bits of the oracle's RMSNorm then product, or of
     # the product of x.
-    if rows == "long" and fmt == "Q8_0":
-        pytest.skip("Q8_0 rows of 8192 values are longer than a step of the streamed kernel")
     monkeypatch.setenv("TMH_PLAN_KERNEL", "stream")
+    if rows == "long" and fmt == "Q8_0":
+        # A Q8_0 row of 8192 values (8704 bytes) is longer than a step of
+        # the streamed kernel, and the tiled kernel takes f32 x only: a plan
+        # with such a product in another input mode is refused.
+        wq = weights(fmt, 16, 8192, 3000)
+        x = acts(1, 8192, 4000)
+        for mode in (1, 2):
+            xbuf, xin, _ = plan_input(dev, mode, x, 8192, 5000)
+            with pytest.raises(th.ShapeError):
+                dev.plan(fmt, [(dev.from_array(wq), 0, xbuf, dev.alloc(64), None, 16, 8192, xin)])
+        return
     monkeypatch.setenv("TMH_STREAM_WGS", wgs)
     monkeypatch.setenv("TMH_STREAM_RING", ring)
     rng = np.random.default_rng(950)
