@@ -74,6 +74,10 @@ struct Llama {
     bool generating = false;       // the device state continues a generation
 
     hipGraphExec_t graph = nullptr;
+    // The step graph is captured on this stream of the model's own, so that
+    // no other call (another thread's product on the device's stream) can
+    // enqueue into the capture; the graph then runs on the device's stream.
+    hipStream_t capture = nullptr;
     void* owned = nullptr;  // weights this decoder loaded itself (tmh_llama_load_gguf)
     uint32_t mode = TMH_MODE_AUTO;  // the products' BlockMatMulMode: AUTO, or UNORDERED (tmh_llama_set_mode)
 };
@@ -289,11 +293,20 @@ hipError_t decode_step(const Llama& m, const DeviceContext& ctx) {
 int run_step(Llama& m, const DeviceContext& ctx, bool graph) {
     if (!graph) return code(decode_step(m, ctx));
     if (!m.graph) {
+        if (!m.capture) {
+            hipError_t e = hipStreamCreateWithFlags(&m.capture, hipStreamNonBlocking);
+            if (e != hipSuccess) {
+                m.capture = nullptr;
+                return code(e);
+            }
+        }
+        DeviceContext cap = ctx;
+        cap.stream = m.capture;
         hipGraph_t g = nullptr;
-        hipError_t e = hipStreamBeginCapture(ctx.stream, hipStreamCaptureModeThreadLocal);
+        hipError_t e = hipStreamBeginCapture(cap.stream, hipStreamCaptureModeThreadLocal);
         if (e != hipSuccess) return code(e);
-        hipError_t step = decode_step(m, ctx);
-        e = hipStreamEndCapture(ctx.stream, &g);
+        hipError_t step = decode_step(m, cap);
+        e = hipStreamEndCapture(cap.stream, &g);
         if (step != hipSuccess) {
             if (g) (void)hipGraphDestroy(g);
             return code(step);
@@ -712,6 +725,7 @@ int tmh_llama_destroy(uint64_t model) {
     Llama* m = (Llama*)model;
     if (tmh::device_context(&ctx, false) == TMH_SUCCESS) (void)hipStreamSynchronize(ctx.stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    if (m->capture) (void)hipStreamDestroy(m->capture);
     if (m->memory) (void)hipFree(m->memory);
     if (m->owned) (void)hipFree(m->owned);
     delete m;

@@ -7,7 +7,8 @@ drains the retired list into the pool, in a loop. Every product bit for bit
 against the oracle's Quant.matmul (quant.cr:155-182). The library serialises
 launches on its one stream; buffers one thread gives back are taken again by
 the others through the pool (CUDA#alloc / #retire / #sync, cuda.cr:339-353,
-439-454).
+439-454). And a decoder capturing its step graph while another thread's
+products run on the same device: neither's work lands in the other's.
 """
 import queue
 import sys
@@ -16,6 +17,7 @@ import threading
 import numpy as np
 import pytest
 
+from llama_fixtures import random_llama
 from oracle import oracle
 import tensomite_hip as th
 
@@ -82,3 +84,58 @@ def test_threads_share_one_device():
     after = dev.counters()
     assert not failures, failures[:5]
     assert after["pool_hits"] > before["pool_hits"]  # memory given back by one thread taken by another call
+
+
+def test_products_beside_a_decoder_capturing_its_step():
+    # The decoder captures its step graph on a stream of the model's own, so
+    # another thread's products on the device's stream meanwhile run at once
+    # and are not recorded into the graph: every product and every decoded
+    # token the CPU's (llama.cr:256-303, generative.cr:155-190).
+    dev = th.HIPDevice(0)
+    config = dict(layers=2, width=256, heads=4, kv_heads=2, head_width=64, hidden=512, vocab=300, context=128,
+                  eps=1e-5, theta=10000.0, kind="Q4_0")
+    weights = random_llama(config, seed=1400, norm_jitter=0.1)
+    prompt = [int(v) for v in np.random.default_rng(1401).integers(0, 300, 20)]
+    steps = 12
+    want_tokens = oracle.Llama(config, weights).generate(prompt, steps)
+    rng = np.random.default_rng(1402)
+    fmt, rows, n, k = "Q4_1", 3, 320, 512
+    wq = oracle.quantize(fmt, rng.standard_normal(n * k, dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(rows * k, dtype=np.float32)
+    want = oracle.matmul(fmt, x, wq, rows, n, k)
+    stop = threading.Event()
+    failures, done = [], [0]
+
+    def products():
+        try:
+            while not stop.is_set():
+                wbuf, xbuf = dev.from_array(wq), dev.from_array(x)
+                out = dev.block_matmul(fmt, wbuf, xbuf, rows, n, k)
+                got = dev.to_array(out, np.float32, rows * n).reshape(rows, n)
+                if not np.array_equal(bits(got), bits(want)):
+                    failures.append(("product", done[0]))
+                for b in (wbuf, xbuf, out):
+                    b.release()
+                done[0] += 1
+        except Exception as e:
+            failures.append(("product raised", repr(e)))
+
+    say("decoder captures beside products")
+    worker = threading.Thread(target=products)
+    worker.start()
+    try:
+        for i in range(6):
+            model = th.HIPLlama(dev, config, weights, rows=1, capacity=64, max_tokens=32)
+            model.forward(prompt, row=0, last_only=True)
+            tokens = model.generate(steps, graph=True)[0]  # the first step captures the graph
+            if list(tokens) != want_tokens:
+                failures.append(("tokens", i, list(tokens)))
+            model.destroy()
+    finally:
+        stop.set()
+        worker.join(timeout=120)
+    dev.sync()
+    assert not worker.is_alive()
+    assert not failures, failures[:5]
+    assert done[0] > 0
+
