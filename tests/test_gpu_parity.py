@@ -350,6 +350,32 @@ def test_few_rows_nan_and_inf_blocks(dev, fmt):
         assert same_or_both_nan(got, want[:rows]), rows
 
 
+def test_empty_calls_succeed_and_write_nothing(dev):
+    # Empty work through the C ABI, as tensomite's empty tensors reach it:
+    # products of no rows or no outputs (every mode, and the allocation-free
+    # entry point), a quantise pass of no rows, a gather of no ids and a plan
+    # of no products all return success, launch nothing, and leave the
+    # output as it was; with nothing to do, null buffers are accepted too.
+    wq = weights("Q4_0", 8, 64, 1)
+    wbuf, xbuf = dev.from_array(wq), dev.from_array(acts(1, 64, 2))
+    sentinel = np.full(16, 7.0, np.float32)
+    out = dev.from_array(sentinel)
+    say("empty calls")
+    for entry in ("tmh_block_matmul", "tmh_block_matmul_fixed"):
+        fn = getattr(dev.lib, entry)
+        for rows, n in ((0, 8), (1, 0), (0, 0)):
+            for mode in range(8):
+                th.check(entry, fn(th.Q4_0, wbuf.pointer, 0, xbuf.pointer, 64, out.pointer, 0, rows, n, 64, mode))
+        th.check(entry, fn(th.Q4_0, 0, 0, 0, 64, 0, 0, 0, 8, 64, 0))
+    th.check("tmh_quantize_rows_q8", dev.lib.tmh_quantize_rows_q8(xbuf.pointer, 0, 64, 64, 0, 0, 0, 0))
+    th.check("tmh_gather_blocks", dev.lib.tmh_gather_blocks(th.Q4_0, wbuf.pointer, 0, 8, 64, 0, 0, out.pointer))
+    plan = dev.plan("Q4_0", [])
+    plan.run()
+    plan.destroy()
+    dev.sync()
+    assert np.array_equal(dev.to_array(out, np.float32, 16), sentinel)
+
+
 @pytest.mark.parametrize("rows", [1, 2, 5, 8, 16, 40])
 def test_zero_rows_fold_from_plus_zero(dev, rows):
     # Q4_0 with negative block scales and all-zero activation rows: every
