@@ -439,7 +439,8 @@ typedef struct tmh_llama_weights {
 } tmh_llama_weights;
 
 /* Makes a decoder for `rows` sequences of at most `capacity` positions
- * (≤ context), running at most `max_tokens` tokens per forward. Allocates its
+ * (≤ context), its buffers sized for `max_tokens` tokens a forward (a longer
+ * forward runs as forwards of `max_tokens` in turn, with the same bits). Allocates its
  * caches, activations and rotation tables (RotaryEmbedding's, in F32 by
  * powf/cosf/sinf). */
 int tmh_llama_create(const tmh_llama_config* config, const tmh_llama_weights* weights, uint32_t rows,

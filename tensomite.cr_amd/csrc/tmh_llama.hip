@@ -566,11 +566,27 @@ int tmh_llama_forward(uint64_t model, uint32_t row, const int32_t* ids, uint32_t
     Llama* m = model_of(model, ctx, &err);
     if (!m) return err;
     if (row >= m->rows || !ids) return TMH_ERROR_INVALID_VALUE;
-    if (count == 0 || count > m->max_tokens) return TMH_ERROR_SHAPE;
+    if (count == 0) return TMH_ERROR_SHAPE;
     const int32_t past = m->length[row];
     if ((uint64_t)past + count > m->capacity) return TMH_ERROR_SHAPE;
     for (uint32_t i = 0; i < count; ++i)
         if (ids[i] < 0 || ids[i] >= m->c.vocab) return TMH_ERROR_INVALID_VALUE;
+    if (count > m->max_tokens) {
+        // More ids than one forward's buffers hold: forwards of max_tokens
+        // ids in turn, each after the positions the ones before it cached.
+        // Every position reads the cache by position, so its bits are those
+        // of one forward over all the ids (as prefill equals one-by-one
+        // decode); the logits of each part land at its offset, or with
+        // last_only only the last id's.
+        const size_t vocab = (size_t)m->c.vocab;
+        for (uint32_t off = 0; off < count; off += m->max_tokens) {
+            const uint32_t part = std::min(m->max_tokens, count - off);
+            const bool last = off + part == count;
+            float* out = !logits ? nullptr : last_only ? (last ? logits : nullptr) : logits + (size_t)off * vocab;
+            if ((err = tmh_llama_forward(model, row, ids + off, part, last_only, out)) != TMH_SUCCESS) return err;
+        }
+        return TMH_SUCCESS;
+    }
     // ids, slots, then the attention table, in one upload
     std::vector<int32_t> host((size_t)count * 5);
     for (uint32_t i = 0; i < count; ++i) {

@@ -289,6 +289,26 @@ def test_small_llama_generate_matches_cpu(dev, kind):
     assert gpu.length() == len(prompt) + 29
 
 
+@pytest.mark.parametrize("kind", ["Q8_0", "Q4_1"])
+def test_forward_longer_than_max_tokens(dev, kind):
+    # A forward of more ids than the decoder's buffers hold (max_tokens 8,
+    # 29 ids) runs as forwards of 8 in turn: every position's logits, and
+    # with last_only the last one's, are the CPU's bits for one forward over
+    # all 29 (llama.cr:256-303); generation then continues from it.
+    say("long forward", kind)
+    config = small_config(kind)
+    weights = random_llama(config, seed=31, norm_jitter=0.1)
+    cpu = oracle.Llama(config, weights)
+    prompt = [int(v) for v in np.random.default_rng(32).integers(0, 512, 29)]
+    want = cpu.forward(prompt)
+    gpu = th.HIPLlama(dev, config, weights, max_tokens=8)
+    assert np.array_equal(bits(gpu.forward(prompt)), bits(want))
+    assert gpu.length() == 29
+    gpu.reset()
+    assert np.array_equal(bits(gpu.forward(prompt, last_only=True)), bits(want[-1:]))
+    assert list(gpu.generate(10, graph=True)[0]) == oracle.Llama(config, weights).generate(prompt, 10)
+
+
 @pytest.mark.parametrize("kind,rows", [("Q8_0", 1), ("Q4_0", 1), ("Q4_1", 3)])
 def test_decoder_nan_at_a_lane_start(dev, kind, rows):
     # The decoder's fused quantisers (RMSNorm+quantise before qkv, gate_up
@@ -411,9 +431,12 @@ def test_decoder_limits(dev):
     weights = random_llama(config, seed=25)
     gpu = th.HIPLlama(dev, config, weights, capacity=20, max_tokens=8)
     with pytest.raises(th.ShapeError):
-        gpu.forward(list(range(9)))          # more than max_tokens
+        gpu.forward(list(range(21)))         # more positions than the cache holds
     with pytest.raises(th.DeviceError):
         gpu.forward([config["vocab"]])        # an id out of range
+    with pytest.raises(th.DeviceError):
+        gpu.forward(list(range(12)) + [-1])  # one bad id in the second part of a long forward
+    assert gpu.length() == 0                  # refused before any part ran
     gpu.forward(list(range(8)), last_only=True)
     with pytest.raises(th.ShapeError):
         gpu.generate(14)                      # 8 + 13 positions > 20
